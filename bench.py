@@ -1,0 +1,262 @@
+"""Benchmark of the MI355X MXFP4 hot path (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--suite PATH]
+
+Workload (BASELINE cfg4, the config the headline metric is quoted on):
+A, B fp32 [8192, 8192] = 0.05 * Student-t(3), resident in HBM.  One step =
+quantize A along K (fused quantize+pack, E8M0 scales) + quantize B along K +
+f4 x f4 block-scaled GEMM (v_mfma_scale_f32_32x32x64_f8f6f4), bf16 out.
+
+`value` is the whole step's rate, 2*M*N*K / step time.  `gemm` and `quantize`
+give per-kernel rates from HIP events recorded on the stream the kernels run
+on, and `roofline` prices the dominant kernel (the GEMM) against MI355X's
+dense FP4 MFMA peak; `roofline_quantize` prices the quantizer against HBM.
+`cpu_baseline` times the CPU oracle (a restatement of the reference's CPU
+path: fp4.py quantizer + dequantize-then-fp32-matmul, the fake-quant branch
+of fp4_linear.py:40) on this host, on rank 0 only.
+
+--suite PATH also measures the other BASELINE configs (dual-batch cfg2, the
+weight-only cfg3 sweep) and writes one JSON line each to PATH.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP4_TFLOPS = 10100.0     # MI355X dense MXFP4 MFMA
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--size", type=int, default=8192)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--suite", default=None, help="also bench cfg2/cfg3, one JSON line each to this file")
+    return p.parse_args()
+
+
+def median(xs):
+    s = sorted(xs)
+    return s[len(s) // 2] if s else float("nan")
+
+
+def t3(n, gen, dev, torch):
+    z = torch.randn((n, n), device=dev, generator=gen)
+    chi = torch.zeros_like(z)
+    for _ in range(3):
+        chi += torch.randn((n, n), device=dev, generator=gen).square()
+    return (z / torch.sqrt(chi / 3.0) * 0.05).contiguous()
+
+
+def traffic_from_profiles(kernel_prefix: str):
+    """HBM bytes per launch from committed rocprofv3 --pmc summaries, if any."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        data = json.loads(f.read_text())
+        return data.get(kernel_prefix, {}).get("bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def cpu_baseline(n: int):
+    """Time the CPU oracle on the cfg4 workload: quantize A and B (C oracle,
+    OpenMP), dequantize, fp32 A @ B^T (numpy/OpenBLAS) -- the fake-quant CPU
+    path of fp4_linear.py:40 restated.  Rate = 2*R*n*n / time for R rows of C
+    (R = n unless that would exceed ~30 s)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import oracle as O
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    O.lib()
+    rng = np.random.default_rng(4001)
+    R = n
+    a = (rng.standard_t(3, (R, n)) * 0.05).astype(np.float32)
+    b = (rng.standard_t(3, (n, n)) * 0.05).astype(np.float32)
+    with threadpool_limits(limits=cores):
+        times = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            ac, as_ = O.quantize_mxfp4(a)
+            bc, bs_ = O.quantize_mxfp4(b)
+            A = O.dequantize_mxfp4(ac, as_)
+            B = O.dequantize_mxfp4(bc, bs_)
+            C = A @ B.T
+            times.append(time.perf_counter() - t0)
+            del C, A, B
+    t = min(times)
+    return {"value": round(2.0 * R * n * n / t / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"full cfg4 ({R}x{n}x{n}): quantize A and B with the C oracle (OpenMP, "
+                      f"{O.num_threads()} threads), dequantize, fp32 A@B^T (numpy/OpenBLAS, {cores} threads); "
+                      f"{t:.2f} s per step, best of 2",
+            "seconds": round(t, 3)}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "this build has no multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from lockstep_amd import fp4, mxfp4_gemm
+    from lockstep_amd import _capi
+
+    _capi.load()
+    dev = torch.device("cuda", 0)
+    props = torch.cuda.get_device_properties(0)
+    n = args.size
+    g = torch.Generator(device=dev).manual_seed(4001)
+    A = t3(n, g, dev, torch)
+    B = t3(n, g, dev, torch)
+    torch.cuda.synchronize()
+
+    def step(ev=None):
+        if ev:
+            ev[0].record()
+        apk, ae8 = fp4.quantize_pack_mxfp4(A)
+        if ev:
+            ev[1].record()
+        bpk, be8 = fp4.quantize_pack_mxfp4(B)
+        if ev:
+            ev[2].record()
+        c = mxfp4_gemm.mxfp4_gemm_packed(apk, bpk, ae8, be8, out_dtype=torch.bfloat16)
+        if ev:
+            ev[3].record()
+        return c
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` steps, synchronized on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    # per-kernel durations from HIP events on the kernels' stream
+    qa, qb, gm = [], [], []
+    for _ in range(max(args.steps, 5)):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        step(ev)
+        torch.cuda.synchronize()
+        qa.append(ev[0].elapsed_time(ev[1]))
+        qb.append(ev[1].elapsed_time(ev[2]))
+        gm.append(ev[2].elapsed_time(ev[3]))
+    gemm_ms = median(gm)
+    quant_ms = median(qa + qb)
+
+    flop = 2.0 * n * n * n
+    gemm_tflops = flop / (gemm_ms * 1e-3) / 1e12
+    q_bytes = n * n * (4 + 0.5 + 1.0 / 32)            # fp32 in, packed nibbles + E8M0 out
+    quant_gbs = q_bytes / (quant_ms * 1e-3) / 1e9
+    value = flop / (ms_per_step * 1e-3) / 1e12
+
+    out = {
+        "metric": f"MXFP4 GEMM TFLOPS at {n}^3 (cfg4: on-the-fly quantize of A and B + f4xf4 GEMM)",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4 (e2m1 x e2m1, e8m0 scales, fp32 accumulate, bf16 out)",
+        "data": "synthetic: A, B = 0.05 * Student-t(df=3), torch.Generator(seed 4001) on device, fp32",
+        "config": {"workload": "cfg4 fully-FP4 GEMM", "M": n, "N": n, "K": n, "input_dtype": "f32",
+                   "out_dtype": "bf16", "block": 32, "parallelism": "single GPU"},
+        "device": props.name,
+        "gemm": {"ms": round(gemm_ms, 4), "tflops": round(gemm_tflops, 1),
+                 "frac_fp4_peak": round(gemm_tflops / PEAK_FP4_TFLOPS, 4)},
+        "quantize": {"ms_per_operand": round(quant_ms, 4), "gbs": round(quant_gbs, 1),
+                     "frac_hbm": round(quant_gbs / PEAK_HBM_GBS, 4),
+                     "bytes_per_launch": int(q_bytes)},
+        "roofline": {"bound": "mfma", "kernel": "gemm_f4f4_kernel", "achieved": round(gemm_tflops, 1),
+                     "peak": PEAK_FP4_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tflops / PEAK_FP4_TFLOPS, 4),
+                     "traffic": traffic_from_profiles("gemm_f4f4_kernel")},
+        "roofline_quantize": {"bound": "hbm", "kernel": "quantize_rows_kernel", "achieved": round(quant_gbs, 1),
+                              "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(quant_gbs / PEAK_HBM_GBS, 4),
+                              "traffic": traffic_from_profiles("quantize_rows_kernel")},
+    }
+    if args.suite:
+        run_suite(args.suite, torch, dev)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(n)
+    print(json.dumps(out), flush=True)
+
+
+def _time_events(fn, reps=20, warm=3):
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return median(ts)
+
+
+def run_suite(path, torch, dev):
+    """cfg2 (dual-batch) and cfg3 (weight-only sweep), one JSON line each."""
+    from lockstep_amd import dual_gemm, fp4, mxfp4_gemm
+    lines = []
+    g = torch.Generator(device=dev).manual_seed(2001)
+    # cfg2: A0, A1 bf16 [2048, 4096], W [4096, 4096] MXFP4
+    a0 = torch.randn((2048, 4096), device=dev, generator=g).to(torch.bfloat16)
+    a1 = torch.randn((2048, 4096), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((4096, 4096), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    ms = _time_events(lambda: dual_gemm.dual_mxfp4(a0, a1, wpk, we8))
+    fl = 2.0 * 2 * 2048 * 4096 * 4096
+    lines.append({"config": "cfg2 dual-batch bf16 x mxfp4, 2x[2048,4096] . [4096,4096]^T", "ms": ms,
+                  "tflops": fl / ms / 1e9, "frac_bf16_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS})
+    ms2 = _time_events(lambda: (mxfp4_gemm.mxfp4_gemm_bf16(a0, wpk, we8), mxfp4_gemm.mxfp4_gemm_bf16(a1, wpk, we8)))
+    lines[-1]["two_launch_ms"] = ms2
+    # cfg3: W [14336, 4096], M sweep
+    w3 = torch.randn((14336, 4096), device=dev, generator=g) * 0.02
+    w3pk, w3e8 = fp4.quantize_pack_mxfp4(w3)
+    for M in (1, 16, 128, 1024, 8192):
+        a = torch.randn((M, 4096), device=dev, generator=g).to(torch.bfloat16)
+        ms = _time_events(lambda: mxfp4_gemm.mxfp4_gemm_bf16(a, w3pk, w3e8))
+        fl = 2.0 * M * 14336 * 4096
+        by = 14336 * 4096 * (0.5 + 1 / 32) + 2 * M * 4096 + 2 * M * 14336
+        lines.append({"config": f"cfg3 weight-only bf16 x mxfp4, M={M}, N=14336, K=4096", "ms": ms,
+                      "tflops": fl / ms / 1e9, "gbs": by / ms / 1e6,
+                      "frac_bf16_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS, "frac_hbm": by / ms / 1e6 / PEAK_HBM_GBS})
+    with open(path, "w") as f:
+        for ln in lines:
+            f.write(json.dumps(ln) + "\n")
+            print(json.dumps(ln), file=sys.stderr, flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * lsmx.h -- C ABI of the MI355X (gfx950) MXFP4 library, liblsmx.so.
+ *
+ * MXFP4 = E2M1 4-bit elements with one E8M0 (power-of-two) scale per 32
+ * consecutive elements along the contraction axis K; two elements per byte,
+ * the even-indexed element in the low nibble.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers; sizes, leading dimensions (ld*) and
+ *     offsets are in ELEMENTS of the pointed-to type (bytes for packed codes
+ *     and E8M0 scales).  Row-major, unit stride along the last axis.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Every call is
+ *     asynchronous and stream-ordered; none synchronizes the device.
+ *   - The library never allocates device memory.
+ *   - Return value: LSMX_OK (0) or a negative LSMX_ERR_* code; the message
+ *     for the calling thread is in lsmx_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the lockstep checkout):
+ * each declaration cites the Python/Triton/CUDA function whose semantics it
+ * implements.
+ */
+#ifndef LSMX_H
+#define LSMX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define LSMX_OK 0
+#define LSMX_ERR_SHAPE -1   /* a size or block that the reference asserts against */
+#define LSMX_ERR_ALIGN -2   /* pointer or leading dimension misaligned            */
+#define LSMX_ERR_DTYPE -3   /* unsupported element type or format                 */
+#define LSMX_ERR_DEVICE -4  /* no device, or the current device is not gfx950     */
+#define LSMX_ERR_LAUNCH -5  /* the HIP runtime rejected a kernel launch           */
+#define LSMX_ERR_ARG -6     /* null pointer or otherwise invalid argument         */
+
+/* element types */
+#define LSMX_F32 0
+#define LSMX_BF16 1
+#define LSMX_F16 2
+
+/* code formats */
+#define LSMX_CODES_PACKED 0    /* [rows, K/2] bytes, even element in the low nibble */
+#define LSMX_CODES_UNPACKED 1  /* [rows, K] bytes, one code (0..15) per byte         */
+
+/* scale formats */
+#define LSMX_SCALE_E8M0 0  /* one byte per block: biased exponent, 0xFF = NaN        */
+#define LSMX_SCALE_F32 1   /* one fp32 per block holding the power of two (fp4.py)   */
+
+/* Library version string, e.g. "lsmx 0.1.0 gfx950". */
+const char *lsmx_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *lsmx_last_error(void);
+
+/* LSMX_OK if the current HIP device is a gfx950 (MI355X class) GPU.
+ * Replaces the device guard of h100.py:8-15 / fp4_linear.py:19. */
+int lsmx_device_check(void);
+
+/* MXFP4 quantization of x[rows, K] along K.
+ * Replaces fp4.py:57-72 quantize_mxfp4 (codes + fp32 scale, UNPACKED) and,
+ * with LSMX_CODES_PACKED, the fused quantize_mxfp4 + pack_fp4 of
+ * fp4_linear.py:36-39 / fp4.py:91-94.
+ *   x_dtype   LSMX_F32 | LSMX_BF16 | LSMX_F16; ldx >= K (elements).
+ *   block     32 or 16 (K % block == 0, as fp4.py:65 asserts).
+ *   codes     [rows, ld_codes] bytes; ld_codes >= K/2 (PACKED) or K (UNPACKED).
+ *   scale     [rows, ld_scale] E8M0 bytes or fp32; ld_scale >= K/block.
+ * Scale exponent: floor(RN_f32(log2(max(amax, 1e-30)))) - 2, clamped to
+ * [-127, 127]; 1.0 for an all-zero block; NaN (0xFF) for a block with a NaN.
+ * Rounding: to nearest with ties toward the smaller magnitude, clip at 6,
+ * sign copied from the input (-0 -> code 8), exactly as fp4.py:43-54. */
+int lsmx_quantize_mxfp4(const void *x, int x_dtype, int64_t rows, int64_t K, int64_t ldx,
+                        int block, void *codes, int codes_fmt, int64_t ld_codes, void *scale,
+                        int scale_fmt, int64_t ld_scale, void *stream);
+
+/* The same quantizer along the OTHER axis: x[K, cols] (ldx >= cols) is
+ * quantized in blocks of `block` consecutive ROWS, and the outputs are laid
+ * out for x^T: codes [cols, ld_codes], scale [cols, ld_scale].
+ * Equivalent to fp4.py:57-72 applied to x.t().contiguous() (the requantization
+ * of a transposed operand, as bench.py:161 does for B). */
+int lsmx_quantize_mxfp4_t(const void *x, int x_dtype, int64_t K, int64_t cols, int64_t ldx,
+                          int block, void *codes, int codes_fmt, int64_t ld_codes, void *scale,
+                          int scale_fmt, int64_t ld_scale, void *stream);
+
+/* fp4.py:43-54 _round_to_e2m1: codes[i] = E2M1 code of q[i] (scale 1):
+ * nearest, ties toward the smaller magnitude, clip at 6, sign copied, NaN -> 7.
+ * q_dtype LSMX_F32 | LSMX_BF16 | LSMX_F16; n elements, one code byte each. */
+int lsmx_round_e2m1(const void *q, int q_dtype, int64_t n, uint8_t *codes, void *stream);
+
+/* fp4.py:91-94 pack_fp4: n_bytes output bytes from 2*n_bytes codes. */
+int lsmx_pack_fp4(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, void *stream);
+
+/* fp4.py:97-99 unpack_fp4: 2*n_bytes codes from n_bytes packed bytes. */
+int lsmx_unpack_fp4(const uint8_t *packed, uint8_t *codes, int64_t n_bytes, void *stream);
+
+/* fp4.py:75-78 dequantize_mxfp4: out[r, k] = value(code[r, k]) * scale[r, k/block],
+ * out_dtype LSMX_F32 | LSMX_BF16 (exact in both: the scale is a power of two). */
+int lsmx_dequantize_mxfp4(const void *codes, int codes_fmt, int64_t ld_codes, const void *scale,
+                          int scale_fmt, int64_t ld_scale, int64_t rows, int64_t K, int block,
+                          void *out, int out_dtype, int64_t ld_out, void *stream);
+
+/* fp4.py:81-83 codes_to_e4m3 / cuda/fp4_unpack.cuh:52-55 fp4x8_to_e4m3x8 /
+ * cuda/mxfp4_mma_gemm.cu:187-195 unpack_kernel: each input word of 8 packed
+ * codes becomes 8 E4M3 bytes, out[2i] = codes 0..3, out[2i+1] = codes 4..7. */
+int lsmx_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
+
+/* Block-scaled FP4 x FP4 GEMM:  C[M, N] = sum_kb sa[m,kb] sb[n,kb] (A_kb . Bt_kb).
+ * Replaces mxfp4_gemm.py:220-233 mxfp4_gemm_packed / _mxfp4_gemm_packed_kernel
+ * (mxfp4_gemm.py:175-217) and cuda/mxfp4_mma_gemm.cu:69-184.
+ *   a_pk  [M, lda] bytes (lda >= K/2),   a_scale [M, ld_sa] (E8M0 or fp32)
+ *   bt_pk [N, ldb] bytes (ldb >= K/2),   b_scale [N, ld_sb]
+ *   c     [M, ldc] of c_dtype (LSMX_F32 | LSMX_BF16 | LSMX_F16), fp32 accumulate.
+ *   K % 128 == 0 (mxfp4_gemm.py:225); any M, N >= 1.
+ * fp32 scales must hold powers of two (what fp4.py produces); they are read
+ * as their exponent field. */
+int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_t ld_sa,
+                   const uint8_t *bt_pk, int64_t ldb, const void *b_scale, int64_t ld_sb,
+                   int scale_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N,
+                   int64_t K, void *stream);
+
+/* Weight-only GEMM, bf16 activations x MXFP4 weight:
+ *   C[M, N] = A[M, K] . deq(W)[N, K]^T, fp32 accumulate.
+ * Replaces the forward of fp4_linear.py:34-40 for an unquantized activation
+ * (the fake-quant F.linear on dequantized weights) at LLM MLP shapes.
+ *   a [M, lda] bf16;  w_pk [N, ldw] bytes;  w_scale [N, ld_sw] E8M0 or fp32.
+ *   c [M, ldc] of c_dtype.  K % 128 == 0. */
+int lsmx_gemm_bf16f4(const void *a, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                     const void *w_scale, int64_t ld_sw, int scale_fmt, void *c, int c_dtype,
+                     int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* Dual-batch weight-only GEMM: C0 = A0 . deq(W)^T and C1 = A1 . deq(W)^T in
+ * ONE launch, each W tile loaded and dequantized once for both batches.
+ * Replaces dual_gemm.py:244-255 dual_separate(a1, a2, b, b) as used with a
+ * shared weight (train_step.py:52-53), with W in MXFP4.
+ *   a0, a1 [M, lda] bf16; c0, c1 [M, ldc]; other arguments as lsmx_gemm_bf16f4. */
+int lsmx_gemm_dual_bf16f4(const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk,
+                          int64_t ldw, const void *w_scale, int64_t ld_sw, int scale_fmt,
+                          void *c0, void *c1, int c_dtype, int64_t ldc, int64_t M, int64_t N,
+                          int64_t K, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LSMX_H */

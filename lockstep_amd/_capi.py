@@ -1,0 +1,114 @@
+"""ctypes binding of liblsmx.so (declared in include/lsmx.h).
+
+Loading never compiles: build with `python -m lockstep_amd.build` (or
+__graft_entry__.build()).  A missing library raises at import of the first
+op that needs it -- there is no CPU or torch fallback for the kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "liblsmx.so"
+
+OK = 0
+ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_DEVICE, ERR_LAUNCH, ERR_ARG = -1, -2, -3, -4, -5, -6
+F32, BF16, F16 = 0, 1, 2
+CODES_PACKED, CODES_UNPACKED = 0, 1
+SCALE_E8M0, SCALE_F32 = 0, 1
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+
+# name -> argtypes, in the order of include/lsmx.h
+SIGNATURES = {
+    "lsmx_version": [],
+    "lsmx_last_error": [],
+    "lsmx_device_check": [],
+    "lsmx_quantize_mxfp4": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
+    "lsmx_quantize_mxfp4_t": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
+    "lsmx_round_e2m1": [_vp, _int, _i64, _vp, _vp],
+    "lsmx_pack_fp4": [_vp, _vp, _i64, _vp],
+    "lsmx_unpack_fp4": [_vp, _vp, _i64, _vp],
+    "lsmx_dequantize_mxfp4": [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp],
+    "lsmx_fp4_to_e4m3": [_vp, _vp, _i64, _vp],
+    "lsmx_gemm_f4f4": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
+    "lsmx_gemm_bf16f4": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
+    "lsmx_gemm_dual_bf16f4": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64,
+                              _i64, _vp],
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class LsmxError(RuntimeError):
+    """A liblsmx call returned a non-zero status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[lsmx {code}] {msg}")
+        self.code = code
+
+
+def load() -> ctypes.CDLL:
+    """Load liblsmx.so once; raise loudly if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build the HIP kernels with "
+                    "`python -m lockstep_amd.build` (no CPU fallback exists)")
+            L = ctypes.CDLL(str(LIB_PATH))
+            for name, argtypes in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.argtypes = argtypes
+                fn.restype = ctypes.c_char_p if name in ("lsmx_version", "lsmx_last_error") else ctypes.c_int
+            _lib = L
+    return _lib
+
+
+def version() -> str:
+    return load().lsmx_version().decode()
+
+
+def last_error() -> str:
+    return load().lsmx_last_error().decode()
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise LsmxError on a non-zero status."""
+    rc = getattr(load(), name)(*args)
+    if rc != OK:
+        raise LsmxError(rc, last_error())
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """The raw hipStream_t of torch's current stream on t's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    if dt == torch.float16:
+        return F16
+    raise TypeError(f"unsupported dtype {dt}: expected float32, bfloat16 or float16")
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    """The kernels take device memory only: refuse CPU tensors loudly."""
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                "lockstep_amd runs its MXFP4 ops on a gfx950 GPU only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)")

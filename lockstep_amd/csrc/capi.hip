@@ -1,0 +1,248 @@
+// C ABI of liblsmx.so: argument validation, device guard, error reporting,
+// and dispatch to the kernel launchers.  Declarations and reference
+// citations: include/lsmx.h.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "lsmx_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+// Per-device cache of the architecture check (0 = unknown, 1 = gfx950, 2 = other).
+constexpr int kMaxDev = 64;
+int g_arch_ok[kMaxDev] = {0};
+std::mutex g_arch_mu;
+
+int device_guard() {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0) return fail(LSMX_ERR_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+    if (dev >= kMaxDev) return fail(LSMX_ERR_DEVICE, "device index %d out of range", dev);
+    int ok = g_arch_ok[dev];
+    if (ok == 0) {
+        std::lock_guard<std::mutex> lk(g_arch_mu);
+        hipDeviceProp_t p;
+        e = hipGetDeviceProperties(&p, dev);
+        if (e != hipSuccess) return fail(LSMX_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+        ok = strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+        g_arch_ok[dev] = ok;
+        if (ok != 1) return fail(LSMX_ERR_DEVICE, "needs a gfx950 (MI355X) GPU: found %s", p.gcnArchName);
+    }
+    if (ok != 1) return fail(LSMX_ERR_DEVICE, "needs a gfx950 (MI355X) GPU on device %d", dev);
+    return LSMX_OK;
+}
+
+int launched(hipError_t e, const char *what) {
+    if (e != hipSuccess) return fail(LSMX_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return LSMX_OK;
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int elem_size(int dt) { return dt == LSMX_F32 ? 4 : 2; }
+
+}  // namespace
+
+extern "C" {
+
+const char *lsmx_version(void) { return "lsmx 0.1.0 gfx950"; }
+
+const char *lsmx_last_error(void) { return g_err; }
+
+int lsmx_device_check(void) { return device_guard(); }
+
+static int quantize_common(const void *x, int x_dtype, int64_t rows, int64_t K, int64_t ldx, int block,
+                           void *codes, int codes_fmt, int64_t ld_codes, void *scale, int scale_fmt,
+                           int64_t ld_scale, void *stream, bool cols) {
+    const char *fn = cols ? "lsmx_quantize_mxfp4_t" : "lsmx_quantize_mxfp4";
+    if (!x || !codes || !scale) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (x_dtype != LSMX_F32 && x_dtype != LSMX_BF16 && x_dtype != LSMX_F16)
+        return fail(LSMX_ERR_DTYPE, "%s: x_dtype %d unsupported", fn, x_dtype);
+    if (codes_fmt != LSMX_CODES_PACKED && codes_fmt != LSMX_CODES_UNPACKED)
+        return fail(LSMX_ERR_DTYPE, "%s: codes_fmt %d unsupported", fn, codes_fmt);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32)
+        return fail(LSMX_ERR_DTYPE, "%s: scale_fmt %d unsupported", fn, scale_fmt);
+    if (block != 32 && block != 16) return fail(LSMX_ERR_SHAPE, "%s: block must be 16 or 32, got %d", fn, block);
+    if (rows < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % block != 0) return fail(LSMX_ERR_SHAPE, "K=%lld must be a multiple of block=%d", (long long)K, block);
+    const int64_t lead = cols ? rows : K;  // the contiguous extent of x
+    if (ldx < lead) return fail(LSMX_ERR_SHAPE, "%s: ldx %lld < %lld", fn, (long long)ldx, (long long)lead);
+    const int64_t code_w = codes_fmt == LSMX_CODES_PACKED ? K / 2 : K;
+    if (ld_codes < code_w) return fail(LSMX_ERR_SHAPE, "%s: ld_codes %lld < %lld", fn, (long long)ld_codes, (long long)code_w);
+    if (ld_scale < K / block) return fail(LSMX_ERR_SHAPE, "%s: ld_scale too small", fn);
+    const int es = elem_size(x_dtype);
+    if (!cols) {
+        // each lane reads 16 B of a row and writes 2..8 B of codes
+        const int vec_el = 16 / es;
+        const int code_b = (codes_fmt == LSMX_CODES_PACKED ? vec_el / 2 : vec_el);
+        if (!aligned(x, 16) || (ldx * es) % 16) return fail(LSMX_ERR_ALIGN, "%s: x rows must be 16-byte aligned", fn);
+        if (!aligned(codes, code_b) || ld_codes % code_b) return fail(LSMX_ERR_ALIGN, "%s: codes rows must be %d-byte aligned", fn, code_b);
+    } else {
+        if (!aligned(x, es)) return fail(LSMX_ERR_ALIGN, "%s: x misaligned", fn);
+        const int code_b = codes_fmt == LSMX_CODES_PACKED ? block / 2 : 16;
+        if (!aligned(codes, code_b) || ld_codes % code_b) return fail(LSMX_ERR_ALIGN, "%s: codes rows must be %d-byte aligned", fn, code_b);
+    }
+    if (scale_fmt == LSMX_SCALE_F32 && !aligned(scale, 4)) return fail(LSMX_ERR_ALIGN, "%s: fp32 scale misaligned", fn);
+    if (int r = device_guard()) return r;
+    if (rows == 0 || K == 0) return LSMX_OK;
+    lsmx::QuantArgs a{x, x_dtype, rows, K, ldx, block, codes, codes_fmt, ld_codes, scale, scale_fmt, ld_scale};
+    return launched(lsmx::launch_quantize(a, cols, (hipStream_t)stream), fn);
+}
+
+int lsmx_quantize_mxfp4(const void *x, int x_dtype, int64_t rows, int64_t K, int64_t ldx, int block,
+                        void *codes, int codes_fmt, int64_t ld_codes, void *scale, int scale_fmt,
+                        int64_t ld_scale, void *stream) {
+    return quantize_common(x, x_dtype, rows, K, ldx, block, codes, codes_fmt, ld_codes, scale, scale_fmt,
+                           ld_scale, stream, false);
+}
+
+int lsmx_quantize_mxfp4_t(const void *x, int x_dtype, int64_t K, int64_t cols, int64_t ldx, int block,
+                          void *codes, int codes_fmt, int64_t ld_codes, void *scale, int scale_fmt,
+                          int64_t ld_scale, void *stream) {
+    return quantize_common(x, x_dtype, cols, K, ldx, block, codes, codes_fmt, ld_codes, scale, scale_fmt,
+                           ld_scale, stream, true);
+}
+
+int lsmx_round_e2m1(const void *q, int q_dtype, int64_t n, uint8_t *codes, void *stream) {
+    if (!q || !codes) return fail(LSMX_ERR_ARG, "lsmx_round_e2m1: null pointer");
+    if (q_dtype != LSMX_F32 && q_dtype != LSMX_BF16 && q_dtype != LSMX_F16)
+        return fail(LSMX_ERR_DTYPE, "lsmx_round_e2m1: q_dtype %d unsupported", q_dtype);
+    if (n < 0) return fail(LSMX_ERR_SHAPE, "lsmx_round_e2m1: negative size");
+    if (!aligned(q, elem_size(q_dtype))) return fail(LSMX_ERR_ALIGN, "lsmx_round_e2m1: q misaligned");
+    if (int r = device_guard()) return r;
+    if (n == 0) return LSMX_OK;
+    return launched(lsmx::launch_round(q, q_dtype, n, codes, (hipStream_t)stream), "lsmx_round_e2m1");
+}
+
+int lsmx_pack_fp4(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, void *stream) {
+    if (!codes || !packed) return fail(LSMX_ERR_ARG, "lsmx_pack_fp4: null pointer");
+    if (n_bytes < 0) return fail(LSMX_ERR_SHAPE, "lsmx_pack_fp4: negative size");
+    if (!aligned(codes, 16) || !aligned(packed, 8)) return fail(LSMX_ERR_ALIGN, "lsmx_pack_fp4: codes need 16-byte, packed 8-byte alignment");
+    if (int r = device_guard()) return r;
+    if (n_bytes == 0) return LSMX_OK;
+    return launched(lsmx::launch_pack(codes, packed, n_bytes, (hipStream_t)stream), "lsmx_pack_fp4");
+}
+
+int lsmx_unpack_fp4(const uint8_t *packed, uint8_t *codes, int64_t n_bytes, void *stream) {
+    if (!codes || !packed) return fail(LSMX_ERR_ARG, "lsmx_unpack_fp4: null pointer");
+    if (n_bytes < 0) return fail(LSMX_ERR_SHAPE, "lsmx_unpack_fp4: negative size");
+    if (!aligned(codes, 16) || !aligned(packed, 8)) return fail(LSMX_ERR_ALIGN, "lsmx_unpack_fp4: codes need 16-byte, packed 8-byte alignment");
+    if (int r = device_guard()) return r;
+    if (n_bytes == 0) return LSMX_OK;
+    return launched(lsmx::launch_unpack(packed, codes, n_bytes, (hipStream_t)stream), "lsmx_unpack_fp4");
+}
+
+int lsmx_dequantize_mxfp4(const void *codes, int codes_fmt, int64_t ld_codes, const void *scale, int scale_fmt,
+                          int64_t ld_scale, int64_t rows, int64_t K, int block, void *out, int out_dtype,
+                          int64_t ld_out, void *stream) {
+    const char *fn = "lsmx_dequantize_mxfp4";
+    if (!codes || !scale || !out) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (codes_fmt != LSMX_CODES_PACKED && codes_fmt != LSMX_CODES_UNPACKED) return fail(LSMX_ERR_DTYPE, "%s: codes_fmt", fn);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32) return fail(LSMX_ERR_DTYPE, "%s: scale_fmt", fn);
+    if (out_dtype != LSMX_F32 && out_dtype != LSMX_BF16) return fail(LSMX_ERR_DTYPE, "%s: out_dtype", fn);
+    if (block != 32 && block != 16) return fail(LSMX_ERR_SHAPE, "%s: block must be 16 or 32", fn);
+    if (rows < 0 || K < 0 || K % block) return fail(LSMX_ERR_SHAPE, "K=%lld must be a multiple of block=%d", (long long)K, block);
+    const int cb = codes_fmt == LSMX_CODES_PACKED ? 4 : 8;
+    if (!aligned(codes, cb) || ld_codes % cb) return fail(LSMX_ERR_ALIGN, "%s: codes rows misaligned", fn);
+    const int ob = out_dtype == LSMX_F32 ? 4 : 2;
+    if (!aligned(out, 16) || (ld_out * ob) % 16) return fail(LSMX_ERR_ALIGN, "%s: out rows must be 16-byte aligned", fn);
+    if (scale_fmt == LSMX_SCALE_F32 && !aligned(scale, 4)) return fail(LSMX_ERR_ALIGN, "%s: scale misaligned", fn);
+    if (int r = device_guard()) return r;
+    if (rows == 0 || K == 0) return LSMX_OK;
+    lsmx::DequantArgs a{codes, codes_fmt, ld_codes, scale, scale_fmt, ld_scale, rows, K, block, out, out_dtype, ld_out};
+    return launched(lsmx::launch_dequant(a, (hipStream_t)stream), fn);
+}
+
+int lsmx_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream) {
+    if (!in || !out) return fail(LSMX_ERR_ARG, "lsmx_fp4_to_e4m3: null pointer");
+    if (n_words < 0) return fail(LSMX_ERR_SHAPE, "lsmx_fp4_to_e4m3: negative size");
+    if (!aligned(in, 4) || !aligned(out, 8)) return fail(LSMX_ERR_ALIGN, "lsmx_fp4_to_e4m3: misaligned");
+    if (int r = device_guard()) return r;
+    if (n_words == 0) return LSMX_OK;
+    return launched(lsmx::launch_fp4_to_e4m3(in, out, n_words, (hipStream_t)stream), "lsmx_fp4_to_e4m3");
+}
+
+static int check_scale(const char *fn, const void *s, int64_t ld, int fmt, int per_stage) {
+    // the GEMMs read `per_stage` consecutive scales with one aligned load
+    const int bytes = per_stage * (fmt == LSMX_SCALE_F32 ? 4 : 1);
+    if (!aligned(s, bytes) || (ld * (fmt == LSMX_SCALE_F32 ? 4 : 1)) % bytes)
+        return fail(LSMX_ERR_ALIGN, "%s: scale rows must be %d-byte aligned", fn, bytes);
+    return LSMX_OK;
+}
+
+int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_t ld_sa, const uint8_t *bt_pk,
+                   int64_t ldb, const void *b_scale, int64_t ld_sb, int scale_fmt, void *c, int c_dtype,
+                   int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
+    const char *fn = "lsmx_gemm_f4f4";
+    if (!a_pk || !a_scale || !bt_pk || !b_scale || !c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32) return fail(LSMX_ERR_DTYPE, "%s: scale_fmt", fn);
+    if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % 128 != 0) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
+    if (M > (int64_t)1 << 30 || N > (int64_t)1 << 30) return fail(LSMX_ERR_SHAPE, "%s: M, N must be < 2^30", fn);
+    if (lda < K / 2 || ldb < K / 2 || ldc < N || ld_sa < K / 32 || ld_sb < K / 32)
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (!aligned(a_pk, 16) || !aligned(bt_pk, 16) || lda % 16 || ldb % 16)
+        return fail(LSMX_ERR_ALIGN, "%s: packed rows must be 16-byte aligned", fn);
+    if (int r = check_scale(fn, a_scale, ld_sa, scale_fmt, 4)) return r;
+    if (int r = check_scale(fn, b_scale, ld_sb, scale_fmt, 4)) return r;
+    if (!aligned(c, c_dtype == LSMX_F32 ? 4 : 2)) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
+    lsmx::GemmArgs g{a_pk, nullptr, lda, a_scale, ld_sa, bt_pk, ldb, b_scale, ld_sb, scale_fmt, c, nullptr,
+                     c_dtype, ldc, M, N, K};
+    return launched(lsmx::launch_gemm_f4f4(g, (hipStream_t)stream), fn);
+}
+
+static int w4_common(const char *fn, const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                     const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype, int64_t ldc,
+                     int64_t M, int64_t N, int64_t K, void *stream) {
+    if (!a0 || !w_pk || !w_scale || !c0) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32) return fail(LSMX_ERR_DTYPE, "%s: scale_fmt", fn);
+    if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % 128 != 0) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
+    if (M > (int64_t)1 << 30 || N > (int64_t)1 << 30) return fail(LSMX_ERR_SHAPE, "%s: M, N must be < 2^30", fn);
+    if (lda < K || ldw < K / 2 || ldc < N || ld_sw < K / 32) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (!aligned(a0, 16) || (a1 && !aligned(a1, 16)) || (lda * 2) % 16)
+        return fail(LSMX_ERR_ALIGN, "%s: activation rows must be 16-byte aligned", fn);
+    if (!aligned(w_pk, 16) || ldw % 16) return fail(LSMX_ERR_ALIGN, "%s: packed weight rows must be 16-byte aligned", fn);
+    if (int r = check_scale(fn, w_scale, ld_sw, scale_fmt, 2)) return r;
+    const int cb = c_dtype == LSMX_F32 ? 4 : 2;
+    if (!aligned(c0, cb) || (c1 && !aligned(c1, cb))) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
+    lsmx::GemmArgs g{reinterpret_cast<const uint8_t *>(a0), reinterpret_cast<const uint8_t *>(a1), lda, nullptr, 0,
+                     w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype, ldc, M, N, K};
+    return launched(lsmx::launch_gemm_bf16f4(g, (hipStream_t)stream), fn);
+}
+
+int lsmx_gemm_bf16f4(const void *a, int64_t lda, const uint8_t *w_pk, int64_t ldw, const void *w_scale, int64_t ld_sw,
+                     int scale_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
+    return w4_common("lsmx_gemm_bf16f4", a, nullptr, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c, nullptr, c_dtype,
+                     ldc, M, N, K, stream);
+}
+
+int lsmx_gemm_dual_bf16f4(const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                          const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype,
+                          int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
+    if (!a1 || !c1) return fail(LSMX_ERR_ARG, "lsmx_gemm_dual_bf16f4: null pointer");
+    return w4_common("lsmx_gemm_dual_bf16f4", a0, a1, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype,
+                     ldc, M, N, K, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,252 @@
+// Weight-only bf16 x MXFP4 GEMM and its dual-batch form, for gfx950.
+//
+//   single:  C[m, n]  = sum_k A[m, k]  * deq(W)[n, k]
+//   dual:    C0[m, n] = sum_k A0[m, k] * deq(W)[n, k],  C1 likewise with A1
+//
+// Semantics: the fake-quant forward of fp4_linear.py:40 with an unquantized
+// activation (deq(W) = E2M1 value * 2^e, fp4.py:75-78), and dual_gemm.py:78-110
+// _dual_separate_kernel used with one shared weight (train_step.py:52-53):
+// two accumulators, one launch.  deq(W) is exact in bf16 (at most two
+// significant bits times a power of two inside bf16's exponent range), so
+// the products are exact and only fp32 accumulation rounds.
+//
+// Dequantization happens in registers: each lane pulls the 16 packed bytes
+// (32 codes, one MX block) of its weight column for the stage from LDS and
+// turns them into 32 bf16 values with v_cvt_scalef32_pk_bf16_fp4, which
+// multiplies by the block scale on the way.  The MFMA is
+// v_mfma_f32_32x32x16_bf16.  Its K positions are assigned so that, across
+// the four K=16 steps of a 64-wide stage, lane half h covers block h of the
+// stage: the A operand for step s reads A[row][32h + 8s .. +8].  A and W use
+// the same assignment, so the sum is unchanged.
+//
+// Tiling: 256 "A rows" x 256 weight columns per workgroup of 4 waves (2 x 2),
+// 128 x 128 per wave (4 x 4 MFMA tiles).  In dual mode the 256 A rows are
+// 128 rows of A0 followed by the same 128 rows of A1: one weight tile in LDS
+// feeds both batches and is read from memory once per stage.
+#include "lsmx_internal.h"
+
+namespace lsmx {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+namespace w4 {
+constexpr int BR = 256;        // A rows per workgroup (all batches)
+constexpr int BN = 256;        // weight columns per workgroup
+constexpr int BK = 64;         // K per stage
+constexpr int A_ROW_B = BK * 2;    // 128 bytes of bf16 per A row per stage
+constexpr int W_ROW_B = BK / 2;    // 32 bytes of codes per W row per stage
+constexpr int NT = 256;
+constexpr int WT = 128;
+constexpr int GROUP_M = 4;
+}  // namespace w4
+
+LSMX_DEV int a_swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+LSMX_DEV uint32_t bf16_rne_w(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <int CT>
+LSMX_DEV void store_cw(void *c, int64_t idx, float v) {
+    if constexpr (CT == LSMX_F32) reinterpret_cast<float *>(c)[idx] = v;
+    else if constexpr (CT == LSMX_BF16) reinterpret_cast<uint16_t *>(c)[idx] = (uint16_t)bf16_rne_w(v);
+    else reinterpret_cast<_Float16 *>(c)[idx] = (_Float16)v;
+}
+
+LSMX_DEV void tile_coords_w(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    const int total = tiles_m * tiles_n;
+    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+    const int per_group = w4::GROUP_M * tiles_n;
+    const int group = pid / per_group;
+    const int first_m = group * w4::GROUP_M;
+    const int gsz = min(tiles_m - first_m, w4::GROUP_M);
+    const int in_group = pid - group * per_group;
+    tm = first_m + in_group % gsz;
+    tn = in_group / gsz;
+}
+
+template <bool SF32>
+LSMX_DEV uint32_t load_scale2(const void *s, int64_t off) {
+    // 2 consecutive block scales as E8M0 bytes in the low 16 bits
+    if constexpr (SF32) {
+        const u32x2 v = *reinterpret_cast<const u32x2 *>(reinterpret_cast<const float *>(s) + off);
+        return ((v[0] >> 23) & 0xFF) | (((v[1] >> 23) & 0xFF) << 8);
+    } else {
+        return *reinterpret_cast<const uint16_t *>(reinterpret_cast<const uint8_t *>(s) + off);
+    }
+}
+
+LSMX_DEV float e8m0_scale_f32(uint32_t e) {
+    return e == 0u ? u2f(0x00400000u) : (e == 255u ? u2f(0x7FC00000u) : u2f(e << 23));
+}
+
+template <int NB, bool SF32, int CT>
+__global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
+    using namespace w4;
+    constexpr int RPB = BR / NB;   // A rows per batch per workgroup
+    constexpr int RT = 4 / NB;     // row tiles per batch per wave
+    __shared__ __attribute__((aligned(16))) uint8_t sA[2][BR * A_ROW_B];   // 2 x 32 KiB
+    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * W_ROW_B];   // 2 x 8 KiB, [half][col][16B]
+    __shared__ uint32_t sS[2][BN];
+
+    const int tiles_m = (int)((g.M + RPB - 1) / RPB), tiles_n = (int)((g.N + BN - 1) / BN);
+    int tm, tn;
+    tile_coords_w(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * RPB, n0 = (int64_t)tn * BN;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nk = (int)(g.K / BK);
+
+    // A staging: 8 chunks of 16 B per thread; row = q >> 3, chunk = q & 7
+    const uint8_t *ga[8];
+    int a_off[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = i * NT + t;
+        const int row = q >> 3, c = q & 7;
+        const int b = row / RPB, r = row % RPB;
+        const int64_t am = min(m0 + r, g.M - 1);
+        const uint8_t *base = (NB == 2 && b == 1) ? g.a1 : g.a;
+        ga[i] = base + am * g.lda * 2 + c * 16;
+        a_off[i] = row * A_ROW_B + ((c ^ a_swz(row)) << 4);
+    }
+    // W staging: 2 chunks per thread; row = q >> 1, half = q & 1
+    const uint8_t *gw[2];
+    int w_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = i * NT + t;
+        const int row = q >> 1, h = q & 1;
+        const int64_t wn_ = min(n0 + row, g.N - 1);
+        gw[i] = g.b + wn_ * g.ldb + h * 16;
+        w_off[i] = h * (BN * 16) + row * 16;
+    }
+    const int64_t s_row = min(n0 + t, g.N - 1) * g.ld_sb;
+
+    u32x4 ra[8], rw[2];
+    uint32_t rs;
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(ga[i] + (int64_t)kt * A_ROW_B);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) rw[i] = *reinterpret_cast<const u32x4 *>(gw[i] + (int64_t)kt * W_ROW_B);
+        rs = load_scale2<SF32>(g.sb, s_row + (int64_t)kt * 2);
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&sA[buf][a_off[i]]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4 *>(&sW[buf][w_off[i]]) = rw[i];
+        sS[buf][t] = rs;
+    };
+
+    v16f acc[NB][RT][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.0f;
+
+    const int frow = lane & 31, half = lane >> 5;
+
+    gload(0);
+    swrite(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+
+        // dequantize this wave's 4 weight column tiles for the stage:
+        // 32 codes of block `half` -> 32 bf16, 8 per K=16 step.
+        v8bf fw[4][4];  // [col tile][step]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = wn * WT + j * 32 + frow;
+            const u32x4 pw = *reinterpret_cast<const u32x4 *>(&sW[buf][half * (BN * 16) + col * 16]);
+            const float sc = e8m0_scale_f32((sS[buf][col] >> (8 * half)) & 0xFF);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 0);
+                const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 1);
+                const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 2);
+                const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 3);
+                fw[j][s] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int c = half * 4 + s;  // 16-byte chunk: A[row][32h + 8s .. +8]
+            v8bf fa[NB][RT];
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int i = 0; i < RT; ++i) {
+                    const int row = b * RPB + wm * (RT * 32) + i * 32 + frow;
+                    fa[b][i] = *reinterpret_cast<const v8bf *>(&sA[buf][row * A_ROW_B + ((c ^ a_swz(row)) << 4)]);
+                }
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int i = 0; i < RT; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[b][i], fw[j][s], acc[b][i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) swrite(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        void *cb = (NB == 2 && b == 1) ? g.c1 : g.c;
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = n0 + wn * WT + j * 32 + frow;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int64_t row = m0 + wm * (RT * 32) + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                    if (row < g.M && col < g.N) store_cw<CT>(cb, row * g.ldc + col, acc[b][i][j][e]);
+                }
+            }
+    }
+}
+
+template <int NB>
+static hipError_t launch_w4(const GemmArgs &g, hipStream_t s) {
+    constexpr int RPB = w4::BR / NB;
+    const int tiles = (int)(((g.M + RPB - 1) / RPB) * ((g.N + w4::BN - 1) / w4::BN));
+    const dim3 grid(tiles), blk(w4::NT);
+    const bool f = g.scale_fmt == LSMX_SCALE_F32;
+#define LSMX_W(F, CT) hipLaunchKernelGGL((gemm_bf16f4_kernel<NB, F, CT>), grid, blk, 0, s, g)
+    if (f) {
+        if (g.c_dtype == LSMX_F32) LSMX_W(true, LSMX_F32);
+        else if (g.c_dtype == LSMX_BF16) LSMX_W(true, LSMX_BF16);
+        else LSMX_W(true, LSMX_F16);
+    } else {
+        if (g.c_dtype == LSMX_F32) LSMX_W(false, LSMX_F32);
+        else if (g.c_dtype == LSMX_BF16) LSMX_W(false, LSMX_BF16);
+        else LSMX_W(false, LSMX_F16);
+    }
+#undef LSMX_W
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
+    return g.a1 ? launch_w4<2>(g, s) : launch_w4<1>(g, s);
+}
+
+}  // namespace lsmx

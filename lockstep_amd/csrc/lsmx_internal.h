@@ -1,0 +1,64 @@
+// Internal launcher interface between the C ABI (capi.hip) and the kernels.
+#pragma once
+
+#include "lsmx_common.h"
+
+namespace lsmx {
+
+struct QuantArgs {
+    const void *x;
+    int x_dtype;
+    int64_t rows;  // rows (row mode) or columns (column mode)
+    int64_t K;
+    int64_t ldx;
+    int block;
+    void *codes;
+    int codes_fmt;
+    int64_t ld_codes;
+    void *scale;
+    int scale_fmt;
+    int64_t ld_scale;
+};
+
+struct DequantArgs {
+    const void *codes;
+    int codes_fmt;
+    int64_t ld_codes;
+    const void *scale;
+    int scale_fmt;
+    int64_t ld_scale;
+    int64_t rows, K;
+    int block;
+    void *out;
+    int out_dtype;
+    int64_t ld_out;
+};
+
+struct GemmArgs {
+    const uint8_t *a;  // packed A [M, lda] (f4f4) or bf16 A [M, lda] (bf16f4)
+    const uint8_t *a1; // second activation batch (dual), else null
+    int64_t lda;
+    const void *sa;    // A scales (f4f4 only)
+    int64_t ld_sa;
+    const uint8_t *b;  // packed Bt / W [N, ldb]
+    int64_t ldb;
+    const void *sb;
+    int64_t ld_sb;
+    int scale_fmt;
+    void *c;
+    void *c1;          // second output (dual)
+    int c_dtype;
+    int64_t ldc;
+    int64_t M, N, K;
+};
+
+hipError_t launch_quantize(const QuantArgs &a, bool cols, hipStream_t s);
+hipError_t launch_round(const void *q, int q_dtype, int64_t n, uint8_t *codes, hipStream_t s);
+hipError_t launch_pack(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, hipStream_t s);
+hipError_t launch_unpack(const uint8_t *packed, uint8_t *codes, int64_t n_bytes, hipStream_t s);
+hipError_t launch_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n, hipStream_t s);
+hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
+hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s);
+hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s);
+
+}  // namespace lsmx

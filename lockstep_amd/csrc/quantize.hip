@@ -1,0 +1,443 @@
+// MXFP4 quantize / pack / unpack / dequantize / E4M3-expansion kernels for gfx950.
+//
+// Semantics follow the reference's fp4.py (quantize_mxfp4 :57-72,
+// _round_to_e2m1 :43-54, pack_fp4 :91-94, unpack_fp4 :97-99,
+// dequantize_mxfp4 :75-78) and cuda/fp4_unpack.cuh:45-61 (FP4 -> E4M3).
+//
+// Quantize (row mode) is HBM-bound: per 32-block it reads 128 B (fp32) or
+// 64 B (bf16/fp16) and writes 16 B of nibbles plus one E8M0 byte.  Each lane
+// owns 16 contiguous input bytes, so every global_load_dwordx4 of a wave
+// reads 1 KiB of consecutive memory; the lanes of one block (8 for fp32,
+// 4 for 16-bit inputs) reduce the block absmax with DPP row operations, and
+// the scale decision is all-integer (lsmx::block_e8m0).
+#include "lsmx_internal.h"
+
+namespace lsmx {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- helpers
+template <int N>
+LSMX_DEV uint32_t group_max(uint32_t v) {
+    // Max over aligned groups of N lanes (N = 2, 4 or 8) via DPP.
+    static_assert(N == 2 || N == 4 || N == 8 || N == 1, "group size");
+    if constexpr (N >= 2)
+        v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));  // xor 1
+    if constexpr (N >= 4)
+        v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // xor 2
+    if constexpr (N >= 8)
+        v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // half mirror
+    return v;
+}
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+    static constexpr int kPerVec = 4;  // elements per 16-byte vector
+    LSMX_DEV static void bits(const uint4 &v, uint32_t (&b)[4]) {
+        b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+    }
+};
+// bf16 widens to fp32 by a 16-bit shift.
+struct bf16_t { uint16_t v; };
+struct f16_t { uint16_t v; };
+template <>
+struct Elem<bf16_t> {
+    static constexpr int kPerVec = 8;
+    LSMX_DEV static void bits(const uint4 &v, uint32_t (&b)[8]) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            b[2 * i] = w[i] << 16;
+            b[2 * i + 1] = w[i] & 0xFFFF0000u;
+        }
+    }
+};
+template <>
+struct Elem<f16_t> {
+    static constexpr int kPerVec = 8;
+    LSMX_DEV static void bits(const uint4 &v, uint32_t (&b)[8]) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            b[2 * i] = f2u((float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFF)));
+            b[2 * i + 1] = f2u((float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16)));
+        }
+    }
+};
+
+template <int E>
+struct CodeStore;
+// 4 codes -> 2 packed bytes or 4 unpacked bytes
+template <>
+struct CodeStore<4> {
+    LSMX_DEV static void packed(uint8_t *p, const uint32_t (&c)[4]) {
+        *reinterpret_cast<uint16_t *>(p) =
+            (uint16_t)(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
+    }
+    LSMX_DEV static void unpacked(uint8_t *p, const uint32_t (&c)[4]) {
+        *reinterpret_cast<uint32_t *>(p) = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    }
+};
+template <>
+struct CodeStore<8> {
+    LSMX_DEV static void packed(uint8_t *p, const uint32_t (&c)[8]) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w |= c[i] << (4 * i);
+        *reinterpret_cast<uint32_t *>(p) = w;
+    }
+    LSMX_DEV static void unpacked(uint8_t *p, const uint32_t (&c)[8]) {
+        uint2 w;
+        w.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        w.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+        *reinterpret_cast<uint2 *>(p) = w;
+    }
+};
+
+// ------------------------------------------------------- row-mode quantize
+// Grid: (x = chunks of kThreads*kUnroll vectors along a row, y = rows, grid-
+// strided).  One vector = 16 input bytes.
+constexpr int kQThreads = 256;
+constexpr int kQUnroll = 4;
+
+template <typename T, int BLOCK, bool PACKED, bool SCALE_F32>
+__global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
+    const T *__restrict__ x, int64_t rows, int64_t K, int64_t ldx, uint8_t *__restrict__ codes,
+    int64_t ld_codes, void *__restrict__ scale, int64_t ld_scale) {
+    constexpr int E = Elem<T>::kPerVec;
+    constexpr int G = BLOCK / E;  // lanes per block
+    const int64_t vpr = K / E;    // vectors per row
+    const int64_t v0 = (int64_t)blockIdx.x * (kQThreads * kQUnroll) + threadIdx.x;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const T *xr = x + r * ldx;
+        uint4 buf[kQUnroll];
+#pragma unroll
+        for (int u = 0; u < kQUnroll; ++u) {
+            const int64_t v = v0 + u * kQThreads;
+            if (v < vpr) {
+                // streaming read: each input byte is used exactly once
+                const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr) + v);
+                buf[u] = make_uint4(w[0], w[1], w[2], w[3]);
+            } else {
+                buf[u] = make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kQUnroll; ++u) {
+            const int64_t v = v0 + u * kQThreads;
+            uint32_t b[E];
+            Elem<T>::bits(buf[u], b);
+            uint32_t am = 0;
+#pragma unroll
+            for (int i = 0; i < E; ++i) am = max(am, b[i] & 0x7FFFFFFFu);
+            am = group_max<G>(am);  // every lane of the block participates
+            if (v >= vpr) continue;  // whole blocks are in or out of range
+            const uint32_t e8 = block_e8m0(am);
+            uint32_t c[E];
+#pragma unroll
+            for (int i = 0; i < E; ++i) c[i] = e2m1_code(b[i], e8);
+            const int64_t col = v * E;
+            if constexpr (PACKED) CodeStore<E>::packed(codes + r * ld_codes + col / 2, c);
+            else CodeStore<E>::unpacked(codes + r * ld_codes + col, c);
+            if ((threadIdx.x % G) == 0) {
+                const int64_t kb = col / BLOCK;
+                if constexpr (SCALE_F32)
+                    reinterpret_cast<float *>(scale)[r * ld_scale + kb] = e8m0_to_f32(e8);
+                else
+                    reinterpret_cast<uint8_t *>(scale)[r * ld_scale + kb] = (uint8_t)e8;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------- column-mode quantize
+// x[K, cols]: blocks of BLOCK consecutive rows within one column.  One thread
+// per (column, block); consecutive threads take consecutive columns, so every
+// load instruction of a wave reads 64 consecutive elements of one row.
+constexpr int kTThreads = 256;
+
+template <typename T, int BLOCK, bool PACKED, bool SCALE_F32>
+__global__ __launch_bounds__(kTThreads) void quantize_cols_kernel(
+    const T *__restrict__ x, int64_t K, int64_t cols, int64_t ldx, uint8_t *__restrict__ codes,
+    int64_t ld_codes, void *__restrict__ scale, int64_t ld_scale) {
+    const int64_t c = (int64_t)blockIdx.x * kTThreads + threadIdx.x;
+    if (c >= cols) return;
+    const int64_t nkb = K / BLOCK;
+    for (int64_t kb = blockIdx.y; kb < nkb; kb += gridDim.y) {
+        const T *xp = x + kb * BLOCK * ldx + c;
+        uint32_t b[BLOCK];
+#pragma unroll
+        for (int i = 0; i < BLOCK; ++i) {
+            if constexpr (sizeof(T) == 4) {
+                b[i] = __builtin_bit_cast(uint32_t, xp[i * ldx]);
+            } else {
+                const uint16_t h = __builtin_bit_cast(uint16_t, xp[i * ldx]);
+                uint32_t w = (uint32_t)h;
+                if constexpr (__is_same(T, f16_t))
+                    b[i] = f2u((float)__builtin_bit_cast(_Float16, h));
+                else
+                    b[i] = w << 16;
+            }
+        }
+        uint32_t am = 0;
+#pragma unroll
+        for (int i = 0; i < BLOCK; ++i) am = max(am, b[i] & 0x7FFFFFFFu);
+        const uint32_t e8 = block_e8m0(am);
+        uint8_t *out = codes + c * ld_codes;
+        if constexpr (PACKED) {
+            uint32_t w[BLOCK / 8];
+#pragma unroll
+            for (int j = 0; j < BLOCK / 8; ++j) {
+                w[j] = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[j] |= e2m1_code(b[8 * j + i], e8) << (4 * i);
+            }
+            if constexpr (BLOCK == 32)
+                *reinterpret_cast<uint4 *>(out + kb * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+            else
+                *reinterpret_cast<uint2 *>(out + kb * 8) = make_uint2(w[0], w[1]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < BLOCK / 16; ++j) {
+                uint32_t w[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    w[q] = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) w[q] |= e2m1_code(b[16 * j + 4 * q + i], e8) << (8 * i);
+                }
+                *reinterpret_cast<uint4 *>(out + kb * BLOCK + 16 * j) = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+        if constexpr (SCALE_F32)
+            reinterpret_cast<float *>(scale)[c * ld_scale + kb] = e8m0_to_f32(e8);
+        else
+            reinterpret_cast<uint8_t *>(scale)[c * ld_scale + kb] = (uint8_t)e8;
+    }
+}
+
+// ---------------------------------------------------------- elementwise
+template <int DT>
+__global__ void round_kernel(const void *__restrict__ q, int64_t n, uint8_t *__restrict__ codes) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t b;
+    if constexpr (DT == LSMX_F32) b = reinterpret_cast<const uint32_t *>(q)[i];
+    else if constexpr (DT == LSMX_BF16) b = (uint32_t)reinterpret_cast<const uint16_t *>(q)[i] << 16;
+    else b = f2u((float)reinterpret_cast<const _Float16 *>(q)[i]);
+    codes[i] = (uint8_t)e2m1_code(b, 127u);  // scale 1, never the NaN-block path
+}
+
+__global__ void pack_kernel(const uint4 *__restrict__ codes, uint2 *__restrict__ packed, int64_t n16,
+                            const uint8_t *__restrict__ codes_b, uint8_t *__restrict__ packed_b,
+                            int64_t n_bytes) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16) {
+        const uint4 c = codes[i];  // 16 codes -> 8 bytes
+        const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+        uint32_t o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t a = w[2 * h], b = w[2 * h + 1];
+            uint32_t pa = (a & 0xF) | ((a >> 4) & 0xF0) | ((a >> 8) & 0xF00) | ((a >> 12) & 0xF000);
+            uint32_t pb = (b & 0xF) | ((b >> 4) & 0xF0) | ((b >> 8) & 0xF00) | ((b >> 12) & 0xF000);
+            o[h] = pa | (pb << 16);
+        }
+        packed[i] = make_uint2(o[0], o[1]);
+    }
+    // tail bytes (n_bytes not a multiple of 8)
+    const int64_t t = n16 * 8 + i;
+    if (i < 8 && t < n_bytes) packed_b[t] = (uint8_t)((codes_b[2 * t] & 0xF) | ((codes_b[2 * t + 1] & 0xF) << 4));
+}
+
+__global__ void unpack_kernel(const uint2 *__restrict__ packed, uint4 *__restrict__ codes, int64_t n8,
+                              const uint8_t *__restrict__ packed_b, uint8_t *__restrict__ codes_b,
+                              int64_t n_bytes) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n8) {
+        const uint2 p = packed[i];  // 8 bytes -> 16 codes
+        const uint32_t w[2] = {p.x, p.y};
+        uint32_t o[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                uint32_t s = (w[h] >> (16 * q)) & 0xFFFF;  // 4 nibbles
+                o[2 * h + q] = (s & 0xF) | ((s & 0xF0) << 4) | ((s & 0xF00) << 8) | ((s & 0xF000) << 12);
+            }
+        }
+        codes[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    const int64_t t = n8 * 8 + i;
+    if (i < 8 && t < n_bytes) {
+        codes_b[2 * t] = packed_b[t] & 0xF;
+        codes_b[2 * t + 1] = packed_b[t] >> 4;
+    }
+}
+
+// 4 nibbles (low 16 bits of p) -> 4 E4M3 bytes: magnitude by a byte permute
+// against the 8-entry table {00 30 38 3C 40 44 48 4C}, sign bit 3 -> bit 7.
+LSMX_DEV uint32_t fp4x4_to_e4m3x4(uint32_t p) {
+    const uint32_t spread = (p & 0xF) | ((p & 0xF0) << 4) | ((p & 0xF00) << 8) | ((p & 0xF000) << 12);
+    const uint32_t mag = __builtin_amdgcn_perm(0x4C484440u, 0x3C383000u, spread & 0x07070707u);
+    return mag | ((spread & 0x08080808u) << 4);
+}
+
+__global__ void fp4_to_e4m3_kernel(const uint32_t *__restrict__ in, uint2 *__restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const uint32_t p = in[i];
+        out[i] = make_uint2(fp4x4_to_e4m3x4(p & 0xFFFF), fp4x4_to_e4m3x4(p >> 16));
+    }
+}
+
+template <bool PACKED, bool SCALE_F32, bool OUT_BF16>
+__global__ void dequant_kernel(const uint8_t *__restrict__ codes, int64_t ld_codes,
+                               const void *__restrict__ scale, int64_t ld_scale, int64_t rows,
+                               int64_t K, int block, void *__restrict__ out, int64_t ld_out) {
+    // one thread per 8 consecutive elements of a row
+    const int64_t per_row = K / 8;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * per_row) return;
+    const int64_t r = i / per_row, k0 = (i % per_row) * 8;
+    uint32_t c[8];
+    if constexpr (PACKED) {
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(codes + r * ld_codes + k0 / 2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = (w >> (4 * j)) & 0xF;
+    } else {
+        const uint2 w = *reinterpret_cast<const uint2 *>(codes + r * ld_codes + k0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { c[j] = (w.x >> (8 * j)) & 0xF; c[j + 4] = (w.y >> (8 * j)) & 0xF; }
+    }
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int64_t kb = (k0 + j) / block;
+        float s;
+        if constexpr (SCALE_F32) s = reinterpret_cast<const float *>(scale)[r * ld_scale + kb];
+        else s = e8m0_to_f32(reinterpret_cast<const uint8_t *>(scale)[r * ld_scale + kb]);
+        v[j] = e2m1_value(c[j]) * s;
+    }
+    if constexpr (OUT_BF16) {
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // exact: an E2M1 value times a power of two has <= 2 significant bits
+            const uint32_t lo = f2u(v[2 * j]) >> 16, hi = f2u(v[2 * j + 1]) >> 16;
+            o[j] = lo | (hi << 16);
+        }
+        *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(out) + r * ld_out + k0) =
+            make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+        float4 *o = reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + r * ld_out + k0);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// ---------------------------------------------------------------- launchers
+template <typename T, int BLOCK, bool PACKED, bool SF32>
+static hipError_t launch_rows(const QuantArgs &a, hipStream_t s) {
+    constexpr int E = Elem<T>::kPerVec;
+    const int64_t vpr = a.K / E;
+    const int64_t gx = (vpr + kQThreads * kQUnroll - 1) / (kQThreads * kQUnroll);
+    const int64_t gy = a.rows < 65535 ? a.rows : 65535;
+    hipLaunchKernelGGL((quantize_rows_kernel<T, BLOCK, PACKED, SF32>), dim3((unsigned)gx, (unsigned)gy),
+                       dim3(kQThreads), 0, s, reinterpret_cast<const T *>(a.x), a.rows, a.K, a.ldx,
+                       reinterpret_cast<uint8_t *>(a.codes), a.ld_codes, a.scale, a.ld_scale);
+    return hipGetLastError();
+}
+
+template <typename T, int BLOCK, bool PACKED, bool SF32>
+static hipError_t launch_cols(const QuantArgs &a, hipStream_t s) {
+    // a.rows = cols, a.K = K for the column mode
+    const int64_t gx = (a.rows + kTThreads - 1) / kTThreads;
+    const int64_t nkb = a.K / BLOCK;
+    const int64_t gy = nkb < 65535 ? nkb : 65535;
+    hipLaunchKernelGGL((quantize_cols_kernel<T, BLOCK, PACKED, SF32>), dim3((unsigned)gx, (unsigned)gy),
+                       dim3(kTThreads), 0, s, reinterpret_cast<const T *>(a.x), a.K, a.rows, a.ldx,
+                       reinterpret_cast<uint8_t *>(a.codes), a.ld_codes, a.scale, a.ld_scale);
+    return hipGetLastError();
+}
+
+template <typename T, int BLOCK>
+static hipError_t dispatch_fmt(const QuantArgs &a, bool cols, hipStream_t s) {
+    const bool packed = a.codes_fmt == LSMX_CODES_PACKED, f32 = a.scale_fmt == LSMX_SCALE_F32;
+#define LSMX_Q(P, F) return cols ? launch_cols<T, BLOCK, P, F>(a, s) : launch_rows<T, BLOCK, P, F>(a, s)
+    if (packed && f32) LSMX_Q(true, true);
+    if (packed) LSMX_Q(true, false);
+    if (f32) LSMX_Q(false, true);
+    LSMX_Q(false, false);
+#undef LSMX_Q
+}
+
+template <typename T>
+static hipError_t dispatch_block(const QuantArgs &a, bool cols, hipStream_t s) {
+    return a.block == 32 ? dispatch_fmt<T, 32>(a, cols, s) : dispatch_fmt<T, 16>(a, cols, s);
+}
+
+hipError_t launch_quantize(const QuantArgs &a, bool cols, hipStream_t s) {
+    switch (a.x_dtype) {
+        case LSMX_F32: return dispatch_block<float>(a, cols, s);
+        case LSMX_BF16: return dispatch_block<bf16_t>(a, cols, s);
+        default: return dispatch_block<f16_t>(a, cols, s);
+    }
+}
+
+hipError_t launch_round(const void *q, int q_dtype, int64_t n, uint8_t *codes, hipStream_t s) {
+    const dim3 grid((unsigned)((n + 255) / 256)), blk(256);
+    if (q_dtype == LSMX_F32) hipLaunchKernelGGL(round_kernel<LSMX_F32>, grid, blk, 0, s, q, n, codes);
+    else if (q_dtype == LSMX_BF16) hipLaunchKernelGGL(round_kernel<LSMX_BF16>, grid, blk, 0, s, q, n, codes);
+    else hipLaunchKernelGGL(round_kernel<LSMX_F16>, grid, blk, 0, s, q, n, codes);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, hipStream_t s) {
+    const int64_t n16 = n_bytes / 8;  // groups of 16 codes
+    const int64_t threads = n16 > 8 ? n16 : 8;
+    hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<const uint4 *>(codes), reinterpret_cast<uint2 *>(packed), n16,
+                       codes, packed, n_bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack(const uint8_t *packed, uint8_t *codes, int64_t n_bytes, hipStream_t s) {
+    const int64_t n8 = n_bytes / 8;
+    const int64_t threads = n8 > 8 ? n8 : 8;
+    hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<const uint2 *>(packed), reinterpret_cast<uint4 *>(codes), n8,
+                       packed, codes, n_bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(fp4_to_e4m3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in,
+                       reinterpret_cast<uint2 *>(out), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(const DequantArgs &a, hipStream_t s) {
+    const int64_t n = a.rows * (a.K / 8);
+    const dim3 grid((unsigned)((n + 255) / 256)), blk(256);
+    const bool p = a.codes_fmt == LSMX_CODES_PACKED, f = a.scale_fmt == LSMX_SCALE_F32,
+               b = a.out_dtype == LSMX_BF16;
+#define LSMX_D(P, F, B)                                                                          \
+    hipLaunchKernelGGL((dequant_kernel<P, F, B>), grid, blk, 0, s,                               \
+                       reinterpret_cast<const uint8_t *>(a.codes), a.ld_codes, a.scale, a.ld_scale, \
+                       a.rows, a.K, a.block, a.out, a.ld_out)
+    if (p && f && b) LSMX_D(true, true, true);
+    else if (p && f) LSMX_D(true, true, false);
+    else if (p && b) LSMX_D(true, false, true);
+    else if (p) LSMX_D(true, false, false);
+    else if (f && b) LSMX_D(false, true, true);
+    else if (f) LSMX_D(false, true, false);
+    else if (b) LSMX_D(false, false, true);
+    else LSMX_D(false, false, false);
+#undef LSMX_D
+    return hipGetLastError();
+}
+
+}  // namespace lsmx

@@ -1,0 +1,266 @@
+"""FP4 (E2M1) / MXFP4 primitives on gfx950 -- drop-in for the reference's fp4.py.
+
+Same names, signatures, return dtypes and shapes as fp4.py:20-125.  The
+quantizer, packing, unpacking, dequantization and E4M3 expansion run as HIP
+kernels in liblsmx.so on the tensor's GPU and on torch's current stream;
+they refuse CPU tensors (there is no CPU fallback).  The test-data helpers
+(random_codes, codes_to_q, blockwise_exact_dot) and the fp64 reference GEMM
+are plain torch, like the reference's, and run wherever their inputs live.
+
+Layout conventions (fp4.py:3-8):
+    A      : [M, K]      K-contiguous
+    B      : [K, N]      N-contiguous   (for the fp8 path,  C = A @ B)
+    B_T    : [N, K]      K-contiguous   (for the packed path, C = A @ B_T.T)
+    A scale: [M, K//32]
+    B scale: [K//32, N]  (fp8 path)  or  [N, K//32]  (packed path)
+
+Additions beyond fp4.py: quantize_pack_mxfp4 (fused quantize + pack with
+E8M0 byte scales, the form the GEMMs consume), quantize_mxfp4_t (quantize
+along the other axis), and the E8M0 <-> fp32 scale conversions.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _capi as C
+
+# ---------------------------------------------------------------- E2M1 tables
+# fp4.py:20-34
+_E2M1_MAG = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]          # code & 7 -> magnitude
+FP4_MAX = 6.0
+FP4_EMAX = 2                                                   # max exponent of E2M1
+
+E2M1_VALUES = torch.tensor(_E2M1_MAG + [-v for v in _E2M1_MAG], dtype=torch.float32)
+
+# code -> E4M3 byte: sign<<7 | (exp+6)<<3 | mant<<2, with 0 and 0.5 special.
+E2M1_TO_E4M3 = torch.tensor(
+    [0x00, 0x30, 0x38, 0x3C, 0x40, 0x44, 0x48, 0x4C,
+     0x80, 0xB0, 0xB8, 0xBC, 0xC0, 0xC4, 0xC8, 0xCC], dtype=torch.uint8)
+
+# code -> 2*value as a signed integer (the exact integer grid).
+E2M1_Q = torch.tensor([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12],
+                      dtype=torch.int32)
+
+
+def random_codes(shape, device="cpu") -> torch.Tensor:
+    """Uniform over the 15 distinct E2M1 codes (negative zero excluded). fp4.py:37-40"""
+    pick = torch.tensor([c for c in range(16) if c != 8], device=device, dtype=torch.uint8)
+    return pick[torch.randint(0, 15, shape, device=device)]
+
+
+def _round_to_e2m1(q: torch.Tensor) -> torch.Tensor:
+    """Round-to-nearest onto the E2M1 grid; 4-bit codes as uint8 (fp4.py:43-54).
+
+    Ties go to the smaller magnitude, |q| clips at 6, the sign bit is copied
+    (so -0.0 gives code 8) and NaN gives magnitude 7."""
+    C.require_device(q)
+    if q.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        q = q.float()
+    qc = q.contiguous()
+    out = torch.empty(qc.shape, dtype=torch.uint8, device=q.device)
+    C.call("lsmx_round_e2m1", qc.data_ptr(), C.dtype_code(qc.dtype), qc.numel(), out.data_ptr(),
+           C.stream_of(qc))
+    return out
+
+
+def _as_rows(x: torch.Tensor):
+    """x [..., K] -> (2-D row view with unit stride along K, leading shape)."""
+    *lead, K = x.shape
+    x2 = x.reshape(-1, K) if x.dim() != 2 else x
+    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < K) \
+            or (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2, lead
+
+
+def _src(x: torch.Tensor) -> torch.Tensor:
+    # fp4.py:63 converts to fp32 first; fp32, bf16 and fp16 widen exactly in
+    # the kernel, anything else is widened here.
+    return x if x.dtype in (torch.float32, torch.bfloat16, torch.float16) else x.float()
+
+
+def quantize_mxfp4(x: torch.Tensor, block: int = 32):
+    """MXFP4 quantize along the last dim (fp4.py:57-72).
+
+    Returns (codes uint8 [..., K], scale fp32 [..., K//block]).
+    Shared scale follows OCP MX: 2^(floor(log2(amax)) - emax_elem), emax_elem = 2,
+    with log2 rounded to float32 as torch computes it."""
+    *lead, K = x.shape
+    assert K % block == 0, f"K={K} must be a multiple of block={block}"
+    C.require_device(x)
+    x = _src(x)
+    x2, lead = _as_rows(x)
+    rows = x2.shape[0]
+    codes = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((rows, K // block), dtype=torch.float32, device=x.device)
+    C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
+           x2.stride(0) if rows > 1 else K, block, codes.data_ptr(), C.CODES_UNPACKED, K,
+           scale.data_ptr(), C.SCALE_F32, K // block, C.stream_of(x2))
+    return codes.reshape(*lead, K), scale.reshape(*lead, K // block)
+
+
+def quantize_pack_mxfp4(x: torch.Tensor, block: int = 32):
+    """Fused quantize_mxfp4 + pack_fp4 with E8M0 byte scales.
+
+    Returns (packed uint8 [..., K//2], e8m0 uint8 [..., K//block]); the bytes
+    equal pack_fp4(codes) and the exponent fields of quantize_mxfp4's scales."""
+    *lead, K = x.shape
+    assert K % block == 0, f"K={K} must be a multiple of block={block}"
+    C.require_device(x)
+    x = _src(x)
+    x2, lead = _as_rows(x)
+    rows = x2.shape[0]
+    packed = torch.empty((rows, K // 2), dtype=torch.uint8, device=x.device)
+    e8m0 = torch.empty((rows, K // block), dtype=torch.uint8, device=x.device)
+    C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
+           x2.stride(0) if rows > 1 else K, block, packed.data_ptr(), C.CODES_PACKED, K // 2,
+           e8m0.data_ptr(), C.SCALE_E8M0, K // block, C.stream_of(x2))
+    return packed.reshape(*lead, K // 2), e8m0.reshape(*lead, K // block)
+
+
+def quantize_mxfp4_t(x: torch.Tensor, block: int = 32, packed: bool = True, e8m0: bool = True):
+    """Quantize a 2-D x [K, N] along its FIRST axis, without a transpose copy.
+
+    Equals quantize_pack_mxfp4(x.t().contiguous()) (packed, e8m0) or
+    quantize_mxfp4(x.t().contiguous()) (packed=False, e8m0=False): outputs are
+    laid out for x^T, [N, K//2 or K] and [N, K//block]."""
+    C.require_device(x)
+    x = _src(x)
+    assert x.dim() == 2, "quantize_mxfp4_t takes a 2-D tensor"
+    K, N = x.shape
+    assert K % block == 0, f"K={K} must be a multiple of block={block}"
+    if x.stride(1) != 1 or (K > 1 and x.stride(0) < N):
+        x = x.contiguous()
+    codes = torch.empty((N, K // 2 if packed else K), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((N, K // block), dtype=torch.uint8 if e8m0 else torch.float32,
+                        device=x.device)
+    C.call("lsmx_quantize_mxfp4_t", x.data_ptr(), C.dtype_code(x.dtype), K, N,
+           x.stride(0) if K > 1 else N, block, codes.data_ptr(),
+           C.CODES_PACKED if packed else C.CODES_UNPACKED, codes.shape[1], scale.data_ptr(),
+           C.SCALE_E8M0 if e8m0 else C.SCALE_F32, K // block, C.stream_of(x))
+    return codes, scale
+
+
+def e8m0_to_scale(e8m0: torch.Tensor) -> torch.Tensor:
+    """E8M0 bytes -> fp32 powers of two (0xFF -> NaN).  Exact."""
+    s = (e8m0.to(torch.int32) << 23).view(torch.float32)
+    return torch.where(e8m0 == 255, torch.full_like(s, float("nan")), s)
+
+
+def scale_to_e8m0(scale: torch.Tensor) -> torch.Tensor:
+    """fp32 powers of two -> E8M0 bytes (the exponent field; NaN -> 0xFF).  Exact."""
+    e = ((scale.contiguous().view(torch.int32) >> 23) & 0xFF).to(torch.uint8)
+    return torch.where(torch.isnan(scale), torch.full_like(e, 255), e)
+
+
+def _scale_fmt(scale: torch.Tensor) -> int:
+    if scale.dtype == torch.float32:
+        return C.SCALE_F32
+    if scale.dtype == torch.uint8:
+        return C.SCALE_E8M0
+    raise TypeError(f"scale must be float32 (powers of two) or uint8 (E8M0), got {scale.dtype}")
+
+
+def dequantize_mxfp4(codes: torch.Tensor, scale: torch.Tensor, block: int = 32):
+    """fp32 values = E2M1_VALUES[codes] * scale, per block (fp4.py:75-78).
+
+    `scale` may be fp32 (as quantize_mxfp4 returns) or E8M0 bytes."""
+    C.require_device(codes, scale)
+    *lead, K = codes.shape
+    c2 = codes.reshape(-1, K).contiguous()
+    s2 = scale.reshape(-1, K // block).contiguous()
+    out = torch.empty(c2.shape, dtype=torch.float32, device=codes.device)
+    C.call("lsmx_dequantize_mxfp4", c2.data_ptr(), C.CODES_UNPACKED, K, s2.data_ptr(),
+           _scale_fmt(s2), K // block, c2.shape[0], K, block, out.data_ptr(), C.F32, K,
+           C.stream_of(c2))
+    return out.reshape(*lead, K)
+
+
+def dequantize_packed(packed: torch.Tensor, scale: torch.Tensor, block: int = 32,
+                      out_dtype: torch.dtype = torch.float32):
+    """Packed nibbles [..., K//2] + scales -> values [..., K] in fp32 or bf16 (exact)."""
+    C.require_device(packed, scale)
+    *lead, Kh = packed.shape
+    K = 2 * Kh
+    p2 = packed.reshape(-1, Kh).contiguous()
+    s2 = scale.reshape(-1, K // block).contiguous()
+    out = torch.empty((p2.shape[0], K), dtype=out_dtype, device=packed.device)
+    C.call("lsmx_dequantize_mxfp4", p2.data_ptr(), C.CODES_PACKED, Kh, s2.data_ptr(),
+           _scale_fmt(s2), K // block, p2.shape[0], K, block, out.data_ptr(), C.dtype_code(out_dtype),
+           K, C.stream_of(p2))
+    return out.reshape(*lead, K)
+
+
+def codes_to_e4m3(codes: torch.Tensor) -> torch.Tensor:
+    """Lossless FP4 -> FP8(E4M3) cast via table lookup (fp4.py:81-83)."""
+    C.require_device(codes)
+    shape = codes.shape
+    flat = codes.reshape(-1)
+    n = flat.numel()
+    pad = (-n) % 16
+    if pad:
+        flat = torch.cat([flat, torch.zeros(pad, dtype=torch.uint8, device=codes.device)])
+    words = pack_fp4(flat.contiguous()).view(torch.int32)          # 8 codes per word
+    out = torch.empty(words.numel() * 2, dtype=torch.int32, device=codes.device)
+    C.call("lsmx_fp4_to_e4m3", words.data_ptr(), out.data_ptr(), words.numel(), C.stream_of(words))
+    return out.view(torch.uint8)[:n].reshape(shape).view(torch.float8_e4m3fn)
+
+
+def fp4_to_e4m3_words(words: torch.Tensor) -> torch.Tensor:
+    """cuda/fp4_unpack.cuh:52-55 on a tensor of uint32 words (int32 storage):
+    each word of 8 packed codes -> 2 words of E4M3 bytes."""
+    C.require_device(words)
+    w = words.contiguous()
+    out = torch.empty(w.numel() * 2, dtype=torch.int32, device=w.device)
+    C.call("lsmx_fp4_to_e4m3", w.data_ptr(), out.data_ptr(), w.numel(), C.stream_of(w))
+    return out
+
+
+def codes_to_q(codes: torch.Tensor) -> torch.Tensor:
+    """FP4 code -> 2*value as int32 (the exact integer grid). fp4.py:86-88"""
+    return E2M1_Q.to(codes.device)[codes.long()]
+
+
+def pack_fp4(codes: torch.Tensor) -> torch.Tensor:
+    """[..., K] uint8 codes -> [..., K//2] bytes; even index in the low nibble (fp4.py:91-94)."""
+    assert codes.shape[-1] % 2 == 0
+    C.require_device(codes)
+    c = codes.contiguous()
+    if c.data_ptr() % 16:
+        c = c.clone()
+    out = torch.empty((*c.shape[:-1], c.shape[-1] // 2), dtype=torch.uint8, device=c.device)
+    C.call("lsmx_pack_fp4", c.data_ptr(), out.data_ptr(), out.numel(), C.stream_of(c))
+    return out
+
+
+def unpack_fp4(packed: torch.Tensor) -> torch.Tensor:
+    """[..., K//2] bytes -> [..., K] codes (fp4.py:97-99)."""
+    C.require_device(packed)
+    p = packed.contiguous()
+    if p.data_ptr() % 8:
+        p = p.clone()
+    out = torch.empty((*p.shape[:-1], p.shape[-1] * 2), dtype=torch.uint8, device=p.device)
+    C.call("lsmx_unpack_fp4", p.data_ptr(), out.data_ptr(), p.numel(), C.stream_of(p))
+    return out
+
+
+# ------------------------------------------------------------------ references
+def reference_mxfp4_gemm(a_codes, a_scale, b_codes, b_scale, block=32):
+    """float64 reference for C = A @ B with A [M,K], B [K,N] (fp4.py:103-112).
+
+    b_codes is [K, N] and b_scale is [K//block, N], so B is quantized along K."""
+    A = dequantize_mxfp4(a_codes, a_scale, block).double()                  # [M,K]
+    Bv = E2M1_VALUES.to(b_codes.device)[b_codes.long()].double()            # [K,N]
+    K, N = Bv.shape
+    B = (Bv.reshape(K // block, block, N) * b_scale.double().unsqueeze(1)).reshape(K, N)
+    return (A @ B).float()
+
+
+def blockwise_exact_dot(qa: torch.Tensor, qb: torch.Tensor, block: int = 32):
+    """Exact integer dot products per block from the int grid (fp4.py:115-125).
+
+    Returns int64 [.., K//block] of sum(qa*qb) per block; |sum| <= 144*block."""
+    p = (qa.long() * qb.long())
+    *lead, K = p.shape
+    return p.reshape(*lead, K // block, block).sum(-1)

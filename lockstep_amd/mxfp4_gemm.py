@@ -1,0 +1,100 @@
+"""MXFP4 GEMMs on gfx950's scaled MFMA -- drop-in for the reference's mxfp4_gemm.py.
+
+The reference emulates MXFP4 on Hopper FP8 tensor cores and promotes to an
+fp32 accumulator at every 32-block to apply the scales (mxfp4_gemm.py:1-14).
+gfx950 has block-scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4): each lane
+hands the instruction 32 FP4 codes of one row plus that block's E8M0 scale,
+so no promotion step exists and the packed nibbles go straight from HBM to
+the matrix cores.  Kernel: lockstep_amd/csrc/gemm_f4f4.hip.
+
+Same names and signatures as mxfp4_gemm.py:23-174; the `CFG` dict keeps the
+reference's keys for callers that read it, with this build's tile sizes.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _capi as C
+from . import fp4 as _fp4
+
+# Tile configuration of the gfx950 kernel (the reference's CFG keys).
+CFG = dict(BLOCK_M=256, BLOCK_N=256, SUB=4, GROUP_M=4, num_warps=4, num_stages=2)
+
+
+def _out_code(dt: torch.dtype) -> int:
+    return C.dtype_code(dt)
+
+
+def _rows16(t: torch.Tensor) -> torch.Tensor:
+    """Unit stride along K and 16-byte aligned rows, else a contiguous copy."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or (t.shape[0] > 1 and t.stride(0) % 16):
+        t = t.contiguous()
+    return t
+
+
+def _scales(s: torch.Tensor, rows: int, nkb: int) -> torch.Tensor:
+    fmt_bytes = 4 if s.dtype == torch.float32 else 1
+    if s.stride(-1) != 1 or (rows > 1 and (s.stride(0) * fmt_bytes) % (4 * fmt_bytes)) \
+            or s.data_ptr() % (4 * fmt_bytes):
+        s = s.contiguous()
+    return s
+
+
+def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
+    """a_pk [M,K//2] uint8, bt_pk [N,K//2] uint8, a_scale [M,K//32], b_scale [N,K//32].
+
+    Scales are fp32 powers of two (as fp4.quantize_mxfp4 returns) or E8M0
+    bytes (as fp4.quantize_pack_mxfp4 returns); both operands must use the
+    same format.  Returns C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
+    M, Kh = a_pk.shape
+    N, Kh2 = bt_pk.shape
+    K = Kh * 2
+    assert Kh == Kh2 and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
+    C.require_device(a_pk, bt_pk, a_scale, b_scale)
+    assert a_scale.dtype == b_scale.dtype, "a_scale and b_scale must share a format"
+    a_pk, bt_pk = _rows16(a_pk), _rows16(bt_pk)
+    a_scale = _scales(a_scale, M, K // 32)
+    b_scale = _scales(b_scale, N, K // 32)
+    c = torch.empty((M, N), device=a_pk.device, dtype=out_dtype)
+    if M == 0 or N == 0:
+        return c
+    C.call("lsmx_gemm_f4f4", a_pk.data_ptr(), a_pk.stride(0) if M > 1 else Kh,
+           a_scale.data_ptr(), a_scale.stride(0) if M > 1 else K // 32,
+           bt_pk.data_ptr(), bt_pk.stride(0) if N > 1 else Kh,
+           b_scale.data_ptr(), b_scale.stride(0) if N > 1 else K // 32,
+           _fp4._scale_fmt(a_scale), c.data_ptr(), _out_code(out_dtype), N, M, N, K,
+           C.stream_of(c))
+    return c
+
+
+def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
+    """Weight-only GEMM: a [M,K] bf16 activations x MXFP4 weight w_pk [N,K//2]
+    with w_scale [N,K//32] (fp32 powers of two or E8M0).  Returns
+    a @ deq(W).T [M, N] in out_dtype, fp32 accumulate."""
+    M, K = a.shape
+    N, Kh = w_pk.shape
+    assert K == 2 * Kh and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
+    C.require_device(a, w_pk, w_scale)
+    if a.dtype != torch.bfloat16:
+        a = a.to(torch.bfloat16)
+    a = _rows16(a)
+    w_pk = _rows16(w_pk)
+    w_scale = _scales(w_scale, N, K // 32)
+    c = torch.empty((M, N), device=a.device, dtype=out_dtype)
+    if M == 0 or N == 0:
+        return c
+    C.call("lsmx_gemm_bf16f4", a.data_ptr(), a.stride(0) if M > 1 else K, w_pk.data_ptr(),
+           w_pk.stride(0) if N > 1 else Kh, w_scale.data_ptr(), w_scale.stride(0) if N > 1 else K // 32,
+           _fp4._scale_fmt(w_scale), c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
+    return c
+
+
+def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
+    """a_fp8 [M,K] K-contig, b_fp8 [K,N] N-contig, a_scale [M,K//32], b_scale [K//32,N].
+
+    Operands are E4M3 bytes holding E2M1 values (fp4.codes_to_e4m3), as in
+    mxfp4_gemm.py:133-146."""
+    raise NotImplementedError(
+        "mxfp4_gemm_fp8 (E4M3-operand path) is not built yet on gfx950; "
+        "use mxfp4_gemm_packed on packed FP4 operands")

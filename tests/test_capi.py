@@ -1,0 +1,125 @@
+"""CPU tests of the C ABI: the library loads, exports every entry point the
+header declares, and rejects bad arguments before touching a device.  No
+compute call runs here (no GPU in this process)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from lockstep_amd import _capi as C
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "lsmx.h"
+
+
+def declared_symbols():
+    src = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(lsmx_\w+)\s*\(", src, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.load()
+    names = declared_symbols()
+    assert len(names) >= 13
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(C.SIGNATURES), "ctypes table and header disagree"
+
+
+def test_header_constants_match_binding():
+    src = HEADER.read_text()
+    consts = dict((k, int(v)) for k, v in re.findall(r"#define (LSMX_\w+) (-?\d+)", src))
+    assert consts["LSMX_OK"] == C.OK
+    assert consts["LSMX_ERR_SHAPE"] == C.ERR_SHAPE and consts["LSMX_ERR_ALIGN"] == C.ERR_ALIGN
+    assert consts["LSMX_ERR_DTYPE"] == C.ERR_DTYPE and consts["LSMX_ERR_DEVICE"] == C.ERR_DEVICE
+    assert consts["LSMX_F32"] == C.F32 and consts["LSMX_BF16"] == C.BF16 and consts["LSMX_F16"] == C.F16
+    assert consts["LSMX_CODES_PACKED"] == C.CODES_PACKED and consts["LSMX_SCALE_F32"] == C.SCALE_F32
+
+
+def test_version_string():
+    assert C.version().startswith("lsmx ") and "gfx950" in C.version()
+
+
+def _rc(name, *args):
+    return getattr(C.load(), name)(*args)
+
+
+FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+
+
+def test_null_pointer_is_rejected():
+    assert _rc("lsmx_quantize_mxfp4", None, 0, 4, 64, 64, 32, FAKE, 0, 32, FAKE, 0, 2, None) == C.ERR_ARG
+    assert "null" in C.last_error()
+
+
+def test_block_multiple_is_rejected_with_reference_message():
+    rc = _rc("lsmx_quantize_mxfp4", FAKE, 0, 4, 48, 48, 32, FAKE, 0, 24, FAKE, 0, 2, None)
+    assert rc == C.ERR_SHAPE
+    assert "K=48 must be a multiple of block=32" in C.last_error()   # fp4.py:65
+
+
+def test_gemm_k_multiple_is_rejected_with_reference_message():
+    rc = _rc("lsmx_gemm_f4f4", FAKE, 48, FAKE, 3, FAKE, 48, FAKE, 3, 0, FAKE, 1, 8, 8, 8, 96, None)
+    assert rc == C.ERR_SHAPE
+    assert "K must be a multiple of 128" in C.last_error()          # mxfp4_gemm.py:225
+
+
+def test_bad_dtype_and_alignment_are_rejected():
+    assert _rc("lsmx_quantize_mxfp4", FAKE, 7, 4, 64, 64, 32, FAKE, 0, 32, FAKE, 0, 2, None) == C.ERR_DTYPE
+    misaligned = ctypes.c_void_p(0x1004)
+    rc = _rc("lsmx_quantize_mxfp4", misaligned, 0, 4, 64, 64, 32, FAKE, 0, 32, FAKE, 0, 2, None)
+    assert rc == C.ERR_ALIGN
+    rc = _rc("lsmx_gemm_f4f4", FAKE, 64, FAKE, 4, FAKE, 64, FAKE, 4, 0, FAKE, 9, 8, 8, 8, 128, None)
+    assert rc == C.ERR_DTYPE
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="a GPU is present")
+def test_device_guard_without_gpu():
+    assert _rc("lsmx_device_check") == C.ERR_DEVICE
+
+
+def test_python_api_refuses_cpu_tensors():
+    from lockstep_amd import fp4
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fp4.quantize_mxfp4(torch.zeros(2, 32))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fp4.pack_fp4(torch.zeros(2, 32, dtype=torch.uint8))
+
+
+def test_python_api_keeps_reference_asserts():
+    from lockstep_amd import fp4, mxfp4_gemm
+    with pytest.raises(AssertionError, match="K=48 must be a multiple of block=32"):
+        fp4.quantize_mxfp4(torch.zeros(2, 48))
+    with pytest.raises(AssertionError, match="K must be a multiple of 128"):
+        mxfp4_gemm.mxfp4_gemm_packed(torch.zeros(4, 48, dtype=torch.uint8),
+                                     torch.zeros(4, 48, dtype=torch.uint8),
+                                     torch.ones(4, 3), torch.ones(4, 3))
+
+
+def test_device_guard_module_exits_without_gfx950():
+    from lockstep_amd import device
+    if torch.cuda.is_available() and "gfx950" in torch.cuda.get_device_properties(0).gcnArchName:
+        pytest.skip("running on a gfx950")
+    with pytest.raises(SystemExit, match="needs an MI355X"):
+        device.require_gfx950()
+
+
+def test_fp4_linear_reports_path_without_gpu():
+    from lockstep_amd import fp4_linear
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    assert fp4_linear.kernel() is None and fp4_linear.path() == "unavailable"
+
+
+def test_slot_arithmetic():
+    # tests/test_fp4.py:95-102 (dual slot split round trip)
+    from lockstep_amd import dual_gemm as dg
+    for k in (8, 32, 128):
+        s = dg.slot_offset(k)
+        c1 = torch.tensor([144.0 * k, -144.0 * k, 3.0], dtype=torch.float64)
+        c2 = torch.tensor([-144.0 * k, 144.0 * k, -7.0], dtype=torch.float64)
+        g1, g2 = dg.unpack_dual(c1 + c2 * 2.0 ** s, s)
+        assert torch.equal(g1, c1) and torch.equal(g2, c2)

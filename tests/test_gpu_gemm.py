@@ -1,0 +1,193 @@
+"""GPU parity of the block-scaled GEMMs against the fp64 oracle (fp4.py:103-112).
+
+Tolerances (stated by the build's target, bench.py:71 metric
+max|c - ref| / max|ref|):  fp32 output <= 1e-5,  bf16 output <= 1e-2.
+Integer-grid inputs with unit scales must be bit-exact (bench.py:44-57).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gen
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 1e-2}
+
+
+@pytest.fixture(scope="module")
+def mods(dev):
+    from lockstep_amd import dual_gemm, fp4, fp4_linear, mxfp4_gemm
+    return fp4, mxfp4_gemm, dual_gemm, fp4_linear
+
+
+def quantized_operand(oracle, x: np.ndarray):
+    codes, scale = oracle.quantize_mxfp4(x)
+    return oracle.pack_fp4(codes), oracle.scale_to_e8m0(scale), scale
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_integer_grid_is_bit_exact(dev, mods, oracle):
+    """bench.py:44-57: random codes, unit scales, K=128 -> C == (qa @ qb) / 4."""
+    fp4, mg, _, _ = mods
+    rng = np.random.default_rng(0)
+    pick = np.array([c for c in range(16) if c != 8], dtype=np.uint8)
+    ca = pick[rng.integers(0, 15, (256, 128))]
+    cb = pick[rng.integers(0, 15, (256, 128))]
+    ones_a = torch.ones((256, 4), device=dev)
+    got = mg.mxfp4_gemm_packed(_dev(oracle.pack_fp4(ca), dev), _dev(oracle.pack_fp4(cb), dev),
+                               ones_a, ones_a.clone(), out_dtype=torch.float32).cpu().numpy()
+    qa, qb = oracle.E2M1_Q[ca].astype(np.float64), oracle.E2M1_Q[cb].astype(np.float64)
+    assert np.array_equal(got.astype(np.float64), (qa @ qb.T) / 4.0)
+
+
+def test_random_codes_and_scales(dev, mods, oracle):
+    """cuda/mxfp4_mma_gemm.cu:204-252: codes 0..15 (incl. -0), scales 2^[-3,3]."""
+    fp4, mg, _, _ = mods
+    rng = np.random.default_rng(1234)
+    M = N = K = 256
+    ca = rng.integers(0, 16, (M, K), dtype=np.uint8)
+    cb = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    ea = (127 + rng.integers(-3, 4, (M, K // 32))).astype(np.uint8)
+    eb = (127 + rng.integers(-3, 4, (N, K // 32))).astype(np.uint8)
+    ref = oracle.reference_gemm_packed(oracle.pack_fp4(ca), ea, oracle.pack_fp4(cb), eb)
+    got = mg.mxfp4_gemm_packed(_dev(oracle.pack_fp4(ca), dev), _dev(oracle.pack_fp4(cb), dev),
+                               _dev(ea, dev), _dev(eb, dev), out_dtype=torch.float32).cpu().numpy()
+    assert oracle.max_rel(got, ref) <= 1e-6
+    # each 32-block partial is exact, so only fp32 accumulation rounds
+    el = np.abs(got - ref) / (np.abs(ref) + 1e-9)
+    assert np.median(el) < 1e-7
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (1, 1, 128), (37, 129, 384), (300, 513, 128),
+                                   (512, 256, 1024)])
+def test_quantized_randn_matches_fp64(dev, mods, oracle, out_dtype, M, N, K):
+    """bench.py:60-81 at small shapes, ragged M and N included."""
+    fp4, mg, _, _ = mods
+    a = gen.normal(M * 7 + K, (M, K))
+    bt = gen.student_t3(N * 13 + K, (N, K), scale=0.05)
+    apk, ae8, as32 = quantized_operand(oracle, a)
+    bpk, be8, bs32 = quantized_operand(oracle, bt)
+    ref = oracle.reference_gemm_packed(apk, ae8, bpk, be8)
+    for sa, sb in ((ae8, be8), (as32, bs32)):      # E8M0 bytes and fp32 scales
+        got = mg.mxfp4_gemm_packed(_dev(apk, dev), _dev(bpk, dev), _dev(sa, dev), _dev(sb, dev),
+                                   out_dtype=out_dtype)
+        assert got.dtype == out_dtype and got.shape == (M, N)
+        assert oracle.max_rel(got.float().cpu().numpy(), ref) <= TOL[out_dtype]
+
+
+def test_gpu_quantized_operands_end_to_end(dev, mods, oracle):
+    """Quantize on the GPU, multiply on the GPU, compare with the oracle chain."""
+    fp4, mg, _, _ = mods
+    a = torch.randn(512, 2048, device=dev)
+    b = torch.randn(384, 2048, device=dev) * 0.02
+    apk, ae8 = fp4.quantize_pack_mxfp4(a)
+    bpk, be8 = fp4.quantize_pack_mxfp4(b)
+    c = mg.mxfp4_gemm_packed(apk, bpk, ae8, be8, out_dtype=torch.float32)
+    ref = oracle.reference_gemm_packed(*[t.cpu().numpy() for t in (apk, ae8, bpk, be8)])
+    assert oracle.max_rel(c.cpu().numpy(), ref) <= 1e-5
+    # the reference API spelling: fp32 scales from quantize_mxfp4 + pack_fp4
+    ac, as_ = fp4.quantize_mxfp4(a)
+    bc, bs_ = fp4.quantize_mxfp4(b)
+    c2 = mg.mxfp4_gemm_packed(fp4.pack_fp4(ac), fp4.pack_fp4(bc), as_, bs_, out_dtype=torch.float32)
+    assert torch.equal(c, c2)
+
+
+def test_full_size_8192_cubed_sampled(dev, mods, oracle):
+    """BASELINE cfg4 at full size: A, B = 0.05 * t3 [8192, 8192], quantized on
+    the fly, f4 x f4, bf16 out; sampled rows/columns vs fp64 (the sampling of
+    cuda/mxfp4_mma_gemm.cu:235-236)."""
+    fp4, mg, _, _ = mods
+    n = 8192
+    g = torch.Generator(device=dev).manual_seed(4001)
+
+    def t3():
+        z = torch.randn((n, n), device=dev, generator=g)
+        chi = torch.zeros_like(z)
+        for _ in range(3):
+            chi += torch.randn((n, n), device=dev, generator=g).square()
+        return z / torch.sqrt(chi / 3.0) * 0.05
+
+    a, b = t3(), t3()
+    apk, ae8 = fp4.quantize_pack_mxfp4(a)
+    bpk, be8 = fp4.quantize_pack_mxfp4(b)
+    del a, b
+    c = mg.mxfp4_gemm_packed(apk, bpk, ae8, be8, out_dtype=torch.bfloat16)
+    rows = np.arange(0, n, 37)
+    cols = np.arange(0, n, 41)
+    ref = oracle.reference_gemm_packed(apk.cpu().numpy(), ae8.cpu().numpy(), bpk.cpu().numpy(),
+                                       be8.cpu().numpy(), rows=rows, cols=cols)
+    got = c.float().cpu().numpy()[np.ix_(rows, cols)]
+    assert oracle.max_rel(got, ref) <= 1e-2
+    c32 = mg.mxfp4_gemm_packed(apk, bpk, ae8, be8, out_dtype=torch.float32)
+    assert oracle.max_rel(c32.cpu().numpy()[np.ix_(rows, cols)], ref) <= 1e-5
+    # bf16 output is the RNE rounding of the fp32 result
+    assert torch.equal(c, c32.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (16, 300, 512), (100, 512, 128), (256, 256, 1024),
+                                   (513, 1024, 256)])
+def test_weight_only_bf16_x_fp4(dev, mods, oracle, out_dtype, M, N, K):
+    fp4, mg, _, _ = mods
+    a = gen.to_bf16_bits(gen.normal(M + 5 * K, (M, K)))
+    w = gen.normal(N + 3 * K, (N, K), std=0.02)
+    wpk, we8, ws32 = quantized_operand(oracle, w)
+    ref = oracle.reference_gemm_wonly(gen.bf16_bits_to_f32(a), wpk, we8)
+    at = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).to(dev)
+    for s in (we8, ws32):
+        got = mg.mxfp4_gemm_bf16(at, _dev(wpk, dev), _dev(s, dev), out_dtype=out_dtype)
+        assert oracle.max_rel(got.float().cpu().numpy(), ref) <= TOL[out_dtype]
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (100, 300, 256), (1, 256, 128)])
+def test_dual_batch_matches_single_and_oracle(dev, mods, oracle, M, N, K):
+    """cfg2 (and ragged shapes): two bf16 batches share one MXFP4 weight."""
+    fp4, mg, dg, _ = mods
+    g = torch.Generator(device=dev).manual_seed(2001)
+    a0 = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    a1 = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    c0, c1 = dg.dual_mxfp4(a0, a1, wpk, we8, out_dtype=torch.float32)
+    s0 = mg.mxfp4_gemm_bf16(a0, wpk, we8, out_dtype=torch.float32)
+    s1 = mg.mxfp4_gemm_bf16(a1, wpk, we8, out_dtype=torch.float32)
+    assert torch.equal(c0, s0) and torch.equal(c1, s1)      # same order of summation
+    rows = np.arange(0, M, max(1, M // 64))
+    for a, c in ((a0, c0), (a1, c1)):
+        ref = oracle.reference_gemm_wonly(a.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy(),
+                                          rows=rows)
+        assert oracle.max_rel(c.cpu().numpy()[rows], ref) <= 1e-5
+    b0, b1 = dg.dual_mxfp4(a0, a1, wpk, we8)
+    assert torch.equal(b0, c0.to(torch.bfloat16)) and torch.equal(b1, c1.to(torch.bfloat16))
+
+
+def test_fp4_linear_forward_backward(dev, mods, oracle):
+    """fp4_linear.py:34-45: MXFP4 forward (X and W quantized), STE backward."""
+    fp4, mg, _, fl = mods
+    assert fl.path() == "hip-mxfp4"
+    torch.manual_seed(0)
+    layer = fl.MXFP4Linear(1024, 512).to(dev)
+    x = torch.randn(4, 64, 1024, device=dev, requires_grad=True)
+    y = layer(x)
+    assert y.shape == (4, 64, 512) and y.dtype == torch.float32
+    xq = oracle.quantize_pack(x.detach().reshape(-1, 1024).cpu().numpy())
+    wq = oracle.quantize_pack(layer.weight.detach().cpu().numpy())
+    ref = oracle.reference_gemm_packed(xq[0], xq[1], wq[0], wq[1])
+    assert oracle.max_rel(y.detach().reshape(-1, 512).cpu().numpy(), ref) <= 1e-5
+    gy = torch.randn_like(y)
+    y.backward(gy)
+    gx = gy.reshape(-1, 512) @ layer.weight
+    gw = gy.reshape(-1, 512).t() @ x.detach().reshape(-1, 1024)
+    assert torch.allclose(x.grad.reshape(-1, 1024), gx) and torch.allclose(layer.weight.grad, gw)
+    yb = layer(x.detach().to(torch.bfloat16))
+    assert yb.dtype == torch.bfloat16
+    assert oracle.max_rel(yb.float().reshape(-1, 512).cpu().numpy(),
+                          oracle.reference_gemm_packed(*oracle.quantize_pack(
+                              gen.to_bf16_bits(x.detach().reshape(-1, 1024).cpu().numpy()), "bf16"),
+                              wq[0], wq[1])) <= 1e-2

@@ -1,0 +1,199 @@
+"""GPU parity of the quantize / pack / unpack / dequantize / E4M3 kernels.
+
+Bar: bit-exact.  Each kernel result is compared byte for byte with the CPU
+oracle on the same input, and the quantizer also against the digests the
+reference fp4.py produced (tests/golden/).
+"""
+
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gen
+
+pytestmark = pytest.mark.gpu
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def to_dev(x: np.ndarray, dtype: str, dev):
+    if dtype == "bf16":
+        return torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16).to(dev)
+    if dtype == "f16":
+        return torch.from_numpy(x.view(np.int16).copy()).view(torch.float16).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+@pytest.fixture(scope="module")
+def fp4mod(dev):
+    from lockstep_amd import fp4
+    return fp4
+
+
+def test_quantize_matches_reference_golden(dev, fp4mod):
+    """GPU codes/scales digest-equal to the reference fp4.py's on the golden inputs."""
+    from .test_oracle import golden_inputs
+    cases = json.loads((GOLD / "fp4_golden.json").read_text())["cases"]
+    for name, x in golden_inputs().items():
+        c = cases[name]
+        xt = to_dev(x, c["dtype"], dev)
+        codes, scale = fp4mod.quantize_mxfp4(xt, c["block"])
+        codes, scale = codes.cpu().numpy(), scale.cpu().numpy()
+        assert sha(codes) == c["codes_sha256"], name
+        assert sha(scale.view(np.uint32)) == c["scale_sha256"], name
+
+
+def test_round_all_bf16_patterns_matches_reference(dev, fp4mod):
+    arrays = np.load(GOLD / "fp4_golden.npz")
+    allbf = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    got = fp4mod._round_to_e2m1(torch.from_numpy(allbf.copy()).to(dev)).cpu().numpy()
+    assert np.array_equal(got, arrays["round_all_bf16__codes"])
+    got16 = fp4mod._round_to_e2m1(torch.from_numpy(allbf.copy()).to(dev).to(torch.bfloat16)).cpu().numpy()
+    assert np.array_equal(got16, arrays["round_all_bf16__codes"])
+
+
+SHAPES = [(1, 32), (3, 96), (7, 1056), (64, 4096), (257, 512), (1000, 64)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("block", [32, 16])
+def test_quantize_packed_e8m0_matches_oracle(dev, fp4mod, oracle, dtype, block):
+    for i, (rows, K) in enumerate(SHAPES):
+        if K % block:
+            continue
+        x = gen.student_t3(100 + i, (rows, K), scale=0.05)
+        if dtype == "bf16":
+            xh = gen.to_bf16_bits(x)
+            ref_codes, ref_scale = oracle.quantize_mxfp4(xh, block, "bf16")
+        elif dtype == "f16":
+            xh = x.astype(np.float16).view(np.uint16)
+            ref_codes, ref_scale = oracle.quantize_mxfp4(xh, block, "f16")
+        else:
+            xh = x
+            ref_codes, ref_scale = oracle.quantize_mxfp4(x, block)
+        xt = to_dev(xh, dtype, dev)
+        packed, e8 = fp4mod.quantize_pack_mxfp4(xt, block)
+        assert np.array_equal(packed.cpu().numpy(), oracle.pack_fp4(ref_codes)), (rows, K)
+        assert np.array_equal(e8.cpu().numpy(), oracle.scale_to_e8m0(ref_scale)), (rows, K)
+        codes, scale = fp4mod.quantize_mxfp4(xt, block)
+        assert np.array_equal(codes.cpu().numpy(), ref_codes), (rows, K)
+        assert np.array_equal(scale.cpu().numpy().view(np.uint32), ref_scale.view(np.uint32))
+
+
+def test_quantize_strided_rows_and_leading_dims(dev, fp4mod, oracle):
+    x = gen.normal(31, (2, 5, 8, 256))
+    codes, scale = fp4mod.quantize_mxfp4(to_dev(x, "f32", dev))
+    rc, rs = oracle.quantize_mxfp4(x)
+    assert codes.shape == (2, 5, 8, 256) and scale.shape == (2, 5, 8, 8)
+    assert np.array_equal(codes.cpu().numpy(), rc)
+    big = torch.from_numpy(gen.normal(32, (64, 1024))).to(dev)
+    view = big[:, 256:768]                                   # row stride 1024, offset 1 KiB
+    pk, e8 = fp4mod.quantize_pack_mxfp4(view)
+    rc, rs = oracle.quantize_mxfp4(view.cpu().numpy())
+    assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(rc))
+    assert np.array_equal(e8.cpu().numpy(), oracle.scale_to_e8m0(rs))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("block", [32, 16])
+def test_quantize_transposed_axis_matches_oracle(dev, fp4mod, oracle, dtype, block):
+    for (K, N) in [(32, 1), (64, 300), (1024, 96), (4096, 257)]:
+        if K % block:
+            continue
+        x = gen.normal(41 + K, (K, N), std=0.02)
+        if dtype == "bf16":
+            xh = gen.to_bf16_bits(x)
+            rc, rs = oracle.quantize_mxfp4(np.ascontiguousarray(xh.T), block, "bf16")
+        else:
+            xh = x
+            rc, rs = oracle.quantize_mxfp4(np.ascontiguousarray(x.T), block)
+        xt = to_dev(xh, dtype, dev)
+        pk, e8 = fp4mod.quantize_mxfp4_t(xt, block)
+        assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(rc)), (K, N)
+        assert np.array_equal(e8.cpu().numpy(), oracle.scale_to_e8m0(rs)), (K, N)
+        codes, scale = fp4mod.quantize_mxfp4_t(xt, block, packed=False, e8m0=False)
+        assert np.array_equal(codes.cpu().numpy(), rc)
+        assert np.array_equal(scale.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+
+
+def test_quantize_full_size_cfg4_operand(dev, fp4mod, oracle):
+    """BASELINE cfg4 operand at full size: A [8192, 8192] = 0.05 * t3, fp32."""
+    g = torch.Generator(device=dev).manual_seed(4001)
+    z = torch.randn((8192, 8192), device=dev, generator=g)
+    chi = torch.randn((3, 8192, 8192), device=dev, generator=g).square().sum(0)
+    x = (z / torch.sqrt(chi / 3.0) * 0.05).contiguous()
+    del chi
+    pk, e8 = fp4mod.quantize_pack_mxfp4(x)
+    xc = x.cpu().numpy()
+    rc, rs = oracle.quantize_mxfp4(xc)
+    assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(rc))
+    assert np.array_equal(e8.cpu().numpy(), oracle.scale_to_e8m0(rs))
+    # idempotence: quantizing the dequantized tensor reproduces the same bytes
+    deq = fp4mod.dequantize_packed(pk, e8)
+    pk2, e82 = fp4mod.quantize_pack_mxfp4(deq)
+    nz = (e8 != 127)
+    assert torch.equal(pk2, pk)
+    assert torch.equal(e82[nz], e8[nz])
+
+
+def test_specials_nan_inf_negzero(dev, fp4mod):
+    from .test_oracle import golden_inputs
+    arrays = np.load(GOLD / "fp4_golden.npz")
+    x = golden_inputs()["special"]
+    codes, scale = fp4mod.quantize_mxfp4(to_dev(x, "f32", dev))
+    assert np.array_equal(codes.cpu().numpy(), arrays["special__codes"])
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), arrays["special__scale"].view(np.uint32))
+    pk, e8 = fp4mod.quantize_pack_mxfp4(to_dev(x, "f32", dev))
+    assert int(e8[0, 0]) == 255 and int(e8[2, 0]) == 254 and int(e8[5, 0]) == 127
+
+
+def test_pack_unpack_match_oracle(dev, fp4mod, oracle):
+    rng = np.random.default_rng(7)
+    for n in [2, 14, 16, 18, 1000, 4096 * 33 + 6]:
+        codes = rng.integers(0, 16, (n,), dtype=np.uint8)
+        pk = fp4mod.pack_fp4(torch.from_numpy(codes).to(dev))
+        assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(codes)), n
+        back = fp4mod.unpack_fp4(pk)
+        assert np.array_equal(back.cpu().numpy(), codes), n
+    allb = torch.arange(256, dtype=torch.uint8, device=dev)
+    assert np.array_equal(fp4mod.unpack_fp4(allb).cpu().numpy(), oracle.unpack_fp4(np.arange(256, dtype=np.uint8)))
+
+
+@pytest.mark.parametrize("block", [32, 16])
+def test_dequantize_matches_oracle(dev, fp4mod, oracle, block):
+    x = gen.student_t3(77, (96, 512), scale=0.05)
+    rc, rs = oracle.quantize_mxfp4(x, block)
+    want = oracle.dequantize_mxfp4(rc, rs, block)
+    got = fp4mod.dequantize_mxfp4(torch.from_numpy(rc).to(dev), torch.from_numpy(rs).to(dev), block)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    e8 = torch.from_numpy(oracle.scale_to_e8m0(rs)).to(dev)
+    pk = torch.from_numpy(oracle.pack_fp4(rc)).to(dev)
+    got_bf = fp4mod.dequantize_packed(pk, e8, block, out_dtype=torch.bfloat16)
+    assert torch.equal(got_bf.float().cpu(), torch.from_numpy(want))   # exact in bf16
+
+
+def test_e4m3_expansion_exhaustive(dev, fp4mod, oracle):
+    words = np.arange(1 << 16, dtype=np.uint32) * np.uint32(0x10001) ^ np.uint32(0x9E3779B9)
+    words = np.concatenate([words, np.arange(1 << 16, dtype=np.uint32)])
+    got = fp4mod.fp4_to_e4m3_words(torch.from_numpy(words.view(np.int32)).to(dev)).cpu().numpy().view(np.uint32)
+    lo, hi = oracle.fp4x8_to_e4m3x8(words)
+    assert np.array_equal(got[0::2], lo) and np.array_equal(got[1::2], hi)
+    codes = torch.arange(16, dtype=torch.uint8, device=dev)
+    e4 = fp4mod.codes_to_e4m3(codes)
+    assert e4.dtype == torch.float8_e4m3fn
+    assert torch.equal(e4.float().cpu(), fp4mod.E2M1_VALUES)
+
+
+def test_repeat_runs_are_bitwise_identical(dev, fp4mod):
+    x = torch.randn(512, 4096, device=dev)
+    a = fp4mod.quantize_pack_mxfp4(x)
+    b = fp4mod.quantize_pack_mxfp4(x)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
