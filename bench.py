@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--size", type=int, default=8192)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--suite", default=None, help="also bench cfg2/cfg3, one JSON line each to this file")
+    p.add_argument("--calib", action="store_true",
+                   help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
     return p.parse_args()
 
 
@@ -132,10 +134,10 @@ def main():
     def step(ev=None):
         if ev:
             ev[0].record()
-        apk, ae8 = fp4.quantize_pack_mxfp4(A)
+        apk, ae8 = fp4.quantize_pack_mxfp4(A, scale_layout="kmajor")
         if ev:
             ev[1].record()
-        bpk, be8 = fp4.quantize_pack_mxfp4(B)
+        bpk, be8 = fp4.quantize_pack_mxfp4(B, scale_layout="kmajor")
         if ev:
             ev[2].record()
         c = mxfp4_gemm.mxfp4_gemm_packed(apk, bpk, ae8, be8, out_dtype=torch.bfloat16)
@@ -204,6 +206,14 @@ def main():
     }
     if args.suite:
         run_suite(args.suite, torch, dev)
+    if args.calib:
+        # plain copy of known size: 256 MiB read + 256 MiB written per launch
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["calib_copy_bytes"] = src.numel() * 4
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(n)
     print(json.dumps(out), flush=True)

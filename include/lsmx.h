@@ -49,6 +49,11 @@ extern "C" {
 /* scale formats */
 #define LSMX_SCALE_E8M0 0  /* one byte per block: biased exponent, 0xFF = NaN        */
 #define LSMX_SCALE_F32 1   /* one fp32 per block holding the power of two (fp4.py)   */
+/* E8M0 bytes grouped by 128-element K slices: byte (kb/4, row, kb%4) of a
+ * [K/128][ld_scale][4] array, ld_scale >= rows.  The GEMMs read the four
+ * scales of one K slice for consecutive rows as one contiguous run.  Same
+ * byte count as LSMX_SCALE_E8M0; requires K % 128 == 0. */
+#define LSMX_SCALE_E8M0_KMAJOR 2
 
 /* Library version string, e.g. "lsmx 0.1.0 gfx950". */
 const char *lsmx_version(void);

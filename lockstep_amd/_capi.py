@@ -19,7 +19,7 @@ OK = 0
 ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_DEVICE, ERR_LAUNCH, ERR_ARG = -1, -2, -3, -4, -5, -6
 F32, BF16, F16 = 0, 1, 2
 CODES_PACKED, CODES_UNPACKED = 0, 1
-SCALE_E8M0, SCALE_F32 = 0, 1
+SCALE_E8M0, SCALE_F32, SCALE_E8M0_KMAJOR = 0, 1, 2
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int

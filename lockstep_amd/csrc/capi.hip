@@ -72,16 +72,19 @@ static int quantize_common(const void *x, int x_dtype, int64_t rows, int64_t K, 
         return fail(LSMX_ERR_DTYPE, "%s: x_dtype %d unsupported", fn, x_dtype);
     if (codes_fmt != LSMX_CODES_PACKED && codes_fmt != LSMX_CODES_UNPACKED)
         return fail(LSMX_ERR_DTYPE, "%s: codes_fmt %d unsupported", fn, codes_fmt);
-    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32)
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32 && scale_fmt != LSMX_SCALE_E8M0_KMAJOR)
         return fail(LSMX_ERR_DTYPE, "%s: scale_fmt %d unsupported", fn, scale_fmt);
     if (block != 32 && block != 16) return fail(LSMX_ERR_SHAPE, "%s: block must be 16 or 32, got %d", fn, block);
+    if (scale_fmt == LSMX_SCALE_E8M0_KMAJOR && (block != 32 || K % 128 != 0))
+        return fail(LSMX_ERR_SHAPE, "%s: K-major E8M0 scales need block 32 and K %% 128 == 0", fn);
     if (rows < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
     if (K % block != 0) return fail(LSMX_ERR_SHAPE, "K=%lld must be a multiple of block=%d", (long long)K, block);
     const int64_t lead = cols ? rows : K;  // the contiguous extent of x
     if (ldx < lead) return fail(LSMX_ERR_SHAPE, "%s: ldx %lld < %lld", fn, (long long)ldx, (long long)lead);
     const int64_t code_w = codes_fmt == LSMX_CODES_PACKED ? K / 2 : K;
     if (ld_codes < code_w) return fail(LSMX_ERR_SHAPE, "%s: ld_codes %lld < %lld", fn, (long long)ld_codes, (long long)code_w);
-    if (ld_scale < K / block) return fail(LSMX_ERR_SHAPE, "%s: ld_scale too small", fn);
+    if (scale_fmt == LSMX_SCALE_E8M0_KMAJOR ? ld_scale < rows : ld_scale < K / block)
+        return fail(LSMX_ERR_SHAPE, "%s: ld_scale too small", fn);
     const int es = elem_size(x_dtype);
     if (!cols) {
         // each lane reads 16 B of a row and writes 2..8 B of codes
@@ -174,7 +177,16 @@ int lsmx_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n_words, void *s
     return launched(lsmx::launch_fp4_to_e4m3(in, out, n_words, (hipStream_t)stream), "lsmx_fp4_to_e4m3");
 }
 
-static int check_scale(const char *fn, const void *s, int64_t ld, int fmt, int per_stage) {
+static int check_scale(const char *fn, const void *s, int64_t ld, int fmt, int per_stage, int64_t rows,
+                       int64_t K) {
+    if (fmt == LSMX_SCALE_E8M0_KMAJOR) {
+        // [K/128][ld][4]: one dword per row per 128-K slice
+        if (!aligned(s, 4)) return fail(LSMX_ERR_ALIGN, "%s: K-major scales must be 4-byte aligned", fn);
+        if (ld < rows) return fail(LSMX_ERR_SHAPE, "%s: K-major scale row stride %lld < %lld", fn, (long long)ld, (long long)rows);
+        if (K % 128) return fail(LSMX_ERR_SHAPE, "%s: K-major scales need K %% 128 == 0", fn);
+        return LSMX_OK;
+    }
+    if (ld < K / 32) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
     // the GEMMs read `per_stage` consecutive scales with one aligned load
     const int bytes = per_stage * (fmt == LSMX_SCALE_F32 ? 4 : 1);
     if (!aligned(s, bytes) || (ld * (fmt == LSMX_SCALE_F32 ? 4 : 1)) % bytes)
@@ -187,17 +199,17 @@ int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_
                    int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
     const char *fn = "lsmx_gemm_f4f4";
     if (!a_pk || !a_scale || !bt_pk || !b_scale || !c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
-    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32) return fail(LSMX_ERR_DTYPE, "%s: scale_fmt", fn);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32 && scale_fmt != LSMX_SCALE_E8M0_KMAJOR)
+        return fail(LSMX_ERR_DTYPE, "%s: scale_fmt", fn);
     if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
     if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
     if (K % 128 != 0) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
     if (M > (int64_t)1 << 30 || N > (int64_t)1 << 30) return fail(LSMX_ERR_SHAPE, "%s: M, N must be < 2^30", fn);
-    if (lda < K / 2 || ldb < K / 2 || ldc < N || ld_sa < K / 32 || ld_sb < K / 32)
-        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (lda < K / 2 || ldb < K / 2 || ldc < N) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
     if (!aligned(a_pk, 16) || !aligned(bt_pk, 16) || lda % 16 || ldb % 16)
         return fail(LSMX_ERR_ALIGN, "%s: packed rows must be 16-byte aligned", fn);
-    if (int r = check_scale(fn, a_scale, ld_sa, scale_fmt, 4)) return r;
-    if (int r = check_scale(fn, b_scale, ld_sb, scale_fmt, 4)) return r;
+    if (int r = check_scale(fn, a_scale, ld_sa, scale_fmt, 4, M, K)) return r;
+    if (int r = check_scale(fn, b_scale, ld_sb, scale_fmt, 4, N, K)) return r;
     if (!aligned(c, c_dtype == LSMX_F32 ? 4 : 2)) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
     if (int r = device_guard()) return r;
     if (M == 0 || N == 0) return LSMX_OK;
@@ -216,11 +228,12 @@ static int w4_common(const char *fn, const void *a0, const void *a1, int64_t lda
     if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
     if (K % 128 != 0) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
     if (M > (int64_t)1 << 30 || N > (int64_t)1 << 30) return fail(LSMX_ERR_SHAPE, "%s: M, N must be < 2^30", fn);
-    if (lda < K || ldw < K / 2 || ldc < N || ld_sw < K / 32) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (lda < K || ldw < K / 2 || ldc < N) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
     if (!aligned(a0, 16) || (a1 && !aligned(a1, 16)) || (lda * 2) % 16)
         return fail(LSMX_ERR_ALIGN, "%s: activation rows must be 16-byte aligned", fn);
     if (!aligned(w_pk, 16) || ldw % 16) return fail(LSMX_ERR_ALIGN, "%s: packed weight rows must be 16-byte aligned", fn);
-    if (int r = check_scale(fn, w_scale, ld_sw, scale_fmt, 2)) return r;
+    if (scale_fmt == LSMX_SCALE_E8M0_KMAJOR) return fail(LSMX_ERR_DTYPE, "%s: K-major scales are not supported here", fn);
+    if (int r = check_scale(fn, w_scale, ld_sw, scale_fmt, 2, N, K)) return r;
     const int cb = c_dtype == LSMX_F32 ? 4 : 2;
     if (!aligned(c0, cb) || (c1 && !aligned(c1, cb))) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
     if (int r = device_guard()) return r;

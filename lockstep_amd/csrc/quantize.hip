@@ -102,7 +102,18 @@ struct CodeStore<8> {
 constexpr int kQThreads = 256;
 constexpr int kQUnroll = 4;
 
-template <typename T, int BLOCK, bool PACKED, bool SCALE_F32>
+// Scale store for block kb of row r in format SFMT (LSMX_SCALE_*).
+template <int SFMT>
+LSMX_DEV void store_scale(void *scale, int64_t r, int64_t kb, int64_t ld_scale, uint32_t e8) {
+    if constexpr (SFMT == LSMX_SCALE_F32)
+        reinterpret_cast<float *>(scale)[r * ld_scale + kb] = e8m0_to_f32(e8);
+    else if constexpr (SFMT == LSMX_SCALE_E8M0)
+        reinterpret_cast<uint8_t *>(scale)[r * ld_scale + kb] = (uint8_t)e8;
+    else  // K-major: [K/128][ld_scale rows][4]
+        reinterpret_cast<uint8_t *>(scale)[((kb >> 2) * ld_scale + r) * 4 + (kb & 3)] = (uint8_t)e8;
+}
+
+template <typename T, int BLOCK, bool PACKED, int SFMT>
 __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
     const T *__restrict__ x, int64_t rows, int64_t K, int64_t ldx, uint8_t *__restrict__ codes,
     int64_t ld_codes, void *__restrict__ scale, int64_t ld_scale) {
@@ -141,13 +152,7 @@ __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
             const int64_t col = v * E;
             if constexpr (PACKED) CodeStore<E>::packed(codes + r * ld_codes + col / 2, c);
             else CodeStore<E>::unpacked(codes + r * ld_codes + col, c);
-            if ((threadIdx.x % G) == 0) {
-                const int64_t kb = col / BLOCK;
-                if constexpr (SCALE_F32)
-                    reinterpret_cast<float *>(scale)[r * ld_scale + kb] = e8m0_to_f32(e8);
-                else
-                    reinterpret_cast<uint8_t *>(scale)[r * ld_scale + kb] = (uint8_t)e8;
-            }
+            if ((threadIdx.x % G) == 0) store_scale<SFMT>(scale, r, col / BLOCK, ld_scale, e8);
         }
     }
 }
@@ -158,7 +163,7 @@ __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
 // load instruction of a wave reads 64 consecutive elements of one row.
 constexpr int kTThreads = 256;
 
-template <typename T, int BLOCK, bool PACKED, bool SCALE_F32>
+template <typename T, int BLOCK, bool PACKED, int SFMT>
 __global__ __launch_bounds__(kTThreads) void quantize_cols_kernel(
     const T *__restrict__ x, int64_t K, int64_t cols, int64_t ldx, uint8_t *__restrict__ codes,
     int64_t ld_codes, void *__restrict__ scale, int64_t ld_scale) {
@@ -211,10 +216,7 @@ __global__ __launch_bounds__(kTThreads) void quantize_cols_kernel(
                 *reinterpret_cast<uint4 *>(out + kb * BLOCK + 16 * j) = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
-        if constexpr (SCALE_F32)
-            reinterpret_cast<float *>(scale)[c * ld_scale + kb] = e8m0_to_f32(e8);
-        else
-            reinterpret_cast<uint8_t *>(scale)[c * ld_scale + kb] = (uint8_t)e8;
+        store_scale<SFMT>(scale, c, kb, ld_scale, e8);
     }
 }
 
@@ -339,7 +341,7 @@ __global__ void dequant_kernel(const uint8_t *__restrict__ codes, int64_t ld_cod
 }
 
 // ---------------------------------------------------------------- launchers
-template <typename T, int BLOCK, bool PACKED, bool SF32>
+template <typename T, int BLOCK, bool PACKED, int SF32>
 static hipError_t launch_rows(const QuantArgs &a, hipStream_t s) {
     constexpr int E = Elem<T>::kPerVec;
     const int64_t vpr = a.K / E;
@@ -351,7 +353,7 @@ static hipError_t launch_rows(const QuantArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <typename T, int BLOCK, bool PACKED, bool SF32>
+template <typename T, int BLOCK, bool PACKED, int SF32>
 static hipError_t launch_cols(const QuantArgs &a, hipStream_t s) {
     // a.rows = cols, a.K = K for the column mode
     const int64_t gx = (a.rows + kTThreads - 1) / kTThreads;
@@ -365,12 +367,18 @@ static hipError_t launch_cols(const QuantArgs &a, hipStream_t s) {
 
 template <typename T, int BLOCK>
 static hipError_t dispatch_fmt(const QuantArgs &a, bool cols, hipStream_t s) {
-    const bool packed = a.codes_fmt == LSMX_CODES_PACKED, f32 = a.scale_fmt == LSMX_SCALE_F32;
+    const bool packed = a.codes_fmt == LSMX_CODES_PACKED;
 #define LSMX_Q(P, F) return cols ? launch_cols<T, BLOCK, P, F>(a, s) : launch_rows<T, BLOCK, P, F>(a, s)
-    if (packed && f32) LSMX_Q(true, true);
-    if (packed) LSMX_Q(true, false);
-    if (f32) LSMX_Q(false, true);
-    LSMX_Q(false, false);
+    if (a.scale_fmt == LSMX_SCALE_F32) {
+        if (packed) LSMX_Q(true, LSMX_SCALE_F32);
+        LSMX_Q(false, LSMX_SCALE_F32);
+    }
+    if (a.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) {
+        if (packed) LSMX_Q(true, LSMX_SCALE_E8M0_KMAJOR);
+        LSMX_Q(false, LSMX_SCALE_E8M0_KMAJOR);
+    }
+    if (packed) LSMX_Q(true, LSMX_SCALE_E8M0);
+    LSMX_Q(false, LSMX_SCALE_E8M0);
 #undef LSMX_Q
 }
 

@@ -100,11 +100,14 @@ def quantize_mxfp4(x: torch.Tensor, block: int = 32):
     return codes.reshape(*lead, K), scale.reshape(*lead, K // block)
 
 
-def quantize_pack_mxfp4(x: torch.Tensor, block: int = 32):
+def quantize_pack_mxfp4(x: torch.Tensor, block: int = 32, scale_layout: str = "rows"):
     """Fused quantize_mxfp4 + pack_fp4 with E8M0 byte scales.
 
-    Returns (packed uint8 [..., K//2], e8m0 uint8 [..., K//block]); the bytes
-    equal pack_fp4(codes) and the exponent fields of quantize_mxfp4's scales."""
+    Returns (packed uint8 [..., K//2], e8m0 uint8); the bytes equal
+    pack_fp4(codes) and the exponent fields of quantize_mxfp4's scales.
+    scale_layout "rows": e8m0 is [..., K//block] (row-major, like fp4.py's
+    scales).  "kmajor" (2-D x, block 32, K % 128 == 0): e8m0 is
+    [K//128, rows, 4], the layout the f4 x f4 GEMM streams fastest."""
     *lead, K = x.shape
     assert K % block == 0, f"K={K} must be a multiple of block={block}"
     C.require_device(x)
@@ -112,11 +115,28 @@ def quantize_pack_mxfp4(x: torch.Tensor, block: int = 32):
     x2, lead = _as_rows(x)
     rows = x2.shape[0]
     packed = torch.empty((rows, K // 2), dtype=torch.uint8, device=x.device)
-    e8m0 = torch.empty((rows, K // block), dtype=torch.uint8, device=x.device)
+    if scale_layout == "kmajor":
+        assert block == 32 and K % 128 == 0, "K-major scales need block 32 and K % 128 == 0"
+        e8m0 = torch.empty((K // 128, rows, 4), dtype=torch.uint8, device=x.device)
+        fmt, ld = C.SCALE_E8M0_KMAJOR, rows
+    elif scale_layout == "rows":
+        e8m0 = torch.empty((rows, K // block), dtype=torch.uint8, device=x.device)
+        fmt, ld = C.SCALE_E8M0, K // block
+    else:
+        raise ValueError(f"scale_layout must be 'rows' or 'kmajor', got {scale_layout!r}")
     C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
            x2.stride(0) if rows > 1 else K, block, packed.data_ptr(), C.CODES_PACKED, K // 2,
-           e8m0.data_ptr(), C.SCALE_E8M0, K // block, C.stream_of(x2))
+           e8m0.data_ptr(), fmt, ld, C.stream_of(x2))
+    if scale_layout == "kmajor":
+        return packed.reshape(*lead, K // 2), e8m0
     return packed.reshape(*lead, K // 2), e8m0.reshape(*lead, K // block)
+
+
+def kmajor_scales(e8m0: torch.Tensor) -> torch.Tensor:
+    """Row-major E8M0 scales [rows, K//32] -> K-major [K//128, rows, 4] (a copy)."""
+    rows, nb = e8m0.shape
+    assert nb % 4 == 0, "K must be a multiple of 128"
+    return e8m0.reshape(rows, nb // 4, 4).transpose(0, 1).contiguous()
 
 
 def quantize_mxfp4_t(x: torch.Tensor, block: int = 32, packed: bool = True, e8m0: bool = True):

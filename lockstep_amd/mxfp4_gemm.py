@@ -45,25 +45,36 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
     """a_pk [M,K//2] uint8, bt_pk [N,K//2] uint8, a_scale [M,K//32], b_scale [N,K//32].
 
     Scales are fp32 powers of two (as fp4.quantize_mxfp4 returns) or E8M0
-    bytes (as fp4.quantize_pack_mxfp4 returns); both operands must use the
-    same format.  Returns C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
+    bytes (as fp4.quantize_pack_mxfp4 returns), row-major [rows, K//32] or
+    K-major [K//128, rows, 4] (quantize_pack_mxfp4(..., scale_layout="kmajor"),
+    the fastest form); both operands must use the same format.  Returns
+    C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
     M, Kh = a_pk.shape
     N, Kh2 = bt_pk.shape
     K = Kh * 2
     assert Kh == Kh2 and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
     C.require_device(a_pk, bt_pk, a_scale, b_scale)
-    assert a_scale.dtype == b_scale.dtype, "a_scale and b_scale must share a format"
+    assert a_scale.dtype == b_scale.dtype and a_scale.dim() == b_scale.dim(), \
+        "a_scale and b_scale must share a format"
     a_pk, bt_pk = _rows16(a_pk), _rows16(bt_pk)
-    a_scale = _scales(a_scale, M, K // 32)
-    b_scale = _scales(b_scale, N, K // 32)
     c = torch.empty((M, N), device=a_pk.device, dtype=out_dtype)
     if M == 0 or N == 0:
         return c
+    if a_scale.dim() == 3:
+        assert a_scale.dtype == torch.uint8, "K-major scales are E8M0 bytes"
+        assert a_scale.shape == (K // 128, M, 4) and b_scale.shape == (K // 128, N, 4), \
+            "K-major scales must be [K//128, rows, 4]"
+        a_scale, b_scale = a_scale.contiguous(), b_scale.contiguous()
+        fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
+    else:
+        a_scale = _scales(a_scale, M, K // 32)
+        b_scale = _scales(b_scale, N, K // 32)
+        fmt = _fp4._scale_fmt(a_scale)
+        lsa = a_scale.stride(0) if M > 1 else K // 32
+        lsb = b_scale.stride(0) if N > 1 else K // 32
     C.call("lsmx_gemm_f4f4", a_pk.data_ptr(), a_pk.stride(0) if M > 1 else Kh,
-           a_scale.data_ptr(), a_scale.stride(0) if M > 1 else K // 32,
-           bt_pk.data_ptr(), bt_pk.stride(0) if N > 1 else Kh,
-           b_scale.data_ptr(), b_scale.stride(0) if N > 1 else K // 32,
-           _fp4._scale_fmt(a_scale), c.data_ptr(), _out_code(out_dtype), N, M, N, K,
+           a_scale.data_ptr(), lsa, bt_pk.data_ptr(), bt_pk.stride(0) if N > 1 else Kh,
+           b_scale.data_ptr(), lsb, fmt, c.data_ptr(), _out_code(out_dtype), N, M, N, K,
            C.stream_of(c))
     return c
 

@@ -185,9 +185,28 @@ def test_fp4_linear_forward_backward(dev, mods, oracle):
     gx = gy.reshape(-1, 512) @ layer.weight
     gw = gy.reshape(-1, 512).t() @ x.detach().reshape(-1, 1024)
     assert torch.allclose(x.grad.reshape(-1, 1024), gx) and torch.allclose(layer.weight.grad, gw)
-    yb = layer(x.detach().to(torch.bfloat16))
+    with torch.no_grad():
+        yb = layer(x.detach().to(torch.bfloat16))
     assert yb.dtype == torch.bfloat16
     assert oracle.max_rel(yb.float().reshape(-1, 512).cpu().numpy(),
                           oracle.reference_gemm_packed(*oracle.quantize_pack(
                               gen.to_bf16_bits(x.detach().reshape(-1, 1024).cpu().numpy()), "bf16"),
                               wq[0], wq[1])) <= 1e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (37, 129, 384), (300, 513, 128), (1024, 768, 2048)])
+def test_kmajor_scales_give_identical_gemm(dev, mods, oracle, M, N, K):
+    """The K-major scale layout is a relayout only: same bits out."""
+    fp4, mg, _, _ = mods
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    a = torch.randn((M, K), device=dev, generator=g)
+    b = torch.randn((N, K), device=dev, generator=g) * 0.02
+    apk, ae8 = fp4.quantize_pack_mxfp4(a)
+    bpk, be8 = fp4.quantize_pack_mxfp4(b)
+    _, ak = fp4.quantize_pack_mxfp4(a, scale_layout="kmajor")
+    _, bk = fp4.quantize_pack_mxfp4(b, scale_layout="kmajor")
+    c_rows = mg.mxfp4_gemm_packed(apk, bpk, ae8, be8, out_dtype=torch.float32)
+    c_km = mg.mxfp4_gemm_packed(apk, bpk, ak, bk, out_dtype=torch.float32)
+    assert torch.equal(c_rows, c_km)
+    ref = oracle.reference_gemm_packed(*[t.cpu().numpy() for t in (apk, ae8, bpk, be8)])
+    assert oracle.max_rel(c_km.cpu().numpy(), ref) <= 1e-5

@@ -56,7 +56,9 @@ def test_round_all_bf16_patterns_matches_reference(dev, fp4mod):
     allbf = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
     got = fp4mod._round_to_e2m1(torch.from_numpy(allbf.copy()).to(dev)).cpu().numpy()
     assert np.array_equal(got, arrays["round_all_bf16__codes"])
-    got16 = fp4mod._round_to_e2m1(torch.from_numpy(allbf.copy()).to(dev).to(torch.bfloat16)).cpu().numpy()
+    # bf16 bit patterns built directly (a float32 -> bf16 cast would canonicalize NaNs)
+    bits = torch.from_numpy(np.arange(65536, dtype=np.uint16).view(np.int16).copy())
+    got16 = fp4mod._round_to_e2m1(bits.view(torch.bfloat16).to(dev)).cpu().numpy()
     assert np.array_equal(got16, arrays["round_all_bf16__codes"])
 
 
@@ -197,3 +199,17 @@ def test_repeat_runs_are_bitwise_identical(dev, fp4mod):
     a = fp4mod.quantize_pack_mxfp4(x)
     b = fp4mod.quantize_pack_mxfp4(x)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_quantize_kmajor_scale_layout(dev, fp4mod, oracle):
+    """K-major E8M0 scales hold the same bytes as the row-major ones,
+    rearranged to [K/128, rows, 4]."""
+    for rows, K in [(1, 128), (37, 384), (300, 4096)]:
+        x = gen.student_t3(rows + K, (rows, K), scale=0.05)
+        rc, rs = oracle.quantize_mxfp4(x)
+        pk, e8 = fp4mod.quantize_pack_mxfp4(to_dev(x, "f32", dev), scale_layout="kmajor")
+        want = oracle.scale_to_e8m0(rs).reshape(rows, K // 128, 4).transpose(1, 0, 2)
+        assert e8.shape == (K // 128, rows, 4)
+        assert np.array_equal(e8.cpu().numpy(), want), (rows, K)
+        assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(rc)), (rows, K)
+        assert torch.equal(fp4mod.kmajor_scales(fp4mod.quantize_pack_mxfp4(to_dev(x, "f32", dev))[1]), e8)
