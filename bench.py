@@ -262,10 +262,34 @@ def run_suite(path, torch, dev):
         lines.append({"config": f"cfg3 weight-only bf16 x mxfp4, M={M}, N=14336, K=4096", "ms": ms,
                       "tflops": fl / ms / 1e9, "gbs": by / ms / 1e6,
                       "frac_bf16_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS, "frac_hbm": by / ms / 1e6 / PEAK_HBM_GBS})
+    lines.append(bench_cfg5(torch, dev))
     with open(path, "w") as f:
         for ln in lines:
             f.write(json.dumps(ln) + "\n")
             print(json.dumps(ln), file=sys.stderr, flush=True)
+
+
+def bench_cfg5(torch, dev, T=8192, H=2048, F=8192):
+    """cfg5: one MLP block (fc H->F, out F->H) forward + MXFP4 backward.
+    Per linear: quantize X and W along K + GEMM (fprop), dY along N and W
+    along its columns + GEMM (dgrad), dY and X along T + GEMM (wgrad)."""
+    from lockstep_amd import fp4_linear as fl
+    g = torch.Generator(device=dev).manual_seed(5001)
+    x = torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn((F, H), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((H, F), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    dy = torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16)
+
+    def step():
+        h = fl._forward_hip(x, w1)                 # [T, F]
+        fl._forward_hip(h, w2)                     # [T, H]
+        dh, _ = fl.mxfp4_backward(dy, h, w2)       # dgrad + wgrad of out
+        fl.mxfp4_backward(dh, x, w1)               # dgrad + wgrad of fc
+    ms = _time_events(step, reps=10, warm=2)
+    fl_ = 6 * 2.0 * T * F * H
+    return {"config": f"cfg5 MLP block fwd + MXFP4 bwd, tokens={T} hidden={H} ffn={F}, bf16 in/out",
+            "ms": ms, "tflops": fl_ / ms / 1e9, "frac_fp4_peak": fl_ / ms / 1e9 / PEAK_FP4_TFLOPS,
+            "work": "12 quantizations + 6 f4xf4 GEMMs (1.649e12 FLOP)"}
 
 
 if __name__ == "__main__":

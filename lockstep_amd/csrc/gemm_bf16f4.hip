@@ -225,6 +225,199 @@ __global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
     }
 }
 
+// ------------------------------------------------------------------ skinny M
+// For few activation rows (decode, M <= 64 per batch) the weight stream is the
+// whole cost: N*K/2 bytes of codes against 2*M*K bytes of activations.  The
+// 256-row tile above would leave most CUs idle, so this kernel spreads the
+// weight over the chip instead:
+//   - a workgroup owns 16*CT weight rows, its 8 waves split K: wave w takes
+//     the 128-wide K chunks w, w + 8, w + 16, ...
+//   - each lane loads one 16-byte MX block (32 codes) of one weight row per
+//     chunk straight into registers, dequantizes it with
+//     v_cvt_scalef32_pk_bf16_fp4, and feeds v_mfma_f32_16x16x32_bf16;
+//   - the activation rows (MT tiles of 16, rows past M clamped) come straight
+//     from global memory/L2, where they stay resident: they are tiny;
+//   - the 8 partial sums are added in LDS in wave order and stored.
+// K positions inside a chunk are assigned so that lane group q (lanes
+// 16q..16q+15) of MFMA step s covers K = 128c + 32q + 8s .. +8 for both
+// operands: one lane's 16 weight bytes are one block with one scale.
+// Dual mode: virtual rows [0, M) are A0's and [M, 2M) are A1's, so the
+// weight is streamed once for both batches.  The summation order of an
+// output element depends on K only, so single and dual launches of the same
+// M and K give identical bits.
+#ifndef LSMX_SKINNY_WK
+#define LSMX_SKINNY_WK 8
+#endif
+#ifndef LSMX_SKINNY_U1
+#define LSMX_SKINNY_U1 2
+#endif
+namespace sk {
+constexpr int WK = LSMX_SKINNY_WK;  // waves per workgroup (K split)
+constexpr int CHUNK = 128;
+}  // namespace sk
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// MT <= 2: at most 128 VGPRs, so two workgroups (16 waves) share a CU.
+template <int MT, int CT>
+__global__ __launch_bounds__(64 * sk::WK, MT <= 2 ? 4 : 2) void gemm_bf16f4_skinny_kernel(GemmArgs g) {
+    constexpr int U = MT == 1 ? LSMX_SKINNY_U1 : 1;  // chunks in flight per wave
+    __shared__ float red[sk::WK][MT * CT * 256];
+
+    const int lane = threadIdx.x & 63, wk = threadIdx.x >> 6;
+    const int j = lane & 15, grp = lane >> 4;
+    const bool dual = g.a1 != nullptr;
+    const int64_t VM = dual ? 2 * g.M : g.M;
+    const int64_t nbase = (int64_t)blockIdx.x * (16 * CT);
+    const bool sf32 = g.scale_fmt == LSMX_SCALE_F32;
+
+    const uint8_t *arow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int64_t v = min((int64_t)(16 * mt + j), VM - 1);
+        const bool second = dual && v >= g.M;
+        arow[mt] = (second ? g.a1 : g.a) + (second ? v - g.M : v) * g.lda * 2 + grp * 64;
+    }
+    const uint8_t *wrow[CT];
+    int64_t srow[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        const int64_t n = min(nbase + 16 * ct + j, g.N - 1);
+        wrow[ct] = g.b + n * g.ldb + grp * 16;
+        srow[ct] = n * g.ld_sb + grp;
+    }
+
+    v4f acc[MT][CT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[mt][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const int nchunks = (int)(g.K / sk::CHUNK);
+    for (int c0 = wk; c0 < nchunks; c0 += sk::WK * U) {
+        u32x4 wv[U][CT], av[U][MT][4];
+        uint32_t sv[U][CT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u * sk::WK;
+            if (c < nchunks) {
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    wv[u][ct] = *reinterpret_cast<const u32x4 *>(wrow[ct] + (int64_t)c * 64);
+                    const int64_t so = srow[ct] + (int64_t)c * 4;
+                    sv[u][ct] = sf32 ? (f2u(reinterpret_cast<const float *>(g.sb)[so]) >> 23) & 0xFF
+                                     : reinterpret_cast<const uint8_t *>(g.sb)[so];
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        av[u][mt][s] = *reinterpret_cast<const u32x4 *>(arow[mt] + (int64_t)c * 256 + s * 16);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + u * sk::WK < nchunks) {
+                float sc[CT];
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) sc[ct] = e8m0_scale_f32(sv[u][ct]);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    // dequantize step s of every column tile: codes 8s..8s+7 of the block
+                    v8bf wf[CT];
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct) {
+                        const uint32_t p = wv[u][ct][s];
+                        const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[ct], 0);
+                        const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[ct], 1);
+                        const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[ct], 2);
+                        const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[ct], 3);
+                        wf[ct] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const v8bf fa = __builtin_bit_cast(v8bf, av[u][mt][s]);
+#pragma unroll
+                        for (int ct = 0; ct < CT; ++ct)
+                            acc[mt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, wf[ct], acc[mt][ct], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+
+    // acc[mt][ct][r] = D[4*grp + r][j] of the 16 x 16 tile (rows: activation
+    // rows of m-tile mt, columns: weight rows of col tile ct)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wk][(mt * CT + ct) * 256 + r * 64 + lane] = acc[mt][ct][r];
+    __syncthreads();
+    for (int p = wk; p < MT * CT; p += sk::WK) {
+        const int mt = p / CT, ct = p % CT;
+        const int64_t n = nbase + 16 * ct + j;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < sk::WK; ++w) v += red[w][p * 256 + r * 64 + lane];
+            const int64_t vr = 16 * mt + 4 * grp + r;
+            if (vr < VM && n < g.N) {
+                const bool second = dual && vr >= g.M;
+                void *cb = second ? g.c1 : g.c;
+                const int64_t idx = (second ? vr - g.M : vr) * g.ldc + n;
+                if (g.c_dtype == LSMX_F32) store_cw<LSMX_F32>(cb, idx, v);
+                else if (g.c_dtype == LSMX_BF16) store_cw<LSMX_BF16>(cb, idx, v);
+                else store_cw<LSMX_F16>(cb, idx, v);
+            }
+        }
+    }
+}
+
+#ifndef LSMX_SKINNY_MAX_M
+#define LSMX_SKINNY_MAX_M 64
+#endif
+
+static int num_cus_w() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+static hipError_t launch_skinny(const GemmArgs &g, hipStream_t s) {
+    const int64_t vm = g.a1 ? 2 * g.M : g.M;
+    const int mt = vm <= 16 ? 1 : vm <= 32 ? 2 : vm <= 64 ? 4 : 8;
+    // two 16-row weight tiles per workgroup (the activation loads then serve
+    // twice the weight bytes) while that still gives every CU a workgroup;
+    // MT <= 2 keeps two workgroups resident per CU either way
+#ifndef LSMX_SKINNY_CT2
+#define LSMX_SKINNY_CT2 1
+#endif
+    const int ct = (LSMX_SKINNY_CT2 && mt <= 4 && (g.N + 31) / 32 >= num_cus_w()) ? 2 : 1;
+    const dim3 grid((unsigned)((g.N + 16 * ct - 1) / (16 * ct))), blk(64 * sk::WK);
+#define LSMX_S(MT, CT) hipLaunchKernelGGL((gemm_bf16f4_skinny_kernel<MT, CT>), grid, blk, 0, s, g)
+    switch (mt * 10 + ct) {
+        case 11: LSMX_S(1, 1); break;
+        case 12: LSMX_S(1, 2); break;
+        case 21: LSMX_S(2, 1); break;
+        case 22: LSMX_S(2, 2); break;
+        case 41: LSMX_S(4, 1); break;
+        case 42: LSMX_S(4, 2); break;
+        default: LSMX_S(8, 1); break;
+    }
+#undef LSMX_S
+    return hipGetLastError();
+}
+
 template <int NB>
 static hipError_t launch_w4(const GemmArgs &g, hipStream_t s) {
     constexpr int RPB = w4::BR / NB;
@@ -246,6 +439,8 @@ static hipError_t launch_w4(const GemmArgs &g, hipStream_t s) {
 }
 
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
+    // the same M picks the same kernel for the single and the dual form
+    if (g.M <= LSMX_SKINNY_MAX_M && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
     return g.a1 ? launch_w4<2>(g, s) : launch_w4<1>(g, s);
 }
 

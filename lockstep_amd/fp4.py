@@ -139,12 +139,14 @@ def kmajor_scales(e8m0: torch.Tensor) -> torch.Tensor:
     return e8m0.reshape(rows, nb // 4, 4).transpose(0, 1).contiguous()
 
 
-def quantize_mxfp4_t(x: torch.Tensor, block: int = 32, packed: bool = True, e8m0: bool = True):
+def quantize_mxfp4_t(x: torch.Tensor, block: int = 32, packed: bool = True, e8m0: bool = True,
+                     scale_layout: str = "rows"):
     """Quantize a 2-D x [K, N] along its FIRST axis, without a transpose copy.
 
-    Equals quantize_pack_mxfp4(x.t().contiguous()) (packed, e8m0) or
-    quantize_mxfp4(x.t().contiguous()) (packed=False, e8m0=False): outputs are
-    laid out for x^T, [N, K//2 or K] and [N, K//block]."""
+    Equals quantize_pack_mxfp4(x.t().contiguous(), scale_layout=...) (packed,
+    e8m0) or quantize_mxfp4(x.t().contiguous()) (packed=False, e8m0=False):
+    outputs are laid out for x^T, codes [N, K//2 or K] and scales
+    [N, K//block] ("rows") or [K//128, N, 4] ("kmajor", E8M0 and block 32)."""
     C.require_device(x)
     x = _src(x)
     assert x.dim() == 2, "quantize_mxfp4_t takes a 2-D tensor"
@@ -153,12 +155,21 @@ def quantize_mxfp4_t(x: torch.Tensor, block: int = 32, packed: bool = True, e8m0
     if x.stride(1) != 1 or (K > 1 and x.stride(0) < N):
         x = x.contiguous()
     codes = torch.empty((N, K // 2 if packed else K), dtype=torch.uint8, device=x.device)
-    scale = torch.empty((N, K // block), dtype=torch.uint8 if e8m0 else torch.float32,
-                        device=x.device)
+    if scale_layout == "kmajor":
+        assert e8m0 and block == 32 and K % 128 == 0, \
+            "K-major scales need E8M0, block 32 and K % 128 == 0"
+        scale = torch.empty((K // 128, N, 4), dtype=torch.uint8, device=x.device)
+        fmt, ld = C.SCALE_E8M0_KMAJOR, N
+    elif scale_layout == "rows":
+        scale = torch.empty((N, K // block), dtype=torch.uint8 if e8m0 else torch.float32,
+                            device=x.device)
+        fmt, ld = (C.SCALE_E8M0 if e8m0 else C.SCALE_F32), K // block
+    else:
+        raise ValueError(f"scale_layout must be 'rows' or 'kmajor', got {scale_layout!r}")
     C.call("lsmx_quantize_mxfp4_t", x.data_ptr(), C.dtype_code(x.dtype), K, N,
            x.stride(0) if K > 1 else N, block, codes.data_ptr(),
            C.CODES_PACKED if packed else C.CODES_UNPACKED, codes.shape[1], scale.data_ptr(),
-           C.SCALE_E8M0 if e8m0 else C.SCALE_F32, K // block, C.stream_of(x))
+           fmt, ld, C.stream_of(x))
     return codes, scale
 
 

@@ -123,3 +123,16 @@ def test_slot_arithmetic():
         c2 = torch.tensor([-144.0 * k, 144.0 * k, -7.0], dtype=torch.float64)
         g1, g2 = dg.unpack_dual(c1 + c2 * 2.0 ** s, s)
         assert torch.equal(g1, c1) and torch.equal(g2, c2)
+
+
+def test_quantized_backward_checks_shapes_before_any_kernel():
+    from lockstep_amd import fp4_linear
+    x = torch.zeros(100, 128)
+    w = torch.zeros(128, 128)
+    with pytest.raises(AssertionError, match="multiples of 128"):
+        fp4_linear.mxfp4_backward(torch.zeros(100, 128), x, w)
+    with pytest.raises(AssertionError, match="shapes must be"):
+        fp4_linear.mxfp4_backward(torch.zeros(128, 64), torch.zeros(128, 128), w)
+    layer = fp4_linear.MXFP4Linear(128, 128)
+    assert layer.quantized_backward is False      # the reference's STE backward by default
+    assert fp4_linear.MXFP4Linear(128, 128, quantized_backward=True).quantized_backward
