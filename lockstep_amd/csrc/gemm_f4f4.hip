@@ -8,14 +8,18 @@
 // Instead of promoting an FP8 product to fp32 every 32-block and multiplying
 // by fp32 scales, v_mfma_scale_f32_32x32x64_f8f6f4 (cbsz = blgp = 4, FP4)
 // applies one E8M0 scale per lane per operand inside the instruction: for
-// that instruction each lane supplies the 32 codes (16 bytes) of one row and
-// one 32-block, which is exactly one MX block, and the byte of the scale
-// register selected by op_sel.
+// that instruction each lane supplies the 32 codes (16 bytes, four VGPRs) of
+// one row and one 32-block, which is exactly one MX block, and the byte of
+// the scale register selected by op_sel.
 //
 // Tiling: 256 x 256 macro tile, WGM x WGN waves (default 4 x 2, two waves per
 // SIMD), each wave a (256/WGM) x (256/WGN) sub-tile of 32 x 32 MFMA tiles
-// with fp32 accumulators in AGPRs.  K advances 128 codes (64 bytes per row,
-// four MX blocks) per stage, two MFMA K-steps of 64.
+// with fp32 accumulators.  A pipeline stage holds KS MFMA K-steps of 64
+// codes: KS = 4 stages 128 bytes of every row (256 codes), KS = 2 stages 64.
+// Whole 128-byte rows matter: the direct-to-LDS path is limited by the
+// number of L2 requests, and a 64-byte row segment costs a request for half
+// a cache line (measured: 19 B/clk per CU for 16 rows x 64 B per load
+// instruction, 36 B/clk for 8 rows x 128 B).
 //
 // Persistent schedule: one workgroup per CU walks tiles pid, pid + grid, ...
 // A ring of S stage slots in LDS is filled by direct-to-LDS loads
@@ -26,49 +30,75 @@
 // s_waitcnt vmcnt: the compiler cannot prove that ring slots do not alias and
 // would otherwise wait for every outstanding load before each LDS read.
 //
-// Per stage and wave: the step-1 fragments are read while the step-0 MFMAs
-// run; one s_barrier (after the stage's own reads completed and the next
-// stage's loads landed) frees the slot; then the step-1 MFMAs run with the
-// refill of that slot and the next stage's fragment and scale reads
-// interleaved one by one between them, so the matrix core never waits on a
-// burst of memory instructions.  Refills past the last stage re-load the
-// workgroup's last tile (tile indices are clamped, lsmx_sched.h) into a slot
-// that is never read again, which keeps the loop free of branches and the
-// outstanding-load count constant.
+// Per stage and wave: while the MFMAs of K-step st run, the fragments of
+// K-step st + 1 are read from LDS between them.  Before the last K-step, one
+// s_barrier (after the stage's own reads completed and the next stage's
+// loads landed) frees the slot; the last K-step's MFMAs then run with the
+// refill of that slot and the next stage's scale and K-step-0 fragment reads
+// interleaved, so the matrix core never waits on a burst of memory
+// instructions.  Refills past the last stage re-load the workgroup's last
+// tile (tile indices are clamped, lsmx_sched.h) into a slot that is never
+// read again, which keeps the loop free of branches and the outstanding-load
+// count constant.
 //
-// LDS layout per stage: rows of 64 bytes = four 16-byte chunks; chunk c of
-// row r lives at r*64 + 16*(c ^ swz(r)), which keeps the lanes a ds_read_b128
-// serves per cycle on distinct banks.  The DMA writes slots in lane order, so
-// the swizzle is applied by choosing each lane's source address.
+// LDS layout per stage: rows of 16*CPR bytes (CPR = 2*KS chunks of 16 bytes);
+// chunk c of row r lives at r*16*CPR + 16*(c ^ swz(r)), which keeps the 16
+// lanes a ds_read_b128 serves per cycle on distinct banks.  The DMA writes
+// slots in lane order, so the swizzle is applied by choosing each lane's
+// source address.
 #include "lsmx_internal.h"
 #include "lsmx_sched.h"
 
 namespace lsmx {
 
-typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// The scaled MFMA with 4-VGPR operands: the FP4 form reads only 16 bytes per
+// lane, and the v8i32 form of the clang builtin would hold four zero VGPRs
+// per fragment.  The LLVM intrinsic is overloaded on the operand width.
+__device__ v16f mfma_scale_f4(v4i a, v4i b, v16f c, int cbsz, int blgp, int opsel_a, int scale_a, int opsel_b,
+                              int scale_b) __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v4i32.v4i32");
+
 namespace f4 {
 constexpr int BM = 256, BN = 256;
-constexpr int BKB = 64;           // bytes of K per row per stage (128 codes, 4 blocks)
 constexpr int GROUP_M = 4;
-constexpr int TILE_B = BM * BKB;  // 16 KiB per operand per stage
 }  // namespace f4
 
-LSMX_DEV int f4_swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// swizzle of 16-byte chunk positions in a row of CPR chunks
+template <int CPR>
+LSMX_DEV int f4_swz(int row) {
+    if constexpr (CPR == 4) return ((row >> 1) ^ (row >> 3)) & 3;
+    else return (row >> 1) & 7;
+}
 
 LSMX_DEV uint32_t lds_u32(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-// Direct-to-LDS loads: lane l's bytes land at m0 + l*size.
-LSMX_DEV void dma_x4(const void *g, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory");
+// Direct-to-LDS loads through a buffer descriptor: lane l's bytes land at
+// m0 + l*size, and a lane whose offset lies at or past the descriptor's byte
+// count reads zeros (raw buffer, stride 0), so rows past the operand need no
+// clamping and a load costs no 64-bit address arithmetic.  The descriptor is
+// built in SGPRs from a wave-uniform base and size; dword 3 selects the
+// 32-bit data format that untyped buffer loads require.
+typedef int v4i_rsrc __attribute__((ext_vector_type(4)));
+LSMX_DEV v4i_rsrc buf_rsrc(const void *base, uint64_t bytes) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
+    return v4i_rsrc{(int)__builtin_amdgcn_readfirstlane((uint32_t)p),
+                    (int)(__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) & 0xFFFF),
+                    (int)__builtin_amdgcn_readfirstlane(n), 0x00020000};
 }
-LSMX_DEV void dma_x1(const void *g, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory");
+LSMX_DEV void dma_x4(uint32_t off, v4i_rsrc r, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(off), "s"(r),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
+}
+LSMX_DEV void dma_x1(uint32_t off, v4i_rsrc r, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(off), "s"(r),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
 }
 
 LSMX_DEV uint32_t bf16_rne(float f) {
@@ -128,22 +158,17 @@ LSMX_DEV void quad_transpose(float (&x)[4], int q) {
 template <int N>
 LSMX_DEV void wait_vm_barrier() {
     // all of this thread's loads except the newest N have landed, then sync
-    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory");
-    else if constexpr (N == 10) asm volatile("s_waitcnt vmcnt(10)\n\ts_barrier" ::: "memory");
-    else if constexpr (N == 15) asm volatile("s_waitcnt vmcnt(15)\n\ts_barrier" ::: "memory");
-    else if constexpr (N == 20) asm volatile("s_waitcnt vmcnt(20)\n\ts_barrier" ::: "memory");
-    else if constexpr (N == 30) asm volatile("s_waitcnt vmcnt(30)\n\ts_barrier" ::: "memory");
-    else static_assert(N < 0, "unsupported vmcnt");
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // Scale formats (SFMT = LSMX_SCALE_*): F32 scales arrive as fp32 powers of two
-// (16 bytes per row per stage) and are reduced to E8M0 bytes when read; E8M0
-// row-major scales take one dword per row per stage at a stride of K/32 bytes;
-// K-major E8M0 scales ([K/128][rows][4]) give the dwords of one stage for
-// consecutive rows as one contiguous run -- one 64-byte request per 16 rows
-// instead of one per row.
-template <int SFMT, int CT, int S, int WGM, int WGN>
+// (16 bytes per row per 128 codes) and are reduced to E8M0 bytes when read;
+// E8M0 row-major scales take one dword per row per 128 codes at a stride of
+// K/32 bytes; K-major E8M0 scales ([K/128][rows][4]) give the dwords of one
+// 128-code slice for consecutive rows as one contiguous run -- one 64-byte
+// request per 16 rows instead of one per row.
+template <int SFMT, int CT, int S, int WGM, int WGN, int KS>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g) {
     using namespace f4;
     constexpr bool SF32 = SFMT == LSMX_SCALE_F32;
@@ -152,125 +177,162 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     constexpr int NTH = 64 * NW;
     constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
     constexpr int NMF = TM * TN;               // MFMAs per K-step
-    constexpr int SROW = SF32 ? 16 : 4;        // scale bytes per row per stage
-    constexpr int XA = (BM * BKB / 16) / NTH;  // 16-byte DMA slots per thread per operand
+    constexpr int BKB = 32 * KS;               // bytes of K per row per stage
+    constexpr int CPR = BKB / 16;              // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;              // rows per DMA instruction
+    constexpr int TILE_B = BM * BKB;           // bytes per operand per stage
+    constexpr int NSL = KS / 2;                // 128-code scale slices per stage
+    constexpr int SSL = SF32 ? 16 : 4;         // scale bytes per row per slice
+    constexpr int XA = (TILE_B / 16) / NTH;    // 16-byte DMA slots per thread per operand
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    static_assert(KS == 2 || KS == 4, "2 or 4 K-steps per stage");
     // scale loads: with 4 waves every wave loads 64 rows of A's and of B's
-    // scales; with 8 waves waves 0-3 load A's and waves 4-7 load B's.
-    constexpr int L = 2 * XA + (NW == 4 ? 2 : 1);  // loads per thread per stage
-    constexpr int NRD = TM + TN;                   // fragment reads per K-step
-    static_assert(NMF >= L, "one refill op per MFMA at most");
-    constexpr int RPM0 = (NRD + NMF - 1) / NMF;      // LDS reads per MFMA, step 0
-    constexpr int RPM1 = (2 * NRD + NMF - 1) / NMF;  // LDS reads per MFMA, step 1
+    // scales per slice; with 8 waves waves 0-3 load A's and waves 4-7 B's.
+    constexpr int LS = (NW == 4 ? 2 : 1) * NSL;
+    constexpr int L = 2 * XA + LS;                   // loads per thread per stage
+    constexpr int NRD = TM + TN;                     // fragment (and scale) reads per K-step / stage
+    constexpr int OPM = (L + NMF - 1) / NMF;         // refill ops per MFMA, last K-step
+    constexpr int RPM0 = (NRD + NMF - 1) / NMF;      // LDS reads per MFMA, other K-steps
+    constexpr int RPM1 = (2 * NRD + NMF - 1) / NMF;  // LDS reads per MFMA, last K-step
     __shared__ __attribute__((aligned(16))) uint8_t sA[S][TILE_B];
     __shared__ __attribute__((aligned(16))) uint8_t sB[S][TILE_B];
-    __shared__ __attribute__((aligned(16))) uint8_t sSA[S][BM * SROW];
-    __shared__ __attribute__((aligned(16))) uint8_t sSB[S][BN * SROW];
+    __shared__ __attribute__((aligned(16))) uint8_t sSA[S][NSL][BM * SSL];
+    __shared__ __attribute__((aligned(16))) uint8_t sSB[S][NSL][BN * SSL];
 
     const int tiles_m = (int)((g.M + BM - 1) / BM), tiles_n = (int)((g.N + BN - 1) / BN);
     const int tiles = tiles_m * tiles_n;
     const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int nk = (int)(g.K / 128);
+    const int nk = (int)(g.K / (2 * BKB));
 
     const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS bases stay scalar
     const int wm = wave / WGN, wn = wave % WGN;
     const int frow = lane & 31, half = lane >> 5;
     const int rowA0 = wm * (TM * 32) + frow, rowB0 = wn * (TN * 32) + frow;
 
-    // ---- DMA source of this thread for stage u (tile u / nk, k-step u % nk)
-    int dma_row[XA], dma_c[XA];
-#pragma unroll
-    for (int i = 0; i < XA; ++i) {
-        dma_row[i] = (i * NW + wave) * 16 + (lane >> 2);
-        dma_c[i] = ((lane & 3) ^ f4_swz(dma_row[i])) * 16;
-    }
+    // ---- DMA addressing.  Data load i of this lane reads row
+    // (i*NW + wave)*RPI + lane/CPR of the refill tile; the chunk swizzle of
+    // those rows does not depend on i, so the byte offset is off0 + i*step.
+    // Descriptors start at the refill tile's first row and K offset and end
+    // at the operand's last row: rows past it read zeros.
+    const int drow0 = wave * RPI + lane / CPR;
+    const uint32_t offA0 = (uint32_t)(drow0 * g.lda + ((lane % CPR) ^ f4_swz<CPR>(drow0)) * 16);
+    const uint32_t offB0 = (uint32_t)(drow0 * g.ldb + ((lane % CPR) ^ f4_swz<CPR>(drow0)) * 16);
+    const uint32_t stepA = (uint32_t)(NW * RPI * g.lda), stepB = (uint32_t)(NW * RPI * g.ldb);
     const int srow = (wave & 3) * 64 + lane;
     const bool s_is_b = NW == 8 && wave >= 4;
-    const int64_t sbytes = SF32 ? 4 : 1;
-
-    // origin of this workgroup's tile iteration ti (clamped to its real tiles)
+    // scale arrays: total bytes, and this lane's row offset inside a slice
+    const uint64_t sbytes_a = SKM ? ((g.K / 128 - 1) * g.ld_sa + g.M) * 4
+                                  : ((g.M - 1) * g.ld_sa + g.K / 32) * (SF32 ? 4 : 1);
+    const uint64_t sbytes_b = SKM ? ((g.K / 128 - 1) * g.ld_sb + g.N) * 4
+                                  : ((g.N - 1) * g.ld_sb + g.K / 32) * (SF32 ? 4 : 1);
+    const uint32_t offSA = (uint32_t)(SKM ? srow * 4 : SF32 ? srow * g.ld_sa * 4 : srow * g.ld_sa);
+    const uint32_t offSB = (uint32_t)(SKM ? srow * 4 : SF32 ? srow * g.ld_sb * 4 : srow * g.ld_sb);
+    int64_t rm0 = 0, rn0 = 0;  // origin of the refill tile
+    static_assert(GROUP_M <= 4, "tile_coords divides by group heights up to 4");
+    const TileMap tmap = make_tile_map(tiles_m, tiles_n, GROUP_M);
     auto tile_of = [&](int ti, int64_t &m0, int64_t &n0) {
         int tm, tn;
         ti = imax(0, imin(ti, my_tiles - 1));
-        tile_coords((int)blockIdx.x + ti * (int)gridDim.x, tiles_m, tiles_n, GROUP_M, tm, tn);
+        tile_coords((int)blockIdx.x + ti * (int)gridDim.x, tmap, tm, tn);
         m0 = (int64_t)tm * BM;
         n0 = (int64_t)tn * BN;
     };
-    // one memory op (q = 0..L-1) of loading stage (tile origin m0/n0, k-step
-    // kt) into ring slot s
-    auto issue_op = [&](int64_t m0, int64_t n0, int kt, int s, int q) {
+    auto set_refill_tile = [&](int ti) { tile_of(ti, rm0, rn0); };
+    // one memory op (q = 0..L-1) of loading k-step kt of the refill tile into ring slot s
+    auto issue_op = [&](int kt, int s, int q) {
         const int64_t ko = (int64_t)kt * BKB;
         if (q < 2 * XA) {
             const int i = q >> 1;
-            if ((q & 1) == 0)
-                dma_x4(g.a + min(m0 + dma_row[i], g.M - 1) * g.lda + dma_c[i] + ko,
-                       __builtin_amdgcn_readfirstlane(lds_u32(&sA[s][(i * NW + wave) * 1024])));
-            else
-                dma_x4(g.b + min(n0 + dma_row[i], g.N - 1) * g.ldb + dma_c[i] + ko,
-                       __builtin_amdgcn_readfirstlane(lds_u32(&sB[s][(i * NW + wave) * 1024])));
+            const uint32_t m0 = lds_u32((q & 1) ? &sB[0][0] : &sA[0][0]) + s * TILE_B + (i * NW + wave) * 1024;
+            if ((q & 1) == 0) {
+                const int64_t rows = min(g.M - rm0, (int64_t)BM);
+                dma_x4(offA0 + i * stepA, buf_rsrc(g.a + rm0 * g.lda + ko, (uint64_t)(rows * g.lda - ko)), m0);
+            } else {
+                const int64_t rows = min(g.N - rn0, (int64_t)BN);
+                dma_x4(offB0 + i * stepB, buf_rsrc(g.b + rn0 * g.ldb + ko, (uint64_t)(rows * g.ldb - ko)), m0);
+            }
             return;
         }
-        const int soff = (wave & 3) * 64 * SROW;
-        const bool to_b = NW == 4 ? (q == 2 * XA + 1) : s_is_b;
-        const int64_t srow_g = to_b ? min(n0 + srow, g.N - 1) : min(m0 + srow, g.M - 1);
-        const int64_t sld = to_b ? g.ld_sb : g.ld_sa;
-        // byte offset of this lane's 4 (E8M0) or 16 (F32) scale bytes of stage kt
-        const int64_t so = SKM ? ((int64_t)kt * sld + srow_g) * 4 : srow_g * sld * sbytes + (int64_t)kt * SROW;
+        const int r = q - 2 * XA;
+        const bool to_b = NW == 4 ? (r & 1) : s_is_b;
+        const int j = NW == 4 ? (r >> 1) : r;  // scale slice within the stage
+        const int64_t slice = (int64_t)kt * NSL + j;
         const uint8_t *src = reinterpret_cast<const uint8_t *>(to_b ? g.sb : g.sa);
-        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_u32(to_b ? &sSB[s][soff] : &sSA[s][soff]));
-        if constexpr (SF32) dma_x4(src + so, dst);
-        else dma_x1(src + so, dst);
-    };
-    auto refill = [&](int u, int s) {  // all ops of stage u (prologue)
-        int64_t m0, n0;
-        tile_of(stage_tile_iter(u, nk, my_tiles), m0, n0);
-#pragma unroll
-        for (int q = 0; q < L; ++q) issue_op(m0, n0, u % nk, s, q);
+        const int64_t r0 = to_b ? rn0 : rm0, sld = to_b ? g.ld_sb : g.ld_sa;
+        // scalar part of this slice's address; the lane adds its row offset.
+        // Rows past the operand read other scales or zeros: their products
+        // only reach outputs that are not stored.
+        const int64_t sb0 = SKM ? (slice * sld + r0) * 4 : SF32 ? r0 * sld * 4 + slice * 16 : r0 * sld + slice * 4;
+        const v4i_rsrc rs = buf_rsrc(src + sb0, (to_b ? sbytes_b : sbytes_a) - (uint64_t)sb0);
+        const uint32_t m0 = lds_u32(to_b ? &sSB[s][j][(wave & 3) * 64 * SSL] : &sSA[s][j][(wave & 3) * 64 * SSL]);
+        if constexpr (SF32) dma_x4(to_b ? offSB : offSA, rs, m0);
+        else dma_x1(to_b ? offSB : offSA, rs, m0);
     };
 
-    auto scale_of = [&](const uint8_t *base, int r) -> uint32_t {
-        if constexpr (SF32) {
-            const u32x4 f = *reinterpret_cast<const u32x4 *>(base + r * 16);
-            return ((f[0] >> 23) & 0xFF) | (((f[1] >> 23) & 0xFF) << 8) | (((f[2] >> 23) & 0xFF) << 16) |
-                   (((f[3] >> 23) & 0xFF) << 24);
-        } else {
-            return *reinterpret_cast<const uint32_t *>(base + r * 4);
-        }
-    };
-    // fragment read q (0..NRD-1) of K-step st from slot s: A tiles, then B tiles
-    auto read_frag = [&](int s, int st, int q, v8i (&fa)[TM], v8i (&fb)[TN]) {
-        const int c = 2 * st + half;
+    // K positions: at K-step st, lane half h supplies 16-byte chunk
+    // c = (KS/2)*2*h + st of its row -- for KS = 4 the four blocks of scale
+    // slice h, for KS = 2 blocks 2h and 2h+1 -- so one scale register per
+    // fragment row serves the whole stage and op_sel = st picks the block's
+    // byte.  A and B use the same assignment, so the sum is unchanged.
+    auto chunk_of = [&](int st) { return (KS == 4 ? 4 : 2) * half + st; };
+    auto read_frag = [&](int s, int st, int q, v4i (&fa)[TM], v4i (&fb)[TN]) {
+        const int c = chunk_of(st);
         const int r = q < TM ? rowA0 + q * 32 : rowB0 + (q - TM) * 32;
         const uint8_t *base = q < TM ? sA[s] : sB[s];
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(base + r * BKB + ((c ^ f4_swz(r)) << 4));
-        const v8i f = v8i{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(base + r * BKB + ((c ^ f4_swz<CPR>(r)) << 4));
+        const v4i f = v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
         if (q < TM) fa[q] = f;
         else fb[q - TM] = f;
     };
+    // scale register of fragment row q: the bytes of blocks chunk_of(0..KS-1)
     auto read_scale = [&](int s, int q, uint32_t (&sa)[TM], uint32_t (&sb)[TN]) {
-        if (q < TM) sa[q] = scale_of(sSA[s], rowA0 + q * 32) >> (8 * half);
-        else sb[q - TM] = scale_of(sSB[s], rowB0 + (q - TM) * 32) >> (8 * half);
+        const uint8_t *tab = q < TM ? sSA[s][KS == 4 ? half : 0] : sSB[s][KS == 4 ? half : 0];
+        const int r = q < TM ? rowA0 + q * 32 : rowB0 + (q - TM) * 32;
+        uint32_t v;
+        if constexpr (SF32) {
+            const u32x4 f = *reinterpret_cast<const u32x4 *>(tab + r * 16);
+            v = (((f[0] >> 23) & 0xFF) | (((f[1] >> 23) & 0xFF) << 8) | (((f[2] >> 23) & 0xFF) << 16) |
+                 (((f[3] >> 23) & 0xFF) << 24)) >> (16 * half);
+        } else if constexpr (KS == 4) {
+            v = *reinterpret_cast<const uint32_t *>(tab + r * 4);
+        } else {
+            v = *reinterpret_cast<const uint16_t *>(tab + r * 4 + 2 * half);
+        }
+        if (q < TM) sa[q] = v;
+        else sb[q - TM] = v;
     };
 
     v16f acc[TM][TN];
     uint32_t scA[TM], scB[TN], nA[TM], nB[TN];
-    v8i fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    v4i fa[2][TM], fb[2][TN];
 
     // ---- prologue: fill the ring, publish stage 0, read its step-0 operands
+    {
+        int cur = -1;
 #pragma unroll
-    for (int p = 0; p < S; ++p) refill(p, p);
+        for (int p = 0; p < S; ++p) {
+            const int ti = stage_tile_iter(p, nk, my_tiles);
+            if (ti != cur) {
+                set_refill_tile(ti);
+                cur = ti;
+            }
+#pragma unroll
+            for (int q = 0; q < L; ++q) issue_op(p % nk, p, q);
+        }
+    }
     wait_vm_barrier<(S - 1) * L>();
 #pragma unroll
     for (int q = 0; q < NRD; ++q) read_scale(0, q, scA, scB);
 #pragma unroll
-    for (int q = 0; q < NRD; ++q) read_frag(0, 0, q, fa0, fb0);
+    for (int q = 0; q < NRD; ++q) read_frag(0, 0, q, fa[0], fb[0]);
 
     const bool vec_c = ((reinterpret_cast<uintptr_t>(g.c) & 15) == 0) && (g.ldc % 4 == 0);
     // Stage u + S refills slot u % S.  Stages past the last one re-load the
     // workgroup's last tile (tile_of clamps), so the loads stay inside the
     // operands and land in slots that are never read again.
-    int rt = S / nk, rk = S % nk;  // tile iteration and k-step of stage u + S
+    const DivU32 div_nk = make_div((uint32_t)nk);
     int u = 0;
     for (int ti = 0; ti < my_tiles; ++ti) {
 #pragma unroll
@@ -283,46 +345,54 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
         for (int kt = 0; kt < nk; ++kt, ++u) {
             const int s = u % S;
             const int sn = (u + 1) % S;
-            int64_t rm0, rn0;
-            tile_of(rt, rm0, rn0);
-            // step 0: MFMAs, with the step-1 fragment reads of this stage in between
+            // refill target: tile iteration and k-step of stage u + S
+            const int rt = (int)udiv((uint32_t)(u + S), div_nk);
+            const int rk = u + S - rt * nk;
+            set_refill_tile(rt);
 #pragma unroll
-            for (int idx = 0; idx < NMF; ++idx) {
-                const int i = idx / TN, j = idx % TN;
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                    fa0[i], fb0[j], acc[i][j], 4, 4, 0, (int)scA[i], 0, (int)scB[j]);
-#pragma unroll
-                for (int r = idx * RPM0; r < (idx + 1) * RPM0; ++r)
-                    if (r < NRD) read_frag(s, 1, r, fa1, fb1);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // this wave's reads of slot s are complete; once all waves pass the
-            // barrier slot s is free and stage u+1 has landed
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            wait_vm_barrier<(S - 2) * L>();
-            __builtin_amdgcn_sched_barrier(0);
-            // step 1: MFMAs, with the refill of slot s and the next stage's
-            // scale and step-0 fragment reads in between
-#pragma unroll
-            for (int idx = 0; idx < NMF; ++idx) {
-                const int i = idx / TN, j = idx % TN;
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                    fa1[i], fb1[j], acc[i][j], 4, 4, 2, (int)scA[i], 2, (int)scB[j]);
-                if (idx < L) issue_op(rm0, rn0, rk, s, idx);
-#pragma unroll
-                for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
-                    if (r < NRD) read_scale(sn, r, nA, nB);
-                    else if (r < 2 * NRD) read_frag(sn, 0, r - NRD, fa0, fb0);
+            for (int st = 0; st < KS; ++st) {
+                const int fb_cur = st & 1;
+                if (st == KS - 1) {
+                    // this wave's reads of slot s are complete; once all waves
+                    // pass the barrier slot s is free and stage u+1 has landed
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    wait_vm_barrier<(S - 2) * L>();
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int idx = 0; idx < NMF; ++idx) {
+                    const int i = idx / TN, j = idx % TN;
+                    acc[i][j] = mfma_scale_f4(fa[fb_cur][i], fb[fb_cur][j], acc[i][j], 4, 4, st, (int)scA[i], st,
+                                              (int)scB[j]);
+                    if (st < KS - 1) {
+                        // fragments of the next K-step of this stage
+#pragma unroll
+                        for (int r = idx * RPM0; r < (idx + 1) * RPM0; ++r)
+                            if (r < NRD) read_frag(s, st + 1, r, fa[fb_cur ^ 1], fb[fb_cur ^ 1]);
+                    } else {
+                        // refill of slot s, then the next stage's scales and
+                        // K-step-0 fragments
+#pragma unroll
+                        for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
+                            if (o < L) issue_op(rk, s, o);
+#pragma unroll
+                        for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
+                            if (r < NRD) read_scale(sn, r, nA, nB);
+                            else if (r < 2 * NRD) read_frag(sn, 0, r - NRD, fa[0], fb[0]);
+                        }
+                    }
+                    // Pin this slot's LDS reads here: the MFMA is a pure
+                    // intrinsic, so without a memory clobber the optimizer
+                    // may hoist every later K-step's reads to the top of the
+                    // stage and keep all their fragments live at once.
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i) scA[i] = nA[i];
 #pragma unroll
             for (int j = 0; j < TN; ++j) scB[j] = nB[j];
-            const bool wrap = rk + 1 == nk;
-            rk = wrap ? 0 : rk + 1;
-            rt += wrap ? 1 : 0;
         }
 
         // ---- epilogue of tile ti.  acc element e of tile (i, j) sits at
@@ -357,9 +427,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-#ifndef LSMX_F4_STAGES
-#define LSMX_F4_STAGES 4
-#endif
 // Default: 8 waves in a 4 x 2 grid (64 x 128 per wave), two waves per SIMD,
 // so one wave's MFMAs keep the matrix core busy while the other is held by
 // load back-pressure or the stage barrier (measured 8192^3: 2 x 2 waves
@@ -369,6 +436,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 #endif
 #ifndef LSMX_F4_WGN
 #define LSMX_F4_WGN 2
+#endif
+// K-steps per stage of the wide path (E8M0 scales, K % 256 == 0) and its ring
+// depth: 4 K-steps = 128-byte rows, two 64 KiB stages.
+#ifndef LSMX_F4_KS
+#define LSMX_F4_KS 4
+#endif
+#ifndef LSMX_F4_STAGES
+#define LSMX_F4_STAGES 2
 #endif
 
 static int num_cus() {
@@ -385,20 +460,23 @@ static int num_cus() {
 }
 
 hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s) {
-    constexpr int W = LSMX_F4_WGM, Z = LSMX_F4_WGN, SE = LSMX_F4_STAGES;
+    constexpr int W = LSMX_F4_WGM, Z = LSMX_F4_WGN;
     const int tiles = (int)(((g.M + f4::BM - 1) / f4::BM) * ((g.N + f4::BN - 1) / f4::BN));
     const int grid = tiles < num_cus() ? tiles : num_cus();
     const dim3 blk(64 * W * Z);
-#define LSMX_G(F, CT, S) hipLaunchKernelGGL((gemm_f4f4_kernel<F, CT, S, W, Z>), dim3(grid), blk, 0, s, g)
-#define LSMX_GC(F, S)                                             \
-    do {                                                          \
-        if (g.c_dtype == LSMX_F32) LSMX_G(F, LSMX_F32, S);        \
-        else if (g.c_dtype == LSMX_BF16) LSMX_G(F, LSMX_BF16, S); \
-        else LSMX_G(F, LSMX_F16, S);                              \
+#define LSMX_G(F, CT, S, KS) hipLaunchKernelGGL((gemm_f4f4_kernel<F, CT, S, W, Z, KS>), dim3(grid), blk, 0, s, g)
+#define LSMX_GC(F, S, KS)                                             \
+    do {                                                              \
+        if (g.c_dtype == LSMX_F32) LSMX_G(F, LSMX_F32, S, KS);        \
+        else if (g.c_dtype == LSMX_BF16) LSMX_G(F, LSMX_BF16, S, KS); \
+        else LSMX_G(F, LSMX_F16, S, KS);                              \
     } while (0)
-    if (g.scale_fmt == LSMX_SCALE_F32) LSMX_GC(LSMX_SCALE_F32, 3);  // 16-byte scale rows: one stage less
-    else if (g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) LSMX_GC(LSMX_SCALE_E8M0_KMAJOR, SE);
-    else LSMX_GC(LSMX_SCALE_E8M0, SE);
+    const bool wide = g.K % (64 * LSMX_F4_KS) == 0;
+    if (g.scale_fmt == LSMX_SCALE_F32) LSMX_GC(LSMX_SCALE_F32, 3, 2);  // 16-byte scale rows: narrow stages
+    else if (g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR && wide) LSMX_GC(LSMX_SCALE_E8M0_KMAJOR, LSMX_F4_STAGES, LSMX_F4_KS);
+    else if (g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) LSMX_GC(LSMX_SCALE_E8M0_KMAJOR, 4, 2);
+    else if (wide) LSMX_GC(LSMX_SCALE_E8M0, LSMX_F4_STAGES, LSMX_F4_KS);
+    else LSMX_GC(LSMX_SCALE_E8M0, 4, 2);
 #undef LSMX_GC
 #undef LSMX_G
     return hipGetLastError();

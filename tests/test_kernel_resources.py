@@ -1,0 +1,40 @@
+"""Every gfx950 kernel of liblsmx compiles without scratch memory.
+
+The persistent GEMMs count their outstanding direct-to-LDS loads with
+s_waitcnt vmcnt; a register spill adds scratch loads to that same counter and
+makes the compiler wait for every load in flight (measured: the 8192^3 f4 x f4
+GEMM went from 0.39 ms to 0.94 ms when a change spilled 83 VGPRs).  This test
+compiles each source for gfx950 on the CPU with hipcc's resource report and
+fails if any kernel uses scratch.
+"""
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+CSRC = ROOT / "lockstep_amd" / "csrc"
+
+
+def _hipcc():
+    h = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(h).exists():
+        pytest.skip("hipcc not available")
+    return h
+
+
+@pytest.mark.parametrize("src", ["gemm_f4f4.hip", "gemm_bf16f4.hip", "quantize.hip"])
+def test_kernels_use_no_scratch(src, tmp_path):
+    from lockstep_amd import build as B
+    flags = [f for f in B.FLAGS if f not in ("-shared", "-fPIC")]
+    res = subprocess.run([_hipcc(), *flags, "-c", "-o", str(tmp_path / "k.o"), str(CSRC / src),
+                          "-Rpass-analysis=kernel-resource-usage"], capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-2000:]
+    names = re.findall(r"Function Name: (\S+)", res.stderr)
+    scratch = [int(x) for x in re.findall(r"ScratchSize \[bytes/lane\]: (\d+)", res.stderr)]
+    assert names and len(names) == len(scratch), "resource report not found"
+    bad = [(n, s) for n, s in zip(names, scratch) if s]
+    assert not bad, f"kernels using scratch: {bad}"
