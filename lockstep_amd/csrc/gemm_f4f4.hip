@@ -101,11 +101,11 @@ LSMX_DEV void dma_x1(uint32_t off, v4i_rsrc r, uint32_t m0) {
                  "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
 }
 
-LSMX_DEV uint32_t bf16_rne(float f) {
-    uint32_t u = f2u(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;  // quiet NaN
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
+// fp32 -> bf16 with round-to-nearest-even (the reference's `acc.to(bf16)`):
+// one v_cvt_pk_bf16_f32 per pair of values on gfx950.
+typedef __bf16 v2bf16 __attribute__((ext_vector_type(2)));
+LSMX_DEV uint32_t bf16x2(float lo, float hi) { return __builtin_bit_cast(uint32_t, v2bf16{(__bf16)lo, (__bf16)hi}); }
+LSMX_DEV uint32_t bf16_rne(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f); }
 
 LSMX_DEV uint32_t f16_bits(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f); }
 
@@ -123,7 +123,7 @@ LSMX_DEV void store_c4(void *c, int64_t idx, float v0, float v1, float v2, float
         *reinterpret_cast<u32x4 *>(reinterpret_cast<float *>(c) + idx) = u32x4{f2u(v0), f2u(v1), f2u(v2), f2u(v3)};
     } else if constexpr (CT == LSMX_BF16) {
         *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(c) + idx) =
-            u32x2{bf16_rne(v0) | (bf16_rne(v1) << 16), bf16_rne(v2) | (bf16_rne(v3) << 16)};
+            u32x2{bf16x2(v0, v1), bf16x2(v2, v3)};
     } else {
         *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(c) + idx) =
             u32x2{f16_bits(v0) | (f16_bits(v1) << 16), f16_bits(v2) | (f16_bits(v3) << 16)};
@@ -188,7 +188,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     static_assert(KS == 2 || KS == 4, "2 or 4 K-steps per stage");
     // scale loads: with 4 waves every wave loads 64 rows of A's and of B's
     // scales per slice; with 8 waves waves 0-3 load A's and waves 4-7 B's.
-    constexpr int LS = (NW == 4 ? 2 : 1) * NSL;
+    // K-major E8M0 scales with KS = 4 and 8 waves: one 1 KiB slice (256 rows)
+    // per dwordx4 load; wave w takes operand (w >> 1) & 1, slice w & 1, so
+    // waves w and w + 4 write the same bytes to the same place (8 scale loads
+    // per stage instead of 16, and no branch in the stage loop).
+    constexpr bool SX4 = SKM && KS == 4 && NW == 8;
+    constexpr int LS = SX4 ? 1 : (NW == 4 ? 2 : 1) * NSL;
     constexpr int L = 2 * XA + LS;                   // loads per thread per stage
     constexpr int NRD = TM + TN;                     // fragment (and scale) reads per K-step / stage
     constexpr int OPM = (L + NMF - 1) / NMF;         // refill ops per MFMA, last K-step
@@ -255,6 +260,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             }
             return;
         }
+        if constexpr (SX4) {
+            // q == 2*XA: operand (wave >> 1) & 1, slice wave & 1
+            const bool xb = (wave >> 1) & 1;
+            const int j = wave & 1;
+            const int64_t sld = xb ? g.ld_sb : g.ld_sa;
+            const int64_t sb0 = (((int64_t)kt * NSL + j) * sld + (xb ? rn0 : rm0)) * 4;
+            const v4i_rsrc rs = buf_rsrc(reinterpret_cast<const uint8_t *>(xb ? g.sb : g.sa) + sb0,
+                                         (xb ? sbytes_b : sbytes_a) - (uint64_t)sb0);
+            dma_x4((uint32_t)lane * 16, rs, lds_u32(xb ? &sSB[s][j][0] : &sSA[s][j][0]));
+            return;
+        }
         const int r = q - 2 * XA;
         const bool to_b = NW == 4 ? (r & 1) : s_is_b;
         const int j = NW == 4 ? (r >> 1) : r;  // scale slice within the stage
@@ -306,7 +322,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 
     v16f acc[TM][TN];
     uint32_t scA[TM], scB[TN], nA[TM], nB[TN];
-    v4i fa[2][TM], fb[2][TN];
+    // fragment buffers: KS = 4 keeps three K-steps' fragments at once (see the stage loop)
+    v4i fa[KS == 4 ? 3 : 2][TM], fb[KS == 4 ? 3 : 2][TN];
 
     // ---- prologue: fill the ring, publish stage 0, read its step-0 operands
     {
@@ -349,44 +366,105 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             const int rt = (int)udiv((uint32_t)(u + S), div_nk);
             const int rk = u + S - rt * nk;
             set_refill_tile(rt);
+            if constexpr (KS == 4) {
+                // K-step 0 reads step 1's fragments, step 1 reads steps 2 and
+                // 3's, so slot s is fully read before step 2.  The barrier
+                // sits there, and the slot's refill is spread over steps 2
+                // and 3 (one load per MFMA) instead of being issued in one
+                // burst: a burst of direct-to-LDS loads blocks issue on every
+                // wave at once and the matrix core goes idle.  Buffers: step
+                // 0 -> 0, 1 -> 1, 2 -> 2, 3 -> 0 (free after step 0); the
+                // next stage's step 0 is read into 1 and moved to 0.
+                constexpr int BUF[4] = {0, 1, 2, 0};
+                constexpr int LH = (L + 1) / 2;                  // refill ops in step 2
+                constexpr int OPH = (LH + NMF - 1) / NMF;
+                constexpr int RP1 = (2 * NRD + NMF - 1) / NMF;   // reads per MFMA in step 1
 #pragma unroll
-            for (int st = 0; st < KS; ++st) {
-                const int fb_cur = st & 1;
-                if (st == KS - 1) {
-                    // this wave's reads of slot s are complete; once all waves
-                    // pass the barrier slot s is free and stage u+1 has landed
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    wait_vm_barrier<(S - 2) * L>();
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int st = 0; st < 4; ++st) {
+                    if (st == 2) {
+                        // this wave's reads of slot s are complete; once all
+                        // waves pass the barrier slot s is free and stage u+1
+                        // has landed
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        wait_vm_barrier<(S - 2) * L>();
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+#pragma unroll
+                    for (int idx = 0; idx < NMF; ++idx) {
+                        const int i = idx / TN, j = idx % TN;
+                        acc[i][j] = mfma_scale_f4(fa[BUF[st]][i], fb[BUF[st]][j], acc[i][j], 4, 4, st, (int)scA[i], st,
+                                                  (int)scB[j]);
+                        if (st == 0) {
+                            if (idx < NRD) read_frag(s, 1, idx, fa[1], fb[1]);
+                        } else if (st == 1) {
+#pragma unroll
+                            for (int r = idx * RP1; r < (idx + 1) * RP1; ++r) {
+                                if (r < NRD) read_frag(s, 2, r, fa[2], fb[2]);
+                                else if (r < 2 * NRD) read_frag(s, 3, r - NRD, fa[0], fb[0]);
+                            }
+                        } else if (st == 2) {
+#pragma unroll
+                            for (int o = idx * OPH; o < (idx + 1) * OPH; ++o)
+                                if (o < LH) issue_op(rk, s, o);
+                            if (idx < NRD) read_scale(sn, idx, nA, nB);
+                        } else {
+#pragma unroll
+                            for (int o = LH + idx * OPH; o < LH + (idx + 1) * OPH; ++o)
+                                if (o < L) issue_op(rk, s, o);
+                            if (idx < NRD) read_frag(sn, 0, idx, fa[1], fb[1]);
+                        }
+                        // Pin this slot's LDS reads here: the MFMA is a pure
+                        // intrinsic, so without a memory clobber the optimizer
+                        // may hoist every later K-step's reads to the top of
+                        // the stage and keep all their fragments live at once.
+                        asm volatile("" ::: "memory");
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
 #pragma unroll
-                for (int idx = 0; idx < NMF; ++idx) {
-                    const int i = idx / TN, j = idx % TN;
-                    acc[i][j] = mfma_scale_f4(fa[fb_cur][i], fb[fb_cur][j], acc[i][j], 4, 4, st, (int)scA[i], st,
-                                              (int)scB[j]);
-                    if (st < KS - 1) {
-                        // fragments of the next K-step of this stage
+                for (int i = 0; i < TM; ++i) fa[0][i] = fa[1][i];
 #pragma unroll
-                        for (int r = idx * RPM0; r < (idx + 1) * RPM0; ++r)
-                            if (r < NRD) read_frag(s, st + 1, r, fa[fb_cur ^ 1], fb[fb_cur ^ 1]);
-                    } else {
-                        // refill of slot s, then the next stage's scales and
-                        // K-step-0 fragments
-#pragma unroll
-                        for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
-                            if (o < L) issue_op(rk, s, o);
-#pragma unroll
-                        for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
-                            if (r < NRD) read_scale(sn, r, nA, nB);
-                            else if (r < 2 * NRD) read_frag(sn, 0, r - NRD, fa[0], fb[0]);
-                        }
+                for (int j = 0; j < TN; ++j) fb[0][j] = fb[1][j];
+            } else {
+    #pragma unroll
+                for (int st = 0; st < KS; ++st) {
+                    const int fb_cur = st & 1;
+                    if (st == KS - 1) {
+                        // this wave's reads of slot s are complete; once all waves
+                        // pass the barrier slot s is free and stage u+1 has landed
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        wait_vm_barrier<(S - 2) * L>();
+                        __builtin_amdgcn_sched_barrier(0);
                     }
-                    // Pin this slot's LDS reads here: the MFMA is a pure
-                    // intrinsic, so without a memory clobber the optimizer
-                    // may hoist every later K-step's reads to the top of the
-                    // stage and keep all their fragments live at once.
-                    asm volatile("" ::: "memory");
-                    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                    for (int idx = 0; idx < NMF; ++idx) {
+                        const int i = idx / TN, j = idx % TN;
+                        acc[i][j] = mfma_scale_f4(fa[fb_cur][i], fb[fb_cur][j], acc[i][j], 4, 4, st, (int)scA[i], st,
+                                                  (int)scB[j]);
+                        if (st < KS - 1) {
+                            // fragments of the next K-step of this stage
+    #pragma unroll
+                            for (int r = idx * RPM0; r < (idx + 1) * RPM0; ++r)
+                                if (r < NRD) read_frag(s, st + 1, r, fa[fb_cur ^ 1], fb[fb_cur ^ 1]);
+                        } else {
+                            // refill of slot s, then the next stage's scales and
+                            // K-step-0 fragments
+    #pragma unroll
+                            for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
+                                if (o < L) issue_op(rk, s, o);
+    #pragma unroll
+                            for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
+                                if (r < NRD) read_scale(sn, r, nA, nB);
+                                else if (r < 2 * NRD) read_frag(sn, 0, r - NRD, fa[0], fb[0]);
+                            }
+                        }
+                        // Pin this slot's LDS reads here: the MFMA is a pure
+                        // intrinsic, so without a memory clobber the optimizer
+                        // may hoist every later K-step's reads to the top of the
+                        // stage and keep all their fragments live at once.
+                        asm volatile("" ::: "memory");
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
 #pragma unroll
