@@ -97,7 +97,8 @@ static int quantize_common(const void *x, int x_dtype, int64_t rows, int64_t K, 
         const int code_b = codes_fmt == LSMX_CODES_PACKED ? block / 2 : 16;
         if (!aligned(codes, code_b) || ld_codes % code_b) return fail(LSMX_ERR_ALIGN, "%s: codes rows must be %d-byte aligned", fn, code_b);
     }
-    if (scale_fmt == LSMX_SCALE_F32 && !aligned(scale, 4)) return fail(LSMX_ERR_ALIGN, "%s: fp32 scale misaligned", fn);
+    if ((scale_fmt == LSMX_SCALE_F32 || scale_fmt == LSMX_SCALE_E8M0_KMAJOR) && !aligned(scale, 4))
+        return fail(LSMX_ERR_ALIGN, "%s: fp32 and K-major scales must be 4-byte aligned", fn);
     if (int r = device_guard()) return r;
     if (rows == 0 || K == 0) return LSMX_OK;
     lsmx::QuantArgs a{x, x_dtype, rows, K, ldx, block, codes, codes_fmt, ld_codes, scale, scale_fmt, ld_scale};

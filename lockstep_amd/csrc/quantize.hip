@@ -96,11 +96,62 @@ struct CodeStore<8> {
     }
 };
 
+// E codes of the finite block elements b[0..E-1] (fp32 bits) packed into
+// nibbles (element i in nibble i), for the block's E8M0 byte e8 < 255.
+// v_cvt_scalef32_pk_fp4_f32 converts x / 2^(e8-127) to E2M1 with round-to-
+// nearest-even, saturating at 6 and copying the sign (-0 -> code 8); the low
+// nibble of each byte is its first source (all measured on gfx950).  fp4.py
+// rounds ties toward the smaller magnitude instead (fp4.py:50-53); the two
+// differ only where x / 2^e is exactly 0.75, 1.75 or 3.5 -- there ties-to-
+// even picks the larger code -- so those elements, found by comparing the
+// bits of |x| with the three tie values of the block, take one code less.
+template <int I, int E>
+LSMX_DEV uint32_t cvt_fp4_pairs(uint32_t w, const uint32_t (&b)[E], float sc) {
+    if constexpr (I < E) {
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, u2f(b[I]), u2f(b[I + 1]), sc, I / 2);  // byte I/2
+        return cvt_fp4_pairs<I + 2, E>(w, b, sc);
+    } else {
+        return w;
+    }
+}
+
+template <int E>
+LSMX_DEV uint32_t e2m1_pack_hw(const uint32_t (&b)[E], uint32_t e8) {
+    const float sc = u2f(e8 << 23);  // 2^(e8-127); e8 is 25..254 for a non-zero finite block, 127 for zero
+    const uint32_t w = cvt_fp4_pairs<0, E>(0u, b, sc);
+    // A tie has mantissa 0x400000 or 0x600000: bit 22 set, bits 0-20 clear.
+    // Most waves hold no such element and skip the exact comparison.
+    bool maybe_tie = false;
+#pragma unroll
+    for (int i = 0; i < E; ++i) maybe_tie |= (b[i] & 0x005FFFFFu) == 0x00400000u;
+    if (!__any(maybe_tie)) return w;
+    const uint32_t t1 = ((e8 - 1) << 23) | 0x400000u;  // 0.75 * 2^e
+    const uint32_t t2 = (e8 << 23) | 0x600000u;        // 1.75 * 2^e
+    const uint32_t t3 = ((e8 + 1) << 23) | 0x600000u;  // 3.5  * 2^e
+    uint32_t dec = 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const uint32_t ax = b[i] & 0x7FFFFFFFu;
+        dec |= (ax == t1 || ax == t2 || ax == t3) ? (1u << (4 * i)) : 0u;
+    }
+    return w - dec;  // a tie's code magnitude is 2, 4 or 6: no borrow into the next nibble
+}
+
+// The same codes from the element-by-element rule (lsmx::e2m1_code), which
+// also covers a NaN block (e8 == 255).
+template <int E>
+LSMX_DEV uint32_t e2m1_pack_exact(const uint32_t (&b)[E], uint32_t e8) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) w |= e2m1_code(b[i], e8) << (4 * i);
+    return w;
+}
+
 // ------------------------------------------------------- row-mode quantize
 // Grid: (x = chunks of kThreads*kUnroll vectors along a row, y = rows, grid-
 // strided).  One vector = 16 input bytes.
 constexpr int kQThreads = 256;
-constexpr int kQUnroll = 4;
+constexpr int kQUnroll = 2;  // measured: 2 vectors per thread beat 1, 4 and 8 (more, shorter workgroups)
 
 // Scale store for block kb of row r in format SFMT (LSMX_SCALE_*).
 template <int SFMT>
@@ -144,15 +195,39 @@ __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
 #pragma unroll
             for (int i = 0; i < E; ++i) am = max(am, b[i] & 0x7FFFFFFFu);
             am = group_max<G>(am);  // every lane of the block participates
-            if (v >= vpr) continue;  // whole blocks are in or out of range
             const uint32_t e8 = block_e8m0(am);
-            uint32_t c[E];
-#pragma unroll
-            for (int i = 0; i < E; ++i) c[i] = e2m1_code(b[i], e8);
+            // K-major scales: the lane holding block kb (kb % 4 == 0) gathers
+            // the bytes of kb..kb+3 -- the same row's dword -- for one store.
+            // Every lane takes part in the cross-lane reads.
+            uint32_t e4 = 0;
+            if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR && BLOCK == 32) {
+                const int l = (int)(threadIdx.x & 63);
+                e4 = e8 | ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + G) & 63) << 2, (int)e8) << 8) |
+                     ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + 2 * G) & 63) << 2, (int)e8) << 16) |
+                     ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + 3 * G) & 63) << 2, (int)e8) << 24);
+            }
+            if (v >= vpr) continue;  // whole blocks are in or out of range
+            // NaN blocks are rare: any lane with one takes the whole wave
+            // through the exact per-element rule
+            const uint32_t w = __any(e8 == 255u) ? e2m1_pack_exact<E>(b, e8) : e2m1_pack_hw<E>(b, e8);
             const int64_t col = v * E;
-            if constexpr (PACKED) CodeStore<E>::packed(codes + r * ld_codes + col / 2, c);
-            else CodeStore<E>::unpacked(codes + r * ld_codes + col, c);
-            if ((threadIdx.x % G) == 0) store_scale<SFMT>(scale, r, col / BLOCK, ld_scale, e8);
+            if constexpr (PACKED) {
+                if constexpr (E == 4) *reinterpret_cast<uint16_t *>(codes + r * ld_codes + col / 2) = (uint16_t)w;
+                else *reinterpret_cast<uint32_t *>(codes + r * ld_codes + col / 2) = w;
+            } else {
+                uint32_t c[E];
+#pragma unroll
+                for (int i = 0; i < E; ++i) c[i] = (w >> (4 * i)) & 0xF;
+                CodeStore<E>::unpacked(codes + r * ld_codes + col, c);
+            }
+            if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR && BLOCK == 32) {
+                const int64_t kb = col / BLOCK;
+                // vectors of a wave start on a 4-block boundary (64 lanes x E elements)
+                if ((threadIdx.x % (4 * G)) == 0)
+                    reinterpret_cast<uint32_t *>(scale)[(kb >> 2) * ld_scale + r] = e4;
+            } else {
+                if ((threadIdx.x % G) == 0) store_scale<SFMT>(scale, r, col / BLOCK, ld_scale, e8);
+            }
         }
     }
 }

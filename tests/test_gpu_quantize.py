@@ -213,3 +213,50 @@ def test_quantize_kmajor_scale_layout(dev, fp4mod, oracle):
         assert np.array_equal(e8.cpu().numpy(), want), (rows, K)
         assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(rc)), (rows, K)
         assert torch.equal(fp4mod.kmajor_scales(fp4mod.quantize_pack_mxfp4(to_dev(x, "f32", dev))[1]), e8)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_exact_ties_round_toward_smaller_magnitude(dev, fp4mod, oracle, dtype):
+    """Elements at exactly 0.75, 1.75 and 3.5 times their block scale (fp4.py
+    rounds those ties down, fp4.py:50-53) spread thinly over random blocks, so
+    most waves hold none and a few hold one or two.  Packed codes, E8M0 bytes
+    and the K-major layout equal the oracle's."""
+    rows, K = 96, 1024
+    x = gen.normal(4242, (rows, K)).astype(np.float32)
+    # round to the input dtype first, so the block scales below are the ones
+    # the dtype's values give (tie values have 2 significant bits: exact in all three)
+    if dtype == "bf16":
+        x = (gen.to_bf16_bits(x).astype(np.uint32) << 16).view(np.float32)
+    elif dtype == "f16":
+        x = x.astype(np.float16).astype(np.float32)
+    ref_codes, ref_scale = oracle.quantize_mxfp4(x)
+    e = np.log2(ref_scale).astype(np.int32)                      # block exponents, [rows, K/32]
+    rng = np.random.default_rng(7)
+    n_ties = 60
+    rr = rng.integers(0, rows, n_ties)
+    kk = rng.integers(0, K, n_ties)
+    # never overwrite a block's largest element: the tie values lie below
+    # the block's amax (>= 4 * 2^e), so every block scale is unchanged
+    amax = np.abs(x).reshape(rows, K // 32, 32).max(axis=2)
+    keep = np.abs(x[rr, kk]) < amax[rr, kk // 32]
+    rr, kk = rr[keep], kk[keep]
+    mult = rng.choice([0.75, 1.75, 3.5], len(rr)) * rng.choice([-1.0, 1.0], len(rr))
+    x[rr, kk] = (mult * np.exp2(e[rr, kk // 32].astype(np.float64))).astype(np.float32)
+    if dtype == "bf16":
+        xh = gen.to_bf16_bits(x)
+    elif dtype == "f16":
+        xh = x.astype(np.float16).view(np.uint16)
+    else:
+        xh = x
+    ref_codes, ref_scale = oracle.quantize_mxfp4(xh, 32, None if dtype == "f32" else dtype)
+    assert np.array_equal(np.log2(ref_scale).astype(np.int32), e), "block scales must not move"
+    q = ref_codes[rr, kk] & 7
+    assert len(rr) > 40 and np.all(np.isin(q, [1, 3, 5])), "planted values must be ties the reference rounds down"
+    xt = to_dev(xh, dtype, dev)
+    packed, e8 = fp4mod.quantize_pack_mxfp4(xt)
+    assert np.array_equal(packed.cpu().numpy(), oracle.pack_fp4(ref_codes))
+    assert np.array_equal(e8.cpu().numpy(), oracle.scale_to_e8m0(ref_scale))
+    pk, e8k = fp4mod.quantize_pack_mxfp4(xt, scale_layout="kmajor")
+    assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(ref_codes))
+    want = oracle.scale_to_e8m0(ref_scale).reshape(rows, K // 128, 4).transpose(1, 0, 2)
+    assert np.array_equal(e8k.cpu().numpy(), want)
