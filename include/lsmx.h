@@ -41,6 +41,7 @@ extern "C" {
 #define LSMX_F32 0
 #define LSMX_BF16 1
 #define LSMX_F16 2
+#define LSMX_E4M3 3  /* FP8 E4M3 (torch.float8_e4m3fn): dense GEMM operands only */
 
 /* code formats */
 #define LSMX_CODES_PACKED 0    /* [rows, K/2] bytes, even element in the low nibble */
@@ -113,12 +114,12 @@ int lsmx_dequantize_mxfp4(const void *codes, int codes_fmt, int64_t ld_codes, co
 int lsmx_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n_words, void *stream);
 
 /* Block-scaled FP4 x FP4 GEMM:  C[M, N] = sum_kb sa[m,kb] sb[n,kb] (A_kb . Bt_kb).
- * Replaces mxfp4_gemm.py:220-233 mxfp4_gemm_packed / _mxfp4_gemm_packed_kernel
- * (mxfp4_gemm.py:175-217) and cuda/mxfp4_mma_gemm.cu:69-184.
+ * Replaces mxfp4_gemm.py:161-174 mxfp4_gemm_packed / _mxfp4_gemm_packed_kernel
+ * (mxfp4_gemm.py:116-158) and cuda/mxfp4_mma_gemm.cu:69-184.
  *   a_pk  [M, lda] bytes (lda >= K/2),   a_scale [M, ld_sa] (E8M0 or fp32)
  *   bt_pk [N, ldb] bytes (ldb >= K/2),   b_scale [N, ld_sb]
  *   c     [M, ldc] of c_dtype (LSMX_F32 | LSMX_BF16 | LSMX_F16), fp32 accumulate.
- *   K % 128 == 0 (mxfp4_gemm.py:225); any M, N >= 1.
+ *   K % 128 == 0 (mxfp4_gemm.py:166); any M, N >= 1.
  * fp32 scales must hold powers of two (what fp4.py produces); they are read
  * as their exponent field. */
 int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_t ld_sa,
@@ -145,6 +146,50 @@ int lsmx_gemm_dual_bf16f4(const void *a0, const void *a1, int64_t lda, const uin
                           int64_t ldw, const void *w_scale, int64_t ld_sw, int scale_fmt,
                           void *c0, void *c1, int c_dtype, int64_t ldc, int64_t M, int64_t N,
                           int64_t K, void *stream);
+
+/* Dense GEMM with fp32 accumulation and fp32 output, operands K-contiguous:
+ *   a0, a1 [M, lda] and bt0, bt1 [N, ldb] of dtype LSMX_BF16 | LSMX_F16 | LSMX_E4M3.
+ *   mode 0: c0 = a0 . bt0^T                       dual_gemm.py:189-226 gemm
+ *   mode 1: c0 = a0 . bt0^T + a1 . bt1^T          dual_gemm.py:43-72, 230-241 dual_packed
+ *           (one accumulator; the caller pre-scales a1 by 2^s as the reference does)
+ *   mode 2: c0 = a0 . bt0^T,  c1 = a1 . bt1^T     dual_gemm.py:79-110, 244-255 dual_separate
+ * splits > 1: K is cut into `splits` equal slices whose partial sums are added
+ * into c0 (and c1) with fp32 atomics, so the outputs must hold zeros on entry
+ * (dual_gemm.py:118-179, 261-289 splitk_packed / splitk_separate; the order of
+ * the additions, hence the last bits, varies from run to run as there).
+ * The reference takes B as [K, N]; pass its transpose (lsmx_transpose).
+ * K % (64 * splits) == 0 (dual_gemm.py:219, 265); rows 16-byte aligned. */
+int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0, const void *bt1, int64_t ldb,
+                    int dtype, int mode, float *c0, float *c1, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                    int splits, void *stream);
+
+/* MXFP4 GEMM on E4M3 operands holding E2M1 values, with E8M0 block scales:
+ *   C[M, N] = sum_kb 2^(sa[m,kb]-127) 2^(sb[n,kb]-127) (A_kb . Bt_kb)
+ * Replaces mxfp4_gemm.py:74-87 mxfp4_gemm_fp8 / _mxfp4_gemm_fp8_kernel
+ * (mxfp4_gemm.py:29-71), which promotes each 32-block product to fp32 and
+ * multiplies fp32 scales; here the scaled MFMA applies the exponents.
+ *   a [M, lda] and bt [N, ldb] E4M3 bytes (K-contiguous; the reference's
+ *   b_fp8 [K, N] transposed), a_e8m0 [M, ld_sa], b_e8m0 [N, ld_sb] bytes
+ *   (lsmx_scale_to_e8m0 of fp4.py's fp32 power-of-two scales),
+ *   c [M, ldc] of c_dtype (LSMX_F32 | LSMX_BF16 | LSMX_F16).  K % 128 == 0
+ *   (mxfp4_gemm.py:78). */
+int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *bt,
+                   int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, void *c, int c_dtype, int64_t ldc, int64_t M,
+                   int64_t N, int64_t K, void *stream);
+
+/* y[cols, ldy] = x[rows, ldx]^T for elements of elem_bytes = 1, 2 or 4 bytes.
+ * Lays out the reference's N-contiguous B operands ([K, N], dual_gemm.py:
+ * 189-289, mxfp4_gemm.py:29-87) K-contiguous for the kernels above. */
+int lsmx_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, int64_t ldx, void *y, int64_t ldy,
+                   void *stream);
+
+/* E8M0 bytes of fp32 power-of-two scales (their exponent field), the exact
+ * inverse of fp4.py:61-69's 2^e: out[r, c] = e8m0(s[r, c]), or with
+ * transpose = 1 out[c, r] = e8m0(s[r, c]) (mxfp4_gemm.py:79's b_scale
+ * [K/32, N] to [N, K/32]).  A scale that is not a power of two keeps only its
+ * exponent. */
+int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+                       int64_t ldo, void *stream);
 
 #ifdef __cplusplus
 }

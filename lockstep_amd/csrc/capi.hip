@@ -220,6 +220,84 @@ int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_
     return launched(lsmx::launch_gemm_f4f4(g, (hipStream_t)stream), fn);
 }
 
+static int rows16(const void *p, int64_t ld, int es) { return aligned(p, 16) && (ld * es) % 16 == 0; }
+
+int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0, const void *bt1, int64_t ldb,
+                    int dtype, int mode, float *c0, float *c1, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                    int splits, void *stream) {
+    const char *fn = "lsmx_gemm_dense";
+    if (dtype != LSMX_BF16 && dtype != LSMX_F16 && dtype != LSMX_E4M3)
+        return fail(LSMX_ERR_DTYPE, "%s: dtype must be bf16, fp16 or e4m3", fn);
+    if (mode < 0 || mode > 2) return fail(LSMX_ERR_ARG, "%s: mode must be 0, 1 or 2", fn);
+    if (!a0 || !bt0 || !c0 || (mode && (!a1 || !bt1)) || (mode == 2 && !c1))
+        return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % 64) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 64 (max BLOCK_K); zero-pad if shorter");
+    if (splits < 1 || K % (64 * (int64_t)splits)) return fail(LSMX_ERR_SHAPE, "K must divide splits*BK");
+    if (splits > 65535) return fail(LSMX_ERR_SHAPE, "%s: at most 65535 splits", fn);
+    if (((M + 127) / 128) * ((N + 127) / 128) > 0x7FFFFFFF)
+        return fail(LSMX_ERR_SHAPE, "%s: more than 2^31 - 1 output tiles", fn);
+    if (lda < K || ldb < K || ldc < N) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    const int es = dtype == LSMX_E4M3 ? 1 : 2;
+    if (!rows16(a0, lda, es) || !rows16(bt0, ldb, es) || (mode && (!rows16(a1, lda, es) || !rows16(bt1, ldb, es))))
+        return fail(LSMX_ERR_ALIGN, "%s: operand rows must be 16-byte aligned", fn);
+    if (!aligned(c0, 4) || (c1 && !aligned(c1, 4))) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
+    lsmx::DenseArgs g{reinterpret_cast<const uint8_t *>(a0), reinterpret_cast<const uint8_t *>(a1), lda,
+                      reinterpret_cast<const uint8_t *>(bt0), reinterpret_cast<const uint8_t *>(bt1), ldb,
+                      nullptr, nullptr, 0, 0, c0, c1, LSMX_F32, ldc, M, N, K, K / splits};
+    return launched(lsmx::launch_gemm_dense(g, dtype, mode, (hipStream_t)stream), fn);
+}
+
+int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *bt,
+                   int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, void *c, int c_dtype, int64_t ldc, int64_t M,
+                   int64_t N, int64_t K, void *stream) {
+    const char *fn = "lsmx_gemm_f8f8";
+    if (!a || !a_e8m0 || !bt || !b_e8m0 || !c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % 128) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
+    if (((M + 127) / 128) * ((N + 127) / 128) > 0x7FFFFFFF)
+        return fail(LSMX_ERR_SHAPE, "%s: more than 2^31 - 1 output tiles", fn);
+    if (lda < K || ldb < K || ldc < N || ld_sa < K / 32 || ld_sb < K / 32)
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (!rows16(a, lda, 1) || !rows16(bt, ldb, 1)) return fail(LSMX_ERR_ALIGN, "%s: operand rows must be 16-byte aligned", fn);
+    if (!aligned(c, c_dtype == LSMX_F32 ? 4 : 2)) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
+    lsmx::DenseArgs g{a, nullptr, lda, bt, nullptr, ldb, a_e8m0, b_e8m0, ld_sa, ld_sb, c, nullptr, c_dtype, ldc,
+                      M, N, K, K};
+    return launched(lsmx::launch_gemm_f8f8_scaled(g, (hipStream_t)stream), fn);
+}
+
+int lsmx_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, int64_t ldx, void *y, int64_t ldy,
+                   void *stream) {
+    const char *fn = "lsmx_transpose";
+    if (!x || !y) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) return fail(LSMX_ERR_DTYPE, "%s: elem_bytes", fn);
+    if (rows < 0 || cols < 0 || ldx < cols || ldy < rows) return fail(LSMX_ERR_SHAPE, "%s: bad shape", fn);
+    if (!aligned(x, elem_bytes) || !aligned(y, elem_bytes)) return fail(LSMX_ERR_ALIGN, "%s: misaligned", fn);
+    if (rows > (int64_t)65535 * 32 || cols > (int64_t)0x7FFFFFFF * 32) return fail(LSMX_ERR_SHAPE, "%s: too large", fn);
+    if (int r = device_guard()) return r;
+    if (rows == 0 || cols == 0) return LSMX_OK;
+    return launched(lsmx::launch_transpose(x, elem_bytes, rows, cols, ldx, y, ldy, (hipStream_t)stream), fn);
+}
+
+int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+                       int64_t ldo, void *stream) {
+    const char *fn = "lsmx_scale_to_e8m0";
+    if (!s || !out) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (rows < 0 || cols < 0 || lds < cols || ldo < (transpose ? rows : cols)) return fail(LSMX_ERR_SHAPE, "%s: bad shape", fn);
+    if (!aligned(s, 4)) return fail(LSMX_ERR_ALIGN, "%s: misaligned", fn);
+    if (rows > 0 && cols > ((int64_t)1 << 38) / rows) return fail(LSMX_ERR_SHAPE, "%s: too large", fn);
+    if (int r = device_guard()) return r;
+    if (rows == 0 || cols == 0) return LSMX_OK;
+    return launched(lsmx::launch_scale_to_e8m0(s, rows, cols, lds, transpose, out, ldo, (hipStream_t)stream), fn);
+}
+
 static int w4_common(const char *fn, const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
                      const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype, int64_t ldc,
                      int64_t M, int64_t N, int64_t K, void *stream) {

@@ -1,0 +1,358 @@
+// Dense GEMMs with fp32 accumulation on gfx950's MFMA: the kernels behind the
+// reference's dual_gemm.py family and mxfp4_gemm_fp8.
+//
+//   single        C  = A0 . Bt0^T                       dual_gemm.py:189-226 (gemm)
+//   dual packed   C  = A0 . Bt0^T + A1 . Bt1^T  (one accumulator)
+//                                                       dual_gemm.py:43-72, 230-241
+//   dual separate C0 = A0 . Bt0^T,  C1 = A1 . Bt1^T      dual_gemm.py:79-110, 244-255
+//   split-K       any of the above over K slices, fp32 atomic adds into a
+//                 zeroed output                          dual_gemm.py:118-179, 261-289
+//   fp8 scaled    C  = sum_kb sa[m,kb] sb[n,kb] (A_kb . Bt_kb), E4M3 operands,
+//                 E8M0 block scales                      mxfp4_gemm.py:29-87
+//
+// Operands are K-contiguous: A [M, lda], Bt [N, ldb].  The reference takes B
+// as [K, N] (N-contiguous); the Python layer hands a transposed copy (or the
+// K-contiguous tensor B is a view of) to these kernels.
+//
+// Element types: bf16 and fp16 (v_mfma_f32_32x32x16_{bf16,f16}: each lane
+// supplies 8 consecutive K of one row) and E4M3 (v_mfma_scale_f32_32x32x64_
+// f8f6f4 with cbsz = blgp = 0: each lane supplies 16 K of each of the two
+// 32-blocks, and the E8M0 scale of block lane / 32, 127 = 1.0 when unscaled).
+//
+// Tiling: 128 x 128 per workgroup of 4 waves (2 x 2, 64 x 64 per wave, 2 x 2
+// MFMA tiles of 32 x 32).  A stage is 64 elements of K (128 bytes of a bf16
+// row, 64 of an E4M3 row), staged through VGPRs into a double-buffered LDS
+// tile; the next stage's global loads are in flight while this one computes.
+// Rows past M or N are clamped to the last row (their outputs are not
+// stored).  LDS rows are XOR-swizzled by 16-byte chunk.
+#include "lsmx_internal.h"
+
+namespace lsmx {
+
+namespace dn {
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 128, BKE = 64;  // tile and stage (elements of K)
+constexpr int NT = 256;                       // 4 waves
+constexpr int TM = 2, TN = 2;                 // 32 x 32 MFMA tiles per wave
+
+LSMX_DEV int swz(int row, int cpr) { return (row >> 1) & (cpr - 1); }
+
+template <int DT>
+struct Ty {
+    static constexpr int es = DT == LSMX_E4M3 ? 1 : 2;  // element bytes
+    static constexpr int RB = BKE * es;                  // bytes per row per stage
+    static constexpr int CPR = RB / 16;                  // 16-byte chunks per row
+    static constexpr int KS = DT == LSMX_E4M3 ? 1 : 4;   // MFMA K-steps per stage
+    static constexpr int LPT = BM * RB / 16 / NT;        // 16-byte loads per thread per operand
+};
+
+template <int DT>
+LSMX_DEV v16f mma(const u32x4 (&a)[2], const u32x4 (&b)[2], v16f c, uint32_t sa, uint32_t sb) {
+    if constexpr (DT == LSMX_BF16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a[0]), __builtin_bit_cast(v8bf, b[0]), c,
+                                                       0, 0, 0);
+    } else if constexpr (DT == LSMX_F16) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a[0]), __builtin_bit_cast(v8h, b[0]), c,
+                                                      0, 0, 0);
+    } else {
+        const v8i va = v8i{(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],
+                           (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]};
+        const v8i vb = v8i{(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
+                           (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va, vb, c, 0, 0, 0, (int)sa, 0, (int)sb);
+    }
+}
+
+LSMX_DEV uint32_t bf16_bits(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f); }
+LSMX_DEV uint32_t f16_bits(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f); }
+
+template <int CT, bool ATOMIC>
+LSMX_DEV void put(void *c, int64_t idx, float v) {
+    if constexpr (ATOMIC) {
+        __hip_atomic_fetch_add(reinterpret_cast<float *>(c) + idx, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if constexpr (CT == LSMX_F32) {
+        reinterpret_cast<float *>(c)[idx] = v;
+    } else if constexpr (CT == LSMX_BF16) {
+        reinterpret_cast<uint16_t *>(c)[idx] = (uint16_t)bf16_bits(v);
+    } else {
+        reinterpret_cast<uint16_t *>(c)[idx] = (uint16_t)f16_bits(v);
+    }
+}
+}  // namespace dn
+
+// MODE: 0 single, 1 dual packed, 2 dual separate.  SHB: the two B operands
+// are one tensor (the shared-weight form, train_step.py:52-53): each B tile is
+// loaded once and feeds both products.  SCALED: E8M0 block scales (E4M3
+// only).  ATOMIC: split-K partial sums added into a zeroed fp32 output.
+template <int DT, int MODE, bool SHB>
+constexpr int dense_lds_bytes() {
+    return 2 * ((MODE == 0 ? 1 : 2) + (MODE == 0 || SHB ? 1 : 2)) * dn::BM * dn::Ty<DT>::RB;
+}
+
+// two workgroups per CU while both fit in the 160 KiB of LDS
+template <int DT, int MODE, bool SHB, bool SCALED, int CT, bool ATOMIC>
+__global__ __launch_bounds__(dn::NT, (dense_lds_bytes<DT, MODE, SHB>() <= 80 * 1024 ? 2 : 1)) void gemm_dense_kernel(
+    DenseArgs g) {
+    using namespace dn;
+    using T = Ty<DT>;
+    constexpr int NO = MODE == 0 ? 1 : 2;      // A operands
+    constexpr int NOB = SHB ? 1 : NO;          // B operands
+    constexpr int NACC = MODE == 2 ? 2 : 1;    // accumulators
+    __shared__ __attribute__((aligned(16))) uint8_t sA[2][NO][BM * T::RB];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[2][NOB][BN * T::RB];
+
+    const int tiles_m = (int)((g.M + BM - 1) / BM), tiles_n = (int)((g.N + BN - 1) / BN);
+    int tm, tn;
+    {
+        // groups of 8 tile rows share B panels in L2
+        const int pid = (int)blockIdx.x, per_group = 8 * tiles_n;
+        const int group = pid / per_group, first = group * 8;
+        const int gsz = min(tiles_m - first, 8);
+        tm = first + (pid - group * per_group) % gsz;
+        tn = (pid - group * per_group) / gsz;
+    }
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t k_begin = (int64_t)blockIdx.y * g.k_split;
+    const int nk = (int)(g.k_split / BKE);
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int frow = lane & 31, half = lane >> 5;
+
+    // staging: load q of thread t covers 16 bytes of row (q*NT + t) / CPR
+    const uint8_t *ga[NO][T::LPT], *gb[NOB][T::LPT];
+    int soff[T::LPT];
+#pragma unroll
+    for (int q = 0; q < T::LPT; ++q) {
+        const int idx = q * NT + t;
+        const int row = idx / T::CPR, c = idx % T::CPR;
+        soff[q] = row * T::RB + ((c ^ swz(row, T::CPR)) << 4);
+        const int64_t ra = min(m0 + row, g.M - 1), rb = min(n0 + row, g.N - 1);
+#pragma unroll
+        for (int o = 0; o < NO; ++o) ga[o][q] = (o ? g.a1 : g.a0) + (ra * g.lda + k_begin) * T::es + c * 16;
+#pragma unroll
+        for (int o = 0; o < NOB; ++o) gb[o][q] = (o ? g.b1 : g.b0) + (rb * g.ldb + k_begin) * T::es + c * 16;
+    }
+    u32x4 ra_[NO][T::LPT], rb_[NOB][T::LPT];
+    auto gload = [&](int kt) __attribute__((always_inline)) {
+        const int64_t off = (int64_t)kt * T::RB;
+#pragma unroll
+        for (int q = 0; q < T::LPT; ++q) {
+#pragma unroll
+            for (int o = 0; o < NO; ++o) ra_[o][q] = *reinterpret_cast<const u32x4 *>(ga[o][q] + off);
+#pragma unroll
+            for (int o = 0; o < NOB; ++o) rb_[o][q] = *reinterpret_cast<const u32x4 *>(gb[o][q] + off);
+        }
+    };
+    auto swrite = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < T::LPT; ++q) {
+#pragma unroll
+            for (int o = 0; o < NO; ++o) *reinterpret_cast<u32x4 *>(&sA[buf][o][soff[q]]) = ra_[o][q];
+#pragma unroll
+            for (int o = 0; o < NOB; ++o) *reinterpret_cast<u32x4 *>(&sB[buf][o][soff[q]]) = rb_[o][q];
+        }
+    };
+    // fragment of K-step s for tile row r: bf16/f16 one 16-byte chunk (8
+    // elements at 16s + 8h); E4M3 two chunks, elements 16h + [0, 16) of
+    // 32-block 0 in VGPRs 0-3 and 32 + 16h + [0, 16) of block 1 in VGPRs 4-7
+    // (the f8f6f4 MFMA's K order for 8-bit operands; lane half h carries the
+    // scale of block h)
+    auto frag = [&](const uint8_t *tile, int r, int s, u32x4 (&f)[2]) __attribute__((always_inline)) {
+        if constexpr (DT == LSMX_E4M3) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                f[j] = *reinterpret_cast<const u32x4 *>(tile + r * T::RB + (((2 * j + half) ^ swz(r, T::CPR)) << 4));
+        } else {
+            f[0] = *reinterpret_cast<const u32x4 *>(tile + r * T::RB + (((2 * s + half) ^ swz(r, T::CPR)) << 4));
+        }
+    };
+    // E8M0 scale of block (k / 32) for a tile row: lane half h covers block 2*kt + h
+    auto scale_of = [&](const uint8_t *s, int64_t ld, int64_t row, int kt) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (SCALED) return s[row * ld + (k_begin / 32) + 2 * kt + half];  // one byte, L2-resident
+        else return 127u;
+    };
+
+    v16f acc[NACC][TM][TN];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[a][i][j][e] = 0.0f;
+
+    // block scales are loaded one stage ahead, with that stage's operands
+    uint32_t sa[TM], sb[TN], nsa[TM], nsb[TN];
+    auto sload = [&](int kt, uint32_t (&xa)[TM], uint32_t (&xb)[TN]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xa[i] = scale_of(g.sa, g.ld_sa, min(m0 + wm * 64 + i * 32 + frow, g.M - 1), kt);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) xb[j] = scale_of(g.sb, g.ld_sb, min(n0 + wn * 64 + j * 32 + frow, g.N - 1), kt);
+    };
+    gload(0);
+    sload(0, sa, sb);
+    swrite(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) {
+            gload(kt + 1);
+            sload(kt + 1, nsa, nsb);
+        }
+#pragma unroll
+        for (int s = 0; s < T::KS; ++s) {
+            u32x4 fb[NOB][TN][2];
+#pragma unroll
+            for (int o = 0; o < NOB; ++o)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) frag(sB[buf][o], wn * 64 + j * 32 + frow, s, fb[o][j]);
+#pragma unroll
+            for (int o = 0; o < NO; ++o) {
+                u32x4 fa[TM][2];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) frag(sA[buf][o], wm * 64 + i * 32 + frow, s, fa[i]);
+                const int ai = MODE == 2 ? o : 0, bi = SHB ? 0 : o;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[ai][i][j] = mma<DT>(fa[i], fb[bi][j], acc[ai][i][j], sa[i], sb[j]);
+            }
+        }
+        if (kt + 1 < nk) {
+            swrite(buf ^ 1);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) sa[i] = nsa[i];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) sb[j] = nsb[j];
+        }
+        __syncthreads();
+    }
+
+    // epilogue: acc element e of tile (i, j) is row i*32 + 8*(e/4) + 4*half + e%4, column j*32 + frow
+#pragma unroll
+    for (int a = 0; a < NACC; ++a) {
+        void *c = a ? g.c1 : g.c0;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int64_t col = n0 + wn * 64 + j * 32 + frow;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int64_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                    if (row < g.M && col < g.N) put<CT, ATOMIC>(c, row * g.ldc + col, acc[a][i][j][e]);
+                }
+            }
+    }
+}
+
+// y[cols, ldy] = x[rows, ldx]^T for elements of ES bytes, through a 32 x 32 LDS tile.
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T *__restrict__ x, int64_t rows, int64_t cols,
+                                                        int64_t ldx, T *__restrict__ y, int64_t ldy) {
+    __shared__ T tile[32][33];
+    const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+#pragma unroll
+    for (int k = 0; k < 32; k += 8) {
+        const int64_t r = r0 + ty + k, c = c0 + tx;
+        if (r < rows && c < cols) tile[ty + k][tx] = x[r * ldx + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 32; k += 8) {
+        const int64_t c = c0 + ty + k, r = r0 + tx;
+        if (r < rows && c < cols) y[c * ldy + r] = tile[tx][ty + k];
+    }
+}
+
+// E8M0 bytes of fp32 power-of-two scales (their exponent field), optionally
+// transposed: out[r, c] = e8m0(s[r, c]) or out[c, r] = e8m0(s[r, c]).  The
+// quantizer's scales 2^e, e in [-127, 127], convert exactly (2^-127 is the
+// subnormal 0x00400000 -> 0).  A scale that is not a positive power of two in
+// that range has no E8M0 form: it becomes 0xFF, E8M0's NaN, so every output
+// that depends on it is NaN rather than silently wrong.
+__global__ void scale_to_e8m0_kernel(const float *__restrict__ s, int64_t rows, int64_t cols, int64_t lds,
+                                     int transpose, uint8_t *__restrict__ out, int64_t ldo) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = transpose ? i % rows : i / cols, c = transpose ? i / rows : i % cols;
+    const uint32_t b = f2u(s[r * lds + c]);
+    const uint32_t ex = b >> 23;  // sign is bit 8: negative scales fail both tests
+    const bool pow2 = ((b & 0x7FFFFFu) == 0 && ex >= 1 && ex <= 254) || b == 0x00400000u;
+    const uint8_t e = pow2 ? (uint8_t)ex : (uint8_t)0xFF;
+    if (transpose) out[c * ldo + r] = e;
+    else out[r * ldo + c] = e;
+}
+
+template <int DT, int MODE, bool SHB, bool SCALED, int CT, bool ATOMIC>
+static void launch_d(const DenseArgs &g, hipStream_t s) {
+    const int tiles = (int)(((g.M + dn::BM - 1) / dn::BM) * ((g.N + dn::BN - 1) / dn::BN));
+    const int splits = (int)(g.K / g.k_split);
+    hipLaunchKernelGGL((gemm_dense_kernel<DT, MODE, SHB, SCALED, CT, ATOMIC>), dim3(tiles, splits), dim3(dn::NT), 0,
+                       s, g);
+}
+
+template <int DT, int MODE, bool SHB>
+static void launch_mode(const DenseArgs &g, hipStream_t s) {
+    if (g.k_split != g.K) launch_d<DT, MODE, SHB, false, LSMX_F32, true>(g, s);
+    else launch_d<DT, MODE, SHB, false, LSMX_F32, false>(g, s);
+}
+
+hipError_t launch_gemm_dense(const DenseArgs &g, int dtype, int mode, hipStream_t s) {
+    const bool shb = mode != 0 && g.b0 == g.b1;
+#define LSMX_DM(DT)                                                      \
+    do {                                                                 \
+        if (mode == 0) launch_mode<DT, 0, false>(g, s);                  \
+        else if (mode == 1 && shb) launch_mode<DT, 1, true>(g, s);       \
+        else if (mode == 1) launch_mode<DT, 1, false>(g, s);             \
+        else if (shb) launch_mode<DT, 2, true>(g, s);                    \
+        else launch_mode<DT, 2, false>(g, s);                            \
+    } while (0)
+    if (dtype == LSMX_BF16) LSMX_DM(LSMX_BF16);
+    else if (dtype == LSMX_F16) LSMX_DM(LSMX_F16);
+    else LSMX_DM(LSMX_E4M3);
+#undef LSMX_DM
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_f8f8_scaled(const DenseArgs &g, hipStream_t s) {
+    if (g.c_dtype == LSMX_F32) launch_d<LSMX_E4M3, 0, false, true, LSMX_F32, false>(g, s);
+    else if (g.c_dtype == LSMX_BF16) launch_d<LSMX_E4M3, 0, false, true, LSMX_BF16, false>(g, s);
+    else launch_d<LSMX_E4M3, 0, false, true, LSMX_F16, false>(g, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, int64_t ldx, void *y,
+                            int64_t ldy, hipStream_t s) {
+    const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)), blk(256);
+    if (elem_bytes == 1)
+        hipLaunchKernelGGL(transpose_kernel<uint8_t>, grid, blk, 0, s, reinterpret_cast<const uint8_t *>(x), rows, cols,
+                           ldx, reinterpret_cast<uint8_t *>(y), ldy);
+    else if (elem_bytes == 2)
+        hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, blk, 0, s, reinterpret_cast<const uint16_t *>(x), rows,
+                           cols, ldx, reinterpret_cast<uint16_t *>(y), ldy);
+    else
+        hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, blk, 0, s, reinterpret_cast<const uint32_t *>(x), rows,
+                           cols, ldx, reinterpret_cast<uint32_t *>(y), ldy);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+                                int64_t ldo, hipStream_t s) {
+    const int64_t n = rows * cols;
+    hipLaunchKernelGGL(scale_to_e8m0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sc, rows, cols, lds,
+                       transpose, out, ldo);
+    return hipGetLastError();
+}
+
+}  // namespace lsmx

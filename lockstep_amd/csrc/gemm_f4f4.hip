@@ -2,7 +2,7 @@
 //
 //   C[m, n] = sum_kb  2^(sa[m,kb]-127) * 2^(sb[n,kb]-127) * sum_{k in kb} A[m,k] * Bt[n,k]
 //
-// Semantics: mxfp4_gemm.py:175-233 (_mxfp4_gemm_packed_kernel /
+// Semantics: mxfp4_gemm.py:116-174 (_mxfp4_gemm_packed_kernel /
 // mxfp4_gemm_packed) and cuda/mxfp4_mma_gemm.cu:69-184, with both operands
 // K-contiguous ("TN"), packed two E2M1 codes per byte, low nibble first.
 // Instead of promoting an FP8 product to fp32 every 32-block and multiplying

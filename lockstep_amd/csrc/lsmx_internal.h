@@ -52,6 +52,20 @@ struct GemmArgs {
     int64_t M, N, K;
 };
 
+struct DenseArgs {
+    const uint8_t *a0, *a1;  // [M, lda] K-contiguous
+    int64_t lda;
+    const uint8_t *b0, *b1;  // Bt [N, ldb] K-contiguous
+    int64_t ldb;
+    const uint8_t *sa, *sb;  // E8M0 [rows, ld] (scaled E4M3 only)
+    int64_t ld_sa, ld_sb;
+    void *c0, *c1;
+    int c_dtype;
+    int64_t ldc;
+    int64_t M, N, K;
+    int64_t k_split;         // K per split (== K without split-K)
+};
+
 hipError_t launch_quantize(const QuantArgs &a, bool cols, hipStream_t s);
 hipError_t launch_round(const void *q, int q_dtype, int64_t n, uint8_t *codes, hipStream_t s);
 hipError_t launch_pack(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, hipStream_t s);
@@ -60,5 +74,11 @@ hipError_t launch_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n, hipS
 hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
 hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s);
+hipError_t launch_gemm_dense(const DenseArgs &g, int dtype, int mode, hipStream_t s);
+hipError_t launch_gemm_f8f8_scaled(const DenseArgs &g, hipStream_t s);
+hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, int64_t ldx, void *y,
+                            int64_t ldy, hipStream_t s);
+hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+                                int64_t ldo, hipStream_t s);
 
 }  // namespace lsmx

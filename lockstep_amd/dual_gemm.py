@@ -19,7 +19,7 @@ import torch
 
 from . import _capi as C
 from . import fp4 as _fp4
-from .mxfp4_gemm import _rows16, _scales
+from .mxfp4_gemm import _rows16, _scales, kmajor_operand
 
 
 def slot_offset(K: int) -> int:
@@ -34,9 +34,9 @@ def unpack_dual(acc: torch.Tensor, s: int):
     return acc - c2 * w, c2
 
 
-# Tile configuration of the gfx950 dual kernel (the reference's CFG keys).
-CFG = dict(BLOCK_M=128, BLOCK_N=256, BLOCK_K=64, num_warps=4, num_stages=2)
-_SK = dict(BM=128, BN=128, BK=64, warps=8, stages=3)
+# Tile configuration of the gfx950 dense kernels (the reference's CFG keys).
+CFG = dict(BLOCK_M=128, BLOCK_N=128, BLOCK_K=64, num_warps=4, num_stages=2)
+_SK = dict(BM=128, BN=128, BK=64, warps=4, stages=2)
 
 
 def dual_mxfp4(a0, a1, w_pk, w_scale, out_dtype=torch.bfloat16):
@@ -66,30 +66,113 @@ def dual_mxfp4(a0, a1, w_pk, w_scale, out_dtype=torch.bfloat16):
     return c0, c1
 
 
-def _dense_not_built(name):
-    raise NotImplementedError(
-        f"dual_gemm.{name} on dense (non-MXFP4) operands is not built yet on gfx950; "
-        "use dual_mxfp4 for the shared-weight MXFP4 form")
+# Dense operands (the reference's dual_gemm.py takes bf16 / fp16 / e4m3 tensors
+# holding integer q-grid values, dual_gemm.py:1-15, train_step.py:90-105) run
+# on lockstep_amd/csrc/gemm_dense.hip: 128 x 128 tiles, 64-deep K stages,
+# fp32 accumulation on MFMA, fp32 outputs.
+_DENSE = {torch.bfloat16: C.BF16, torch.float16: C.F16, torch.float8_e4m3fn: C.E4M3}
+_BK = 64
+
+
+def _dense(mode, a1, a2, b1, b2, out, splits=1):
+    """Launch one dense kernel.  mode 0: out[0] = a1 b1; 1: out[0] = a1 b1 + a2 b2;
+    2: out[0] = a1 b1, out[1] = a2 b2.  b* are [K, N]; a2 and b2 share a1's and
+    b1's layouts (as the reference's kernels assume)."""
+    M, K = a1.shape
+    N = b1.shape[1]
+    C.require_device(a1, b1, *([a2, b2] if mode else []))
+    dt = a1.dtype
+    if dt not in _DENSE:
+        raise TypeError(f"dense GEMMs take bfloat16, float16 or float8_e4m3fn operands, got {dt}")
+    for t in ([b1] + ([a2, b2] if mode else [])):
+        if t.dtype != dt:
+            raise TypeError(f"operand dtypes differ: {dt} and {t.dtype}")
+    if mode:
+        if a2.shape != a1.shape or b2.shape != b1.shape:
+            raise ValueError("a1/a2 and b1/b2 must have the same shapes")
+    if b1.shape[0] != K:
+        raise ValueError(f"inner dimensions differ: a is [{M}, {K}], b is {list(b1.shape)}")
+    if M == 0 or N == 0:
+        return
+    if K == 0:
+        for o in out:
+            o.zero_()
+        return
+    code = _DENSE[dt]
+    raw = (lambda t: t.view(torch.uint8)) if dt == torch.float8_e4m3fn else (lambda t: t)
+    a1 = _rows16(raw(a1))
+    bt1 = kmajor_operand(raw(b1))
+    a2p = bt2p = 0
+    if mode:
+        a2 = _rows16(raw(a2))
+        if a2.stride(0) != a1.stride(0) and M > 1:
+            a1, a2 = a1.contiguous(), a2.contiguous()
+        bt2 = bt1 if b2 is b1 else kmajor_operand(raw(b2))
+        if bt2.stride(0) != bt1.stride(0) and N > 1:
+            bt1, bt2 = bt1.contiguous(), bt2.contiguous()
+        a2p, bt2p = a2.data_ptr(), bt2.data_ptr()
+    c1 = out[1].data_ptr() if mode == 2 else 0
+    C.call("lsmx_gemm_dense", a1.data_ptr(), a2p, a1.stride(0) if M > 1 else K, bt1.data_ptr(), bt2p,
+           bt1.stride(0) if N > 1 else K, code, mode, out[0].data_ptr(), c1, N, M, N, K, splits,
+           C.stream_of(out[0]))
 
 
 def gemm(a, b):
     """Single GEMM, one fp32 accumulator, fp32 out. a [M,K], b [K,N]."""
-    _dense_not_built("gemm")
+    M, K = a.shape
+    N = b.shape[1]
+    assert K % 64 == 0, "K must be a multiple of 64 (max BLOCK_K); zero-pad if shorter"
+    out = torch.empty((M, N), device=a.device, dtype=torch.float32)
+    _dense(0, a, None, b, None, (out,))
+    return out
 
 
 def dual_packed(a1, a2s, b1, b2):
     """Returns the PACKED fp32 tile. Call unpack_dual(acc, s) to split it."""
-    _dense_not_built("dual_packed")
+    M, K = a1.shape
+    N = b1.shape[1]
+    assert K % 64 == 0, "K must be a multiple of 64 (max BLOCK_K); zero-pad if shorter"
+    out = torch.empty((M, N), device=a1.device, dtype=torch.float32)
+    _dense(1, a1, a2s, b1, b2, (out,))
+    return out
 
 
 def dual_separate(a1, a2, b1, b2):
-    """Two GEMMs, two fp32 accumulators, one launch."""
-    _dense_not_built("dual_separate")
+    """Two GEMMs, two fp32 accumulators, one launch.  With b1 is b2 (the
+    shared-weight form) B is transposed once and each B tile feeds both."""
+    M, K = a1.shape
+    N = b1.shape[1]
+    assert K % 64 == 0, "K must be a multiple of 64 (max BLOCK_K); zero-pad if shorter"
+    c1 = torch.empty((M, N), device=a1.device, dtype=torch.float32)
+    c2 = torch.empty_like(c1)
+    _dense(2, a1, a2, b1, b2, (c1, c2))
+    return c1, c2
+
+
+def _splitk_check(K, splits, p):
+    assert K % (splits * p["BK"]) == 0, "K must divide splits*BK"
+    if (K // splits) % _BK:
+        raise ValueError(f"each split's K ({K // splits}) must be a multiple of {_BK} on gfx950")
 
 
 def splitk_packed(a1, a2s, b1, b2, splits=8, **kw):
-    _dense_not_built("splitk_packed")
+    """Packed accumulator over `splits` K slices, fp32 atomic adds into a zeroed output."""
+    p = {**_SK, **kw}
+    M, K = a1.shape
+    N = b1.shape[1]
+    _splitk_check(K, splits, p)
+    out = torch.zeros((M, N), device=a1.device, dtype=torch.float32)
+    _dense(1, a1, a2s, b1, b2, (out,), splits)
+    return out
 
 
 def splitk_separate(a1, a2, b1, b2, splits=8, **kw):
-    _dense_not_built("splitk_separate")
+    """Two accumulators over `splits` K slices, fp32 atomic adds into zeroed outputs."""
+    p = {**_SK, **kw}
+    M, K = a1.shape
+    N = b1.shape[1]
+    _splitk_check(K, splits, p)
+    o1 = torch.zeros((M, N), device=a1.device, dtype=torch.float32)
+    o2 = torch.zeros_like(o1)
+    _dense(2, a1, a2, b1, b2, (o1, o2), splits)
+    return o1, o2

@@ -101,11 +101,79 @@ def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
     return c
 
 
+def _e8m0_rows(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torch.Tensor:
+    """Block scales as E8M0 bytes [rows, nkb]: from fp32 [rows, nkb] (or
+    [nkb, rows] when transposed) through lsmx_scale_to_e8m0, or from E8M0
+    bytes of the same shapes.  An fp32 scale that is not a power of two in
+    [2^-127, 2^127] becomes E8M0 NaN, so the outputs that use it are NaN."""
+    shape = (nkb, rows) if transposed else (rows, nkb)
+    assert tuple(s.shape) == shape
+    out = torch.empty((rows, nkb), device=s.device, dtype=torch.uint8)
+    if rows == 0 or nkb == 0:
+        return out
+    if s.dtype == torch.uint8:
+        if not transposed:
+            return s.contiguous()
+        s = s.contiguous()
+        C.call("lsmx_transpose", s.data_ptr(), 1, nkb, rows, rows, out.data_ptr(), nkb, C.stream_of(out))
+        return out
+    if s.dtype != torch.float32:
+        s = s.float()
+    if s.stride(-1) != 1:
+        s = s.contiguous()
+    C.call("lsmx_scale_to_e8m0", s.data_ptr(), shape[0], shape[1], s.stride(0) if shape[0] > 1 else shape[1],
+           int(transposed), out.data_ptr(), nkb, C.stream_of(out))
+    return out
+
+
+def kmajor_operand(b: torch.Tensor) -> torch.Tensor:
+    """B [K, N] -> the K-contiguous [N, K] operand the kernels read: B.T itself
+    when it already is K-contiguous with 16-byte aligned rows, else a
+    transposed copy made on the device (lsmx_transpose)."""
+    K, N = b.shape
+    bt = b.t()
+    if bt.stride(-1) == 1 and bt.data_ptr() % 16 == 0 and (N <= 1 or (bt.stride(0) * bt.element_size()) % 16 == 0):
+        return bt
+    out = torch.empty((N, K), device=b.device, dtype=b.dtype)
+    if K == 0 or N == 0:
+        return out
+    if b.stride(-1) != 1:
+        b = b.contiguous()
+    C.call("lsmx_transpose", b.data_ptr(), b.element_size(), K, N, b.stride(0) if K > 1 else N, out.data_ptr(), K,
+           C.stream_of(out))
+    return out
+
+
 def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
     """a_fp8 [M,K] K-contig, b_fp8 [K,N] N-contig, a_scale [M,K//32], b_scale [K//32,N].
 
-    Operands are E4M3 bytes holding E2M1 values (fp4.codes_to_e4m3), as in
-    mxfp4_gemm.py:133-146."""
-    raise NotImplementedError(
-        "mxfp4_gemm_fp8 (E4M3-operand path) is not built yet on gfx950; "
-        "use mxfp4_gemm_packed on packed FP4 operands")
+    Operands are E4M3 bytes (float8_e4m3fn or uint8 views of them), normally
+    holding E2M1 values (fp4.codes_to_e4m3).  Scales are fp32 powers of two as
+    fp4.quantize_mxfp4 returns, or E8M0 bytes of the same shapes.  Returns
+    C[m, n] = sum_kb a_scale[m, kb] b_scale[kb, n] (A_kb . B_kb) in out_dtype:
+    the E4M3 products run on the scaled MFMA (v_mfma_scale_f32_32x32x64_
+    f8f6f4, E4M3 mode) with the block scales applied by the instruction and
+    fp32 accumulation (reference: mxfp4_gemm.py:29-87).  B is transposed to
+    K-contiguous rows on the device first unless b_fp8 is a transposed view
+    of such rows."""
+    M, K = a_fp8.shape
+    K2, N = b_fp8.shape
+    assert K == K2 and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
+    assert a_scale.shape == (M, K // 32) and b_scale.shape == (K // 32, N)
+    C.require_device(a_fp8, b_fp8, a_scale, b_scale)
+    for t in (a_fp8, b_fp8):
+        if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
+            raise TypeError(f"mxfp4_gemm_fp8 takes float8_e4m3fn operands, got {t.dtype}")
+    c = torch.empty((M, N), device=a_fp8.device, dtype=out_dtype)
+    if M == 0 or N == 0:
+        return c
+    if K == 0:
+        return c.zero_()
+    a = _rows16(a_fp8.view(torch.uint8))
+    bt = kmajor_operand(b_fp8.view(torch.uint8))
+    sa = _e8m0_rows(a_scale, M, K // 32, transposed=False)
+    sb = _e8m0_rows(b_scale, N, K // 32, transposed=True)
+    C.call("lsmx_gemm_f8f8", a.data_ptr(), a.stride(0) if M > 1 else K, sa.data_ptr(), K // 32,
+           bt.data_ptr(), bt.stride(0) if N > 1 else K, sb.data_ptr(), K // 32, c.data_ptr(),
+           _out_code(out_dtype), N, M, N, K, C.stream_of(c))
+    return c

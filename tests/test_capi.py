@@ -64,7 +64,7 @@ def test_block_multiple_is_rejected_with_reference_message():
 def test_gemm_k_multiple_is_rejected_with_reference_message():
     rc = _rc("lsmx_gemm_f4f4", FAKE, 48, FAKE, 3, FAKE, 48, FAKE, 3, 0, FAKE, 1, 8, 8, 8, 96, None)
     assert rc == C.ERR_SHAPE
-    assert "K must be a multiple of 128" in C.last_error()          # mxfp4_gemm.py:225
+    assert "K must be a multiple of 128" in C.last_error()          # mxfp4_gemm.py:166
 
 
 def test_bad_dtype_and_alignment_are_rejected():
@@ -136,3 +136,47 @@ def test_quantized_backward_checks_shapes_before_any_kernel():
     layer = fp4_linear.MXFP4Linear(128, 128)
     assert layer.quantized_backward is False      # the reference's STE backward by default
     assert fp4_linear.MXFP4Linear(128, 128, quantized_backward=True).quantized_backward
+
+
+def test_dense_entry_points_validate_before_launch():
+    bf = C.BF16
+    # fp32 operands are not a dense GEMM type
+    assert _rc("lsmx_gemm_dense", FAKE, None, 64, FAKE, None, 64, C.F32, 0, FAKE, None, 8, 8, 8, 64, 1,
+               None) == C.ERR_DTYPE
+    rc = _rc("lsmx_gemm_dense", FAKE, None, 96, FAKE, None, 96, bf, 0, FAKE, None, 8, 8, 8, 96, 1, None)
+    assert rc == C.ERR_SHAPE and "K must be a multiple of 64" in C.last_error()      # dual_gemm.py:219
+    rc = _rc("lsmx_gemm_dense", FAKE, FAKE, 192, FAKE, FAKE, 192, bf, 2, FAKE, FAKE, 8, 8, 8, 192, 2, None)
+    assert rc == C.ERR_SHAPE and "K must divide splits*BK" in C.last_error()         # dual_gemm.py:265
+    # dual separate needs both outputs, dual modes both operand pairs
+    assert _rc("lsmx_gemm_dense", FAKE, FAKE, 64, FAKE, FAKE, 64, bf, 2, FAKE, None, 8, 8, 8, 64, 1,
+               None) == C.ERR_ARG
+    assert _rc("lsmx_gemm_dense", FAKE, None, 64, FAKE, FAKE, 64, bf, 1, FAKE, None, 8, 8, 8, 64, 1,
+               None) == C.ERR_ARG
+    assert _rc("lsmx_gemm_dense", FAKE, None, 64, FAKE, None, 64, bf, 3, FAKE, None, 8, 8, 8, 64, 1,
+               None) == C.ERR_ARG
+    rc = _rc("lsmx_gemm_dense", ctypes.c_void_p(0x1008), None, 64, FAKE, None, 64, bf, 0, FAKE, None, 8, 8, 8,
+             64, 1, None)
+    assert rc == C.ERR_ALIGN
+    rc = _rc("lsmx_gemm_f8f8", FAKE, 64, FAKE, 2, FAKE, 64, FAKE, 2, FAKE, C.BF16, 8, 8, 8, 64, None)
+    assert rc == C.ERR_SHAPE and "K must be a multiple of 128" in C.last_error()     # mxfp4_gemm.py:78
+    assert _rc("lsmx_gemm_f8f8", FAKE, 128, FAKE, 4, FAKE, 128, FAKE, 4, FAKE, 7, 8, 8, 8, 128,
+               None) == C.ERR_DTYPE
+    assert _rc("lsmx_transpose", FAKE, 3, 4, 4, 4, FAKE, 4, None) == C.ERR_DTYPE
+    assert _rc("lsmx_transpose", FAKE, 2, 4, 8, 4, FAKE, 4, None) == C.ERR_SHAPE
+    assert _rc("lsmx_scale_to_e8m0", None, 4, 4, 4, 0, FAKE, 4, None) == C.ERR_ARG
+
+
+def test_dense_python_api_asserts_then_refuses_cpu():
+    from lockstep_amd import dual_gemm as dg
+    from lockstep_amd import mxfp4_gemm
+    a = torch.zeros(4, 96, dtype=torch.bfloat16)
+    b = torch.zeros(96, 4, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="K must be a multiple of 64"):
+        dg.gemm(a, b)
+    with pytest.raises(AssertionError, match="K must divide splits\\*BK"):
+        dg.splitk_packed(a[:, :64], a[:, :64], b[:64], b[:64], splits=2)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        dg.dual_separate(a[:, :64], a[:, :64], b[:64], b[:64])
+    f8 = torch.zeros(4, 64, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    with pytest.raises(AssertionError, match="K must be a multiple of 128"):
+        mxfp4_gemm.mxfp4_gemm_fp8(f8, f8.t(), torch.ones(4, 2), torch.ones(2, 4))

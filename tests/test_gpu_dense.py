@@ -1,0 +1,271 @@
+"""GPU parity of the dense GEMM family (dual_gemm.py) and of mxfp4_gemm_fp8.
+
+Closed forms pin these: the reference's operands hold integer q-grid values
+(fp4.codes_to_q, |q| <= 12), so every product and every partial sum up to
+2^24 is exact in fp32 and the result must equal the fp64 integer product bit
+for bit (train_step.py:118-137, bench.py:44-57).  Random-normal operands are
+checked against fp64 with max|c - ref| / max|ref| <= 1e-5 (fp32 output) and
+<= 1e-2 (bf16 output), the reference's own metric (bench.py:71).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float16, torch.float8_e4m3fn]
+
+
+@pytest.fixture(scope="module")
+def mods(dev):
+    from lockstep_amd import _capi, dual_gemm, fp4, mxfp4_gemm
+    return dual_gemm, mxfp4_gemm, fp4, _capi
+
+
+def q_grid(rng, shape):
+    """Integer grid values of random E2M1 codes, negative zero excluded (fp4.py:37-41)."""
+    pick = np.array([0, 1, 2, 3, 4, 6, 8, 12, -1, -2, -3, -4, -6, -8, -12], dtype=np.float64)
+    return pick[rng.integers(0, 15, shape)]
+
+
+def on(dev, x, dt):
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dt).to(dev)
+
+
+def f64(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+SHAPES = [(256, 256, 256), (200, 136, 192), (1, 1, 64), (130, 70, 128), (384, 512, 1024)]
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=str)
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_integer_grid_exact(dev, mods, dt, M, N, K):
+    dg = mods[0]
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    a, b = q_grid(rng, (M, K)), q_grid(rng, (K, N))
+    got = dg.gemm(on(dev, a, dt), on(dev, b, dt))
+    assert got.dtype == torch.float32 and got.shape == (M, N)
+    assert np.array_equal(f64(got), a @ b)
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=str)
+@pytest.mark.parametrize("shared", [False, True], ids=["b1!=b2", "shared-W"])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (190, 300, 256), (64, 33, 64)])
+def test_dual_separate_integer_grid_exact(dev, mods, dt, shared, M, N, K):
+    """train_step.py:52-53 (`dual_separate(a1, a2, W, W)`) and dual_gemm.py:244-255."""
+    dg = mods[0]
+    rng = np.random.default_rng(K + M)
+    a1, a2 = q_grid(rng, (M, K)), q_grid(rng, (M, K))
+    b1 = q_grid(rng, (K, N))
+    b2 = b1 if shared else q_grid(rng, (K, N))
+    tb1 = on(dev, b1, dt)
+    tb2 = tb1 if shared else on(dev, b2, dt)
+    c1, c2 = dg.dual_separate(on(dev, a1, dt), on(dev, a2, dt), tb1, tb2)
+    assert np.array_equal(f64(c1), a1 @ b1) and np.array_equal(f64(c2), a2 @ b2)
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=str)
+@pytest.mark.parametrize("shared", [False, True], ids=["b1!=b2", "shared-W"])
+def test_dual_packed_is_concatenated_k_gemm(dev, mods, dt, shared):
+    """One accumulator: acc = A1.B1 + A2.B2, the GEMM over the K-concatenation
+    [A1 | A2] . [B1; B2] (dual_gemm.py:42-72); exact on the integer grid."""
+    dg = mods[0]
+    rng = np.random.default_rng(5)
+    M, N, K = 160, 200, 320
+    a1, a2 = q_grid(rng, (M, K)), q_grid(rng, (M, K))
+    b1 = q_grid(rng, (K, N))
+    b2 = b1 if shared else q_grid(rng, (K, N))
+    tb1 = on(dev, b1, dt)
+    tb2 = tb1 if shared else on(dev, b2, dt)
+    acc = dg.dual_packed(on(dev, a1, dt), on(dev, a2, dt), tb1, tb2)
+    assert np.array_equal(f64(acc), a1 @ b1 + a2 @ b2)
+    cat = dg.gemm(on(dev, np.concatenate([a1, a2], 1), dt), on(dev, np.concatenate([b1, b2], 0), dt))
+    assert torch.equal(acc, cat)
+
+
+def test_packed_slots_round_trip_where_exact(dev, mods):
+    """train_step.py:58-59 / bench.py:122-128: with 2*bits(144K)+1 <= 24 the
+    packed accumulator splits back into both products exactly (K = 16, padded
+    to 64 with zeros as bench.py:139-149 does)."""
+    dg = mods[0]
+    rng = np.random.default_rng(11)
+    k, kp, M, N = 16, 64, 256, 256
+    s = dg.slot_offset(k)
+    q = [q_grid(rng, sh) for sh in ((M, k), (M, k), (k, N), (k, N))]
+    # every partial sum, in any order, stays an integer below 2^24
+    bound = np.abs(q[0]) @ np.abs(q[2]) + 2.0 ** s * (np.abs(q[1]) @ np.abs(q[3]))
+    assert bound.max() < 2 ** 24
+    pad = [np.pad(q[0], ((0, 0), (0, kp - k))), np.pad(q[1], ((0, 0), (0, kp - k))),
+           np.pad(q[2], ((0, kp - k), (0, 0))), np.pad(q[3], ((0, kp - k), (0, 0)))]
+    acc = dg.dual_packed(on(dev, pad[0], torch.bfloat16), on(dev, pad[1] * 2.0 ** s, torch.bfloat16),
+                         on(dev, pad[2], torch.bfloat16), on(dev, pad[3], torch.bfloat16))
+    ref = q[0] @ q[2] + (q[1] @ q[3]) * 2.0 ** s
+    assert np.array_equal(f64(acc), ref)          # the accumulator itself is exact
+    g1, g2 = dg.unpack_dual(acc.double(), s)
+    assert np.array_equal(g1.cpu().numpy(), q[0] @ q[2]) and np.array_equal(g2.cpu().numpy(), q[1] @ q[3])
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float8_e4m3fn], ids=str)
+@pytest.mark.parametrize("splits", [2, 4, 8])
+def test_splitk_integer_grid_exact(dev, mods, dt, splits):
+    """dual_gemm.py:258-289: partials over K slices, atomic adds into zeros."""
+    dg = mods[0]
+    rng = np.random.default_rng(splits)
+    M, N, K = 200, 260, 1024
+    a1, a2 = q_grid(rng, (M, K)), q_grid(rng, (M, K))
+    b1, b2 = q_grid(rng, (K, N)), q_grid(rng, (K, N))
+    t = [on(dev, x, dt) for x in (a1, a2, b1, b2)]
+    o1, o2 = dg.splitk_separate(*t, splits=splits)
+    assert np.array_equal(f64(o1), a1 @ b1) and np.array_equal(f64(o2), a2 @ b2)
+    acc = dg.splitk_packed(*t, splits)
+    assert np.array_equal(f64(acc), a1 @ b1 + a2 @ b2)
+    s1, s2 = dg.splitk_separate(t[0], t[1], t[2], t[2], splits=splits)   # shared weight
+    assert np.array_equal(f64(s1), a1 @ b1) and np.array_equal(f64(s2), a2 @ b1)
+
+
+def test_splitk_keeps_reference_assert(dev, mods):
+    dg = mods[0]
+    a = torch.zeros((128, 192), device=dev, dtype=torch.bfloat16)
+    b = torch.zeros((192, 128), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="K must divide splits\\*BK"):
+        dg.splitk_separate(a, a, b, b, splits=8)
+    with pytest.raises(AssertionError, match="K must be a multiple of 64"):
+        dg.gemm(a[:, :100], b[:100])
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=str)
+def test_random_normal_against_fp64(dev, mods, dt):
+    dg = mods[0]
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 512, 384, 2048
+    a, b = torch.randn((M, K), generator=g).to(dt), torch.randn((K, N), generator=g).to(dt)
+    ref = a.double() @ b.double()
+    c = dg.gemm(a.to(dev), b.to(dev)).double().cpu()
+    assert ((c - ref).abs().max() / ref.abs().max()).item() <= 1e-5
+    c1, c2 = dg.dual_separate(a.to(dev), a.to(dev), b.to(dev), b.to(dev))
+    assert torch.equal(c1, c2) and torch.equal(c1.double().cpu(), c)
+
+
+def test_transposed_view_operand_is_read_in_place(dev, mods):
+    """b = W.t() of a K-contiguous W [N, K] needs no transposed copy; the
+    result must equal the one through a copied N-contiguous b."""
+    dg = mods[0]
+    rng = np.random.default_rng(9)
+    M, N, K = 96, 160, 256
+    a, w = q_grid(rng, (M, K)), q_grid(rng, (N, K))
+    ta, tw = on(dev, a, torch.bfloat16), on(dev, w, torch.bfloat16)
+    c_view = dg.gemm(ta, tw.t())
+    c_copy = dg.gemm(ta, tw.t().contiguous())
+    assert torch.equal(c_view, c_copy) and np.array_equal(f64(c_view), a @ w.T)
+
+
+def test_empty_and_zero_k(dev, mods):
+    dg, mg = mods[0], mods[1]
+    a = torch.zeros((0, 64), device=dev, dtype=torch.bfloat16)
+    b = torch.zeros((64, 8), device=dev, dtype=torch.bfloat16)
+    assert dg.gemm(a, b).shape == (0, 8)
+    z = dg.gemm(torch.ones((4, 0), device=dev, dtype=torch.bfloat16), torch.ones((0, 8), device=dev,
+                                                                                   dtype=torch.bfloat16))
+    assert z.shape == (4, 8) and not z.any()
+    f8 = torch.zeros((4, 0), device=dev, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    z = mg.mxfp4_gemm_fp8(f8, f8.t(), torch.ones((4, 0), device=dev), torch.ones((0, 4), device=dev),
+                          out_dtype=torch.float32)
+    assert z.shape == (4, 4) and not z.any()
+
+
+@pytest.mark.parametrize("elem", [1, 2, 4])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (33, 65), (256, 96), (1000, 3)])
+def test_transpose_exact(dev, mods, elem, rows, cols):
+    C = mods[3]
+    dt = {1: torch.uint8, 2: torch.int16, 4: torch.int32}[elem]
+    x = torch.randint(0, 100, (rows, cols + 5), dtype=torch.int32).to(dt).to(dev)[:, :cols]
+    y = torch.full((cols, rows), -1, dtype=dt, device=dev)
+    C.call("lsmx_transpose", x.data_ptr(), elem, rows, cols, x.stride(0), y.data_ptr(), rows, C.stream_of(y))
+    assert torch.equal(y.cpu(), x.t().cpu())
+
+
+# ----------------------------------------------------------- mxfp4_gemm_fp8
+def e4m3_of_codes(dev, fp4, codes):
+    return fp4.codes_to_e4m3(torch.from_numpy(codes).to(dev))
+
+
+def test_fp8_unit_scales_bit_exact(dev, mods, oracle):
+    """bench.py:41-57: random codes, unit scales, K = 128 -> C == (qa @ qb) / 4."""
+    _, mg, fp4, _ = mods
+    rng = np.random.default_rng(0)
+    pick = np.array([c for c in range(16) if c != 8], dtype=np.uint8)
+    ca, cb = pick[rng.integers(0, 15, (256, 128))], pick[rng.integers(0, 15, (128, 256))]
+    sa = torch.ones((256, 4), device=dev)
+    sb = torch.ones((4, 256), device=dev)
+    got = mg.mxfp4_gemm_fp8(e4m3_of_codes(dev, fp4, ca), e4m3_of_codes(dev, fp4, cb), sa, sb,
+                            out_dtype=torch.float32)
+    qa, qb = oracle.E2M1_Q[ca].astype(np.float64), oracle.E2M1_Q[cb].astype(np.float64)
+    assert np.array_equal(f64(got), (qa @ qb) / 4.0)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (200, 136, 384), (1, 300, 128)])
+def test_fp8_random_codes_and_scales(dev, mods, oracle, out_dtype, M, N, K):
+    """cuda/mxfp4_mma_gemm.cu:204-252: codes 0..15 (incl. -0), scales 2^[-3,3]."""
+    _, mg, fp4, _ = mods
+    rng = np.random.default_rng(M + K)
+    ca, cb = rng.integers(0, 16, (M, K), dtype=np.uint8), rng.integers(0, 16, (K, N), dtype=np.uint8)
+    sa = np.exp2(rng.integers(-3, 4, (M, K // 32))).astype(np.float32)
+    sb = np.exp2(rng.integers(-3, 4, (K // 32, N))).astype(np.float32)
+    ref = oracle.dequantize_mxfp4(ca, sa).astype(np.float64) @ \
+        oracle.dequantize_mxfp4(cb.T.copy(), sb.T.copy()).astype(np.float64).T
+    got = mg.mxfp4_gemm_fp8(e4m3_of_codes(dev, fp4, ca), e4m3_of_codes(dev, fp4, cb),
+                            torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev), out_dtype=out_dtype)
+    assert got.dtype == out_dtype and got.shape == (M, N)
+    tol = 1e-6 if out_dtype == torch.float32 else 1e-2
+    assert oracle.max_rel(f64(got), ref) <= tol
+    # E8M0 byte scales of the same shapes give the same result
+    got8 = mg.mxfp4_gemm_fp8(e4m3_of_codes(dev, fp4, ca), e4m3_of_codes(dev, fp4, cb),
+                             torch.from_numpy(oracle.scale_to_e8m0(sa)).to(dev),
+                             torch.from_numpy(oracle.scale_to_e8m0(sb)).to(dev), out_dtype=out_dtype)
+    assert torch.equal(got, got8)
+
+
+def test_fp8_quantized_randn_matches_fp64(dev, mods, oracle):
+    """bench.py:60-73: randn -> quantize (A along K, B transposed along K) ->
+    codes_to_e4m3 -> mxfp4_gemm_fp8 vs the fp64 reference, rel < 1e-5; the
+    packed kernel on the same operands agrees."""
+    _, mg, fp4, _ = mods
+    g = torch.Generator().manual_seed(7)
+    M, N, K = 384, 256, 1024
+    a, b = torch.randn((M, K), generator=g), torch.randn((K, N), generator=g)
+    a_codes, a_scale = oracle.quantize_mxfp4(a.numpy())
+    bt_codes, bt_scale = oracle.quantize_mxfp4(b.t().contiguous().numpy())
+    ref = oracle.dequantize_mxfp4(a_codes, a_scale).astype(np.float64) @ \
+        oracle.dequantize_mxfp4(bt_codes, bt_scale).astype(np.float64).T
+    c = mg.mxfp4_gemm_fp8(e4m3_of_codes(dev, fp4, a_codes), e4m3_of_codes(dev, fp4, bt_codes.T.copy()),
+                          torch.from_numpy(a_scale).to(dev), torch.from_numpy(bt_scale.T.copy()).to(dev),
+                          out_dtype=torch.float32)
+    assert oracle.max_rel(f64(c), ref) <= 1e-5
+    cp = mg.mxfp4_gemm_packed(torch.from_numpy(oracle.pack_fp4(a_codes)).to(dev),
+                              torch.from_numpy(oracle.pack_fp4(bt_codes)).to(dev),
+                              torch.from_numpy(a_scale).to(dev), torch.from_numpy(bt_scale).to(dev),
+                              out_dtype=torch.float32)
+    assert oracle.max_rel(f64(cp), ref) <= 1e-5
+
+
+def test_fp8_non_power_of_two_scale_poisons_its_outputs(dev, mods):
+    """A scale with no E8M0 form becomes E8M0 NaN: only the outputs that use it
+    are NaN, the rest are unchanged."""
+    _, mg, fp4, _ = mods
+    rng = np.random.default_rng(2)
+    M = N = 128
+    K = 128
+    ca, cb = rng.integers(0, 16, (M, K), dtype=np.uint8), rng.integers(0, 16, (K, N), dtype=np.uint8)
+    fa, fb = e4m3_of_codes(dev, fp4, ca), e4m3_of_codes(dev, fp4, cb)
+    sa, sb = torch.ones((M, K // 32), device=dev), torch.ones((K // 32, N), device=dev)
+    clean = mg.mxfp4_gemm_fp8(fa, fb, sa, sb, out_dtype=torch.float32)
+    sa[5, 2] = 1.5
+    bad = mg.mxfp4_gemm_fp8(fa, fb, sa, sb, out_dtype=torch.float32)
+    assert bad[5].isnan().all()
+    keep = torch.ones(M, dtype=torch.bool)
+    keep[5] = False
+    assert torch.equal(bad[keep], clean[keep])
