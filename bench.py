@@ -33,6 +33,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_FP4_TFLOPS = 10100.0     # MI355X dense MXFP4 MFMA
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 
 
@@ -263,10 +264,63 @@ def run_suite(path, torch, dev):
                       "tflops": fl / ms / 1e9, "gbs": by / ms / 1e6,
                       "frac_bf16_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS, "frac_hbm": by / ms / 1e6 / PEAK_HBM_GBS})
     lines.append(bench_cfg5(torch, dev))
+    lines += bench_reference_rows(torch, dev)
     with open(path, "w") as f:
         for ln in lines:
             f.write(json.dumps(ln) + "\n")
             print(json.dumps(ln), file=sys.stderr, flush=True)
+
+
+def bench_reference_rows(torch, dev, n=4096):
+    """The throughput rows of the reference's own bench.py at its default
+    4096^3 (bench.py:98-107 mxfp4 rows, :163-176 dual rows): mxfp4_gemm_fp8
+    and mxfp4_gemm_packed, then the dense dual GEMMs on bf16 operands."""
+    from lockstep_amd import dual_gemm as dg
+    from lockstep_amd import fp4, mxfp4_gemm as mg
+    g = torch.Generator(device=dev).manual_seed(4001)
+    fl1 = 2.0 * n ** 3
+    rows = []
+
+    def row(name, ms, flops, peak):
+        rows.append({"config": f"ref-bench {name}, {n}^3", "ms": ms, "tflops": flops / ms / 1e9,
+                     "frac_peak": flops / ms / 1e9 / peak})
+
+    a = torch.randn((n, n), device=dev, generator=g)
+    b = torch.randn((n, n), device=dev, generator=g)
+    a_pk, a_e8 = fp4.quantize_pack_mxfp4(a)
+    bt_pk, bt_e8 = fp4.quantize_pack_mxfp4(b.t().contiguous())
+    a_f8 = fp4.codes_to_e4m3(fp4.unpack_fp4(a_pk))
+    bt_f8 = fp4.codes_to_e4m3(fp4.unpack_fp4(bt_pk))
+    b_f8 = bt_f8.t().contiguous()                      # [K, N] N-contiguous, as the reference passes it
+    a_s, bt_s = fp4.e8m0_to_scale(a_e8), fp4.e8m0_to_scale(bt_e8)
+    b_s = bt_s.t().contiguous()
+    row("mxfp4_gemm_fp8 (N-contiguous B: transposed on the device each call)",
+        _time_events(lambda: mg.mxfp4_gemm_fp8(a_f8, b_f8, a_s, b_s)), fl1, PEAK_FP8_TFLOPS)
+    row("mxfp4_gemm_fp8 (B passed as a view of K-contiguous rows)",
+        _time_events(lambda: mg.mxfp4_gemm_fp8(a_f8, bt_f8.t(), a_e8, bt_e8.t())), fl1, PEAK_FP8_TFLOPS)
+    row("mxfp4_gemm_packed (f4 x f4)", _time_events(lambda: mg.mxfp4_gemm_packed(a_pk, bt_pk, a_e8, bt_e8)),
+        fl1, PEAK_FP4_TFLOPS)
+    a1 = torch.randn((n, n), device=dev, generator=g).to(torch.bfloat16)
+    a2 = torch.randn((n, n), device=dev, generator=g).to(torch.bfloat16)
+    b1 = torch.randn((n, n), device=dev, generator=g).to(torch.bfloat16)
+    b2 = torch.randn((n, n), device=dev, generator=g).to(torch.bfloat16)
+    fl2 = 2 * fl1
+    row("dual: 2x torch.matmul (two launches)", _time_events(lambda: (a1 @ b1, a2 @ b2)), fl2, PEAK_BF16_TFLOPS)
+    row("dual: fused, two accumulators (dual_separate)", _time_events(lambda: dg.dual_separate(a1, a2, b1, b2)),
+        fl2, PEAK_BF16_TFLOPS)
+    row("dual: fused, one packed accumulator (dual_packed)",
+        _time_events(lambda: dg.dual_packed(a1, a2, b1, b2)), fl2, PEAK_BF16_TFLOPS)
+    for splits in (4, 8):
+        row(f"dual: split-K={splits}, two accumulators",
+            _time_events(lambda s=splits: dg.splitk_separate(a1, a2, b1, b2, s)), fl2, PEAK_BF16_TFLOPS)
+        row(f"dual: split-K={splits}, one accumulator",
+            _time_events(lambda s=splits: dg.splitk_packed(a1, a2, b1, b2, s)), fl2, PEAK_BF16_TFLOPS)
+    row("dual_separate, shared weight (b1 is b2)", _time_events(lambda: dg.dual_separate(a1, a2, b1, b1)),
+        fl2, PEAK_BF16_TFLOPS)
+    bt1 = b1.t().contiguous()
+    row("gemm (bf16, B a view of K-contiguous rows)", _time_events(lambda: dg.gemm(a1, bt1.t())), fl1,
+        PEAK_BF16_TFLOPS)
+    return rows
 
 
 def bench_cfg5(torch, dev, T=8192, H=2048, F=8192):
