@@ -158,10 +158,13 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
 
-    # per-kernel durations from HIP events on the kernels' stream
+    # per-kernel durations from HIP events on the kernels' stream; a spin
+    # kernel ahead of each step keeps the GPU busy while the host enqueues,
+    # so no event interval includes host launch time
     qa, qb, gm = [], [], []
     for _ in range(max(args.steps, 5)):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        torch.cuda._sleep(2_000_000)
         step(ev)
         torch.cuda.synchronize()
         qa.append(ev[0].elapsed_time(ev[1]))
@@ -228,6 +231,7 @@ def _time_events(fn, reps=20, warm=3):
     ts = []
     for _ in range(reps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)   # the host enqueues fn while the GPU spins
         e0.record()
         fn()
         e1.record()
