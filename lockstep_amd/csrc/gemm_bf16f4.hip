@@ -34,13 +34,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 namespace w4 {
-constexpr int BR = 256;        // A rows per workgroup (all batches)
-constexpr int BN = 256;        // weight columns per workgroup
 constexpr int BK = 64;         // K per stage
 constexpr int A_ROW_B = BK * 2;    // 128 bytes of bf16 per A row per stage
 constexpr int W_ROW_B = BK / 2;    // 32 bytes of codes per W row per stage
 constexpr int NT = 256;
-constexpr int WT = 128;
 constexpr int GROUP_M = 4;
 }  // namespace w4
 
@@ -86,11 +83,20 @@ LSMX_DEV float e8m0_scale_f32(uint32_t e) {
     return e == 0u ? u2f(0x00400000u) : (e == 255u ? u2f(0x7FC00000u) : u2f(e << 23));
 }
 
-template <int NB, bool SF32, int CT>
-__global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
+// BR A rows (all batches) x BN weight columns per workgroup of 4 waves in a
+// 2 x 2 grid: 256 x 256 for large M; 128 x 128 or 128 x 64 (several
+// workgroups per CU) when larger tiles would leave CUs idle.
+template <int NB, bool SF32, int CT, int BR, int BN>
+__global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(GemmArgs g) {
     using namespace w4;
-    constexpr int RPB = BR / NB;   // A rows per batch per workgroup
-    constexpr int RT = 4 / NB;     // row tiles per batch per wave
+    constexpr int RPB = BR / NB;           // A rows per batch per workgroup
+    constexpr int RT = BR / 64 / NB;       // row tiles per batch per wave
+    constexpr int WT = BN / 2;             // weight columns per wave
+    constexpr int CTW = WT / 32;           // column tiles per wave
+    constexpr int XA = BR * A_ROW_B / 16 / NT;   // A chunks per thread per stage
+    constexpr int XW = BN * W_ROW_B / 16 / NT;   // W chunks per thread per stage (0 for BN = 64: threads
+                                                 // t and t + 128 load the same chunk)
+    static_assert(RT >= 1 && CTW >= 1, "tile too small");
     __shared__ __attribute__((aligned(16))) uint8_t sA[2][BR * A_ROW_B];   // 2 x 32 KiB
     __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * W_ROW_B];   // 2 x 8 KiB, [half][col][16B]
     __shared__ uint32_t sS[2][BN];
@@ -105,11 +111,11 @@ __global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
     const int wm = wave >> 1, wn = wave & 1;
     const int nk = (int)(g.K / BK);
 
-    // A staging: 8 chunks of 16 B per thread; row = q >> 3, chunk = q & 7
-    const uint8_t *ga[8];
-    int a_off[8];
+    // A staging: XA chunks of 16 B per thread; row = q >> 3, chunk = q & 7
+    const uint8_t *ga[XA];
+    int a_off[XA];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < XA; ++i) {
         const int q = i * NT + t;
         const int row = q >> 3, c = q & 7;
         const int b = row / RPB, r = row % RPB;
@@ -118,43 +124,47 @@ __global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
         ga[i] = base + am * g.lda * 2 + c * 16;
         a_off[i] = row * A_ROW_B + ((c ^ a_swz(row)) << 4);
     }
-    // W staging: 2 chunks per thread; row = q >> 1, half = q & 1
-    const uint8_t *gw[2];
-    int w_off[2];
+    // W staging: 2 chunks (one per block half) per weight row; with BN = 128
+    // the 256 threads cover the 256 chunks once, with BN = 64 twice
+    constexpr int XW1 = XW > 0 ? XW : 1;
+    const uint8_t *gw[XW1];
+    int w_off[XW1];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int q = i * NT + t;
+    for (int i = 0; i < XW1; ++i) {
+        const int q = (i * NT + t) % (2 * BN);
         const int row = q >> 1, h = q & 1;
         const int64_t wn_ = min(n0 + row, g.N - 1);
         gw[i] = g.b + wn_ * g.ldb + h * 16;
         w_off[i] = h * (BN * 16) + row * 16;
     }
-    const int64_t s_row = min(n0 + t, g.N - 1) * g.ld_sb;
+    // thread t < BN stages the scales of weight column t (threads past BN
+    // load a clamped column and store nothing)
+    const int64_t s_row = min(n0 + (t % BN), g.N - 1) * g.ld_sb;
 
-    u32x4 ra[8], rw[2];
+    u32x4 ra[XA], rw[XW1];
     uint32_t rs;
     auto gload = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(ga[i] + (int64_t)kt * A_ROW_B);
+        for (int i = 0; i < XA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(ga[i] + (int64_t)kt * A_ROW_B);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) rw[i] = *reinterpret_cast<const u32x4 *>(gw[i] + (int64_t)kt * W_ROW_B);
+        for (int i = 0; i < XW1; ++i) rw[i] = *reinterpret_cast<const u32x4 *>(gw[i] + (int64_t)kt * W_ROW_B);
         rs = load_scale2<SF32>(g.sb, s_row + (int64_t)kt * 2);
     };
     auto swrite = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&sA[buf][a_off[i]]) = ra[i];
+        for (int i = 0; i < XA; ++i) *reinterpret_cast<u32x4 *>(&sA[buf][a_off[i]]) = ra[i];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4 *>(&sW[buf][w_off[i]]) = rw[i];
-        sS[buf][t] = rs;
+        for (int i = 0; i < XW1; ++i) *reinterpret_cast<u32x4 *>(&sW[buf][w_off[i]]) = rw[i];
+        if (BN == NT || t < BN) sS[buf][t % BN] = rs;
     };
 
-    v16f acc[NB][RT][4];
+    v16f acc[NB][RT][CTW];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int i = 0; i < RT; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < CTW; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[b][i][j][e] = 0.0f;
 
@@ -168,11 +178,11 @@ __global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
         const int buf = kt & 1;
         if (kt + 1 < nk) gload(kt + 1);
 
-        // dequantize this wave's 4 weight column tiles for the stage:
+        // dequantize this wave's CTW weight column tiles for the stage:
         // 32 codes of block `half` -> 32 bf16, 8 per K=16 step.
-        v8bf fw[4][4];  // [col tile][step]
+        v8bf fw[CTW][4];  // [col tile][step]
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < CTW; ++j) {
             const int col = wn * WT + j * 32 + frow;
             const u32x4 pw = *reinterpret_cast<const u32x4 *>(&sW[buf][half * (BN * 16) + col * 16]);
             const float sc = e8m0_scale_f32((sS[buf][col] >> (8 * half)) & 0xFF);
@@ -201,7 +211,7 @@ __global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
 #pragma unroll
                 for (int i = 0; i < RT; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < CTW; ++j)
                         acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[b][i], fw[j][s], acc[b][i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) swrite(buf ^ 1);
@@ -214,7 +224,7 @@ __global__ __launch_bounds__(w4::NT, 1) void gemm_bf16f4_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < RT; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < CTW; ++j) {
                 const int64_t col = n0 + wn * WT + j * 32 + frow;
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
@@ -418,13 +428,13 @@ static hipError_t launch_skinny(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int NB>
+template <int NB, int BR, int BN>
 static hipError_t launch_w4(const GemmArgs &g, hipStream_t s) {
-    constexpr int RPB = w4::BR / NB;
-    const int tiles = (int)(((g.M + RPB - 1) / RPB) * ((g.N + w4::BN - 1) / w4::BN));
+    constexpr int RPB = BR / NB;
+    const int tiles = (int)(((g.M + RPB - 1) / RPB) * ((g.N + BN - 1) / BN));
     const dim3 grid(tiles), blk(w4::NT);
     const bool f = g.scale_fmt == LSMX_SCALE_F32;
-#define LSMX_W(F, CT) hipLaunchKernelGGL((gemm_bf16f4_kernel<NB, F, CT>), grid, blk, 0, s, g)
+#define LSMX_W(F, CT) hipLaunchKernelGGL((gemm_bf16f4_kernel<NB, F, CT, BR, BN>), grid, blk, 0, s, g)
     if (f) {
         if (g.c_dtype == LSMX_F32) LSMX_W(true, LSMX_F32);
         else if (g.c_dtype == LSMX_BF16) LSMX_W(true, LSMX_BF16);
@@ -438,10 +448,21 @@ static hipError_t launch_w4(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
+// the largest tile that still gives every CU a workgroup: 256 x 256, then
+// 128 x 128, then 128 x 64 (mid M, e.g. 128 rows against 14336 columns)
+template <int NB>
+static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
+    auto tiles = [&](int br, int bn) { return ((g.M + br / NB - 1) / (br / NB)) * ((g.N + bn - 1) / bn); };
+    const int64_t cus = num_cus_w();
+    if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
+    if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
+    return launch_w4<NB, 128, 64>(g, s);
+}
+
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
     // the same M picks the same kernel for the single and the dual form
     if (g.M <= LSMX_SKINNY_MAX_M && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
-    return g.a1 ? launch_w4<2>(g, s) : launch_w4<1>(g, s);
+    return g.a1 ? launch_w4_any<2>(g, s) : launch_w4_any<1>(g, s);
 }
 
 }  // namespace lsmx

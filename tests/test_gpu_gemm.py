@@ -145,6 +145,24 @@ def test_weight_only_bf16_x_fp4(dev, mods, oracle, out_dtype, M, N, K):
         assert oracle.max_rel(got.float().cpu().numpy(), ref) <= TOL[out_dtype]
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 512), (128, 14336, 512), (1000, 1000, 256)])
+def test_weight_only_tile_paths(dev, mods, oracle, M, N, K):
+    """Large M runs 256 x 256 tiles, mid M (cfg3's M = 128) 128 x 128 tiles:
+    both match the fp64 oracle on sampled rows, and give the same bits."""
+    fp4, mg, _, _ = mods
+    g = torch.Generator(device=dev).manual_seed(M + N)
+    a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    c = mg.mxfp4_gemm_bf16(a, wpk, we8, out_dtype=torch.float32)
+    rows = np.arange(0, M, max(1, M // 48))
+    ref = oracle.reference_gemm_wonly(a.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy(), rows=rows)
+    assert oracle.max_rel(c.cpu().numpy()[rows], ref) <= 1e-5
+    # a row slice runs a different tile size (or grid) and must give the same bits
+    part = mg.mxfp4_gemm_bf16(a[:64 + M // 4], wpk, we8, out_dtype=torch.float32)
+    assert torch.equal(part, c[:64 + M // 4])
+
+
 @pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (100, 300, 256), (1, 256, 128)])
 def test_dual_batch_matches_single_and_oracle(dev, mods, oracle, M, N, K):
     """cfg2 (and ragged shapes): two bf16 batches share one MXFP4 weight."""
