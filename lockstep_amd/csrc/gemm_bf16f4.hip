@@ -386,6 +386,171 @@ __global__ __launch_bounds__(64 * sk::WK, MT <= 2 ? 4 : 2) void gemm_bf16f4_skin
     }
 }
 
+// ------------------------------------------------------------------ GEMV
+// For one or two activation rows per batch (decode) the whole cost is reading
+// W once, and the matrix cores have almost nothing to do.  This kernel reads
+// W with fully contiguous loads and does the arithmetic on the VALU:
+//   - the activation rows are staged once per workgroup in LDS;
+//   - a wave owns GV_RPW weight rows; lane l takes the MX blocks l, l + 64,
+//     l + 128, ... of every row, so each load instruction reads 1 KiB of one
+//     row in one piece, and all of a wave's weight loads are issued before
+//     any arithmetic;
+//   - v_cvt_scalef32_pk_bf16_fp4 expands a block to 32 bf16 (exact, block
+//     scale applied) and v_dot2_f32_bf16 multiplies pairs with the
+//     activations;
+//   - the 64 lane partial sums of each (row, activation row) are added with a
+//     fixed butterfly, so the order depends on K only.
+// VM is the number of virtual activation rows (M, or 2M in dual mode).
+namespace gv {
+constexpr int NT = 512;   // 8 waves
+constexpr int RPW = 4;    // weight rows per wave
+constexpr int UB = 2;     // groups of 64 blocks per lane in flight
+}  // namespace gv
+
+template <int VM, bool SF32, int CT>
+__global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
+    using namespace gv;
+    extern __shared__ __attribute__((aligned(16))) uint8_t sact[];   // [VM][K] bf16
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int64_t n0 = ((int64_t)blockIdx.x * (NT / 64) + wave) * RPW;
+    const int nblk = (int)(g.K / 32);
+    const bool dual = g.a1 != nullptr;
+
+    // stage the activation rows: 16 bytes per thread per step
+    {
+        const int per_row = (int)(g.K / 8);   // 16-byte chunks per row
+        for (int i = t; i < VM * per_row; i += NT) {
+            const int m = i / per_row, c = i - m * per_row;
+            const bool second = dual && m >= (int)g.M;
+            const uint8_t *src = (second ? g.a1 : g.a) + (int64_t)(second ? m - g.M : m) * g.lda * 2 + c * 16;
+            *reinterpret_cast<u32x4 *>(sact + ((int64_t)m * g.K * 2 + c * 16)) = *reinterpret_cast<const u32x4 *>(src);
+        }
+    }
+
+    const uint8_t *wrow[RPW];
+    const uint8_t *srow[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int64_t n = min(n0 + r, g.N - 1);
+        wrow[r] = g.b + n * g.ldb;
+        srow[r] = reinterpret_cast<const uint8_t *>(g.sb) + n * g.ld_sb * (SF32 ? 4 : 1);
+    }
+
+    float acc[RPW][VM];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int m = 0; m < VM; ++m) acc[r][m] = 0.0f;
+
+    u32x4 w[UB][RPW];
+    uint32_t e[UB][RPW];
+    // weight and scale loads of the UB block groups starting at b0 (blocks
+    // past the row are skipped)
+    auto wload = [&](int b0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+            const int b = b0 + 64 * u;
+            if (b < nblk) {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow[r] + (int64_t)b * 16));
+                    e[u][r] = SF32 ? (f2u(reinterpret_cast<const float *>(srow[r])[b]) >> 23) & 0xFF : srow[r][b];
+                }
+            }
+        }
+    };
+    wload(lane);       // the first weight loads are in flight across the barrier
+    __syncthreads();
+    for (int b0 = lane; b0 < nblk;) {
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+            const int b = b0 + 64 * u;
+            if (b >= nblk) break;
+            u32x4 av[VM][4];  // 32 bf16 of activation row m at K = 32b
+#pragma unroll
+            for (int m = 0; m < VM; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    av[m][q] = *reinterpret_cast<const u32x4 *>(sact + ((int64_t)m * g.K * 2 + (int64_t)b * 64 + q * 16));
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const float sc = e8m0_scale_f32(e[u][r]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    // dword q of the block: codes 8q .. 8q+7, low nibble first
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const v2bf d = p == 0 ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[u][r][q], sc, 0)
+                                     : p == 1 ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[u][r][q], sc, 1)
+                                     : p == 2 ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[u][r][q], sc, 2)
+                                              : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[u][r][q], sc, 3);
+#pragma unroll
+                        for (int m = 0; m < VM; ++m) {  // activations 8q + 2p, 8q + 2p + 1 of the block
+                            const u32x4 aq = av[m][q];
+                            const uint32_t ap = p == 0 ? aq.x : p == 1 ? aq.y : p == 2 ? aq.z : aq.w;
+                            acc[r][m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, ap), d, acc[r][m], false);
+                        }
+                    }
+                }
+            }
+        }
+        b0 += 64 * UB;
+        if (b0 < nblk) wload(b0);
+    }
+
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int m = 0; m < VM; ++m) {
+            float v = acc[r][m];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+            acc[r][m] = v;
+        }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int64_t n = n0 + r;
+            if (n >= g.N) continue;
+#pragma unroll
+            for (int m = 0; m < VM; ++m) {
+                if (m >= (dual ? 2 * g.M : g.M)) continue;
+                const bool second = dual && m >= (int)g.M;
+                const int64_t idx = (int64_t)(second ? m - g.M : m) * g.ldc + n;
+                store_cw<CT>(second ? g.c1 : g.c, idx, acc[r][m]);
+            }
+        }
+    }
+}
+
+#ifndef LSMX_GEMV_MAX_M
+#define LSMX_GEMV_MAX_M 2
+#endif
+constexpr int64_t kGemvMaxLds = 64 * 1024;   // activation bytes staged per workgroup
+
+static hipError_t launch_gemv(const GemmArgs &g, hipStream_t s) {
+    const int vm = (int)(g.a1 ? 2 * g.M : g.M);
+    const int vmt = vm == 1 ? 1 : vm == 2 ? 2 : 4;
+    const size_t lds = (size_t)vmt * g.K * 2;
+    const int rows_per_wg = (gv::NT / 64) * gv::RPW;
+    const dim3 grid((unsigned)((g.N + rows_per_wg - 1) / rows_per_wg)), blk(gv::NT);
+    const bool f = g.scale_fmt == LSMX_SCALE_F32;
+#define LSMX_V(VMT, F, CT) hipLaunchKernelGGL((gemv_bf16f4_kernel<VMT, F, CT>), grid, blk, lds, s, g)
+#define LSMX_VC(VMT, F)                                               \
+    do {                                                              \
+        if (g.c_dtype == LSMX_F32) LSMX_V(VMT, F, LSMX_F32);          \
+        else if (g.c_dtype == LSMX_BF16) LSMX_V(VMT, F, LSMX_BF16);   \
+        else LSMX_V(VMT, F, LSMX_F16);                                \
+    } while (0)
+    if (vmt == 1) { if (f) LSMX_VC(1, true); else LSMX_VC(1, false); }
+    else if (vmt == 2) { if (f) LSMX_VC(2, true); else LSMX_VC(2, false); }
+    else { if (f) LSMX_VC(4, true); else LSMX_VC(4, false); }
+#undef LSMX_VC
+#undef LSMX_V
+    return hipGetLastError();
+}
+
 #ifndef LSMX_SKINNY_MAX_M
 #define LSMX_SKINNY_MAX_M 64
 #endif
@@ -461,6 +626,9 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
     // the same M picks the same kernel for the single and the dual form
+    // GEMV when the dual form's 2M activation rows of K bf16 fit in LDS (the
+    // test depends on M and K only, so single and dual launches agree)
+    if (g.M <= LSMX_GEMV_MAX_M && 2 * g.M * g.K * 2 <= kGemvMaxLds) return launch_gemv(g, s);
     if (g.M <= LSMX_SKINNY_MAX_M && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
     return g.a1 ? launch_w4_any<2>(g, s) : launch_w4_any<1>(g, s);
 }

@@ -131,8 +131,8 @@ def test_full_size_8192_cubed_sampled(dev, mods, oracle):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (16, 300, 512), (100, 512, 128), (256, 256, 1024),
-                                   (513, 1024, 256)])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (2, 300, 640), (1, 14336, 4096), (16, 300, 512), (100, 512, 128),
+                                   (256, 256, 1024), (513, 1024, 256)])
 def test_weight_only_bf16_x_fp4(dev, mods, oracle, out_dtype, M, N, K):
     fp4, mg, _, _ = mods
     a = gen.to_bf16_bits(gen.normal(M + 5 * K, (M, K)))
@@ -163,7 +163,7 @@ def test_weight_only_tile_paths(dev, mods, oracle, M, N, K):
     assert torch.equal(part, c[:64 + M // 4])
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (100, 300, 256), (1, 256, 128)])
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (100, 300, 256), (1, 256, 128), (2, 520, 384), (1, 4096, 4096)])
 def test_dual_batch_matches_single_and_oracle(dev, mods, oracle, M, N, K):
     """cfg2 (and ragged shapes): two bf16 batches share one MXFP4 weight."""
     fp4, mg, dg, _ = mods
