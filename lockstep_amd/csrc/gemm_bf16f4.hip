@@ -23,7 +23,9 @@
 // 128 x 128 per wave (4 x 4 MFMA tiles).  In dual mode the 256 A rows are
 // 128 rows of A0 followed by the same 128 rows of A1: one weight tile in LDS
 // feeds both batches and is read from memory once per stage.
+#include "lsmx_dma.h"
 #include "lsmx_internal.h"
+#include "lsmx_sched.h"
 
 namespace lsmx {
 
@@ -233,6 +235,208 @@ __global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(
                 }
             }
     }
+}
+
+// ------------------------------------------------------------------ ring
+// The large-M form: 256 "A rows" x 256 weight columns per workgroup of 8 waves
+// (4 x 2, 64 x 128 per wave: two waves per SIMD, so one wave's MFMAs run
+// while the other waits), a 3-slot LDS ring filled by direct-to-LDS loads
+// (no VGPR staging), one barrier per 64-deep K stage.
+//   - A stage is 128 bytes of every A row (64 bf16; 8 rows per load
+//     instruction, chunk-swizzled) and 32 bytes of every W row (64 codes, two
+//     MX blocks; 32 rows per load instruction).  Rows past the operand read
+//     zeros through the buffer descriptor.
+//   - At the barrier of stage u every wave has its own loads of stage u in
+//     LDS and has finished stage u - 1, so the slot of stage u - 1 is free
+//     and the loads of stage u + 2 go there, spread over the K-steps.
+//     Stages past the end re-load the last stage (same slot pattern, no
+//     branch), and the kernel waits for them before it exits.
+//   - K positions: at K-step s lane half h supplies A[row][32h + 8s .. +8]
+//     and the codes 8s .. 8s+7 of W's block h, so a lane dequantizes one
+//     16-byte block per column tile per stage with one scale.
+//   - E8M0 block scales (row-major [N, K/32]) ride in the same ring: one dword
+//     per weight row per stage holds the scales of this stage and its
+//     neighbour (scale rows must be dword-aligned; fp32 scales use the
+//     VGPR-staged kernel).  Every wave issues one scale load (waves w and
+//     w + 4 write the same bytes), so all waves count the same loads.
+namespace wr {
+constexpr int BR = 256, BN = 256, BK = 64;
+constexpr int NW = 8, NT = 64 * NW, S = 3;
+constexpr int A_ROW_B = BK * 2, W_ROW_B = BK / 2;
+constexpr int A_SLOT = BR * A_ROW_B, W_SLOT = BN * W_ROW_B;   // 32 KiB, 8 KiB
+constexpr int XA = A_SLOT / 1024 / NW;                        // A load instructions per wave per stage (4)
+constexpr int L = XA + 2;                                     // + one W load + one scale load
+constexpr int GROUP_M = 4;
+LSMX_DEV int swz(int row) { return (row >> 1) & 7; }
+}  // namespace wr
+
+template <int NB, int CT>
+__global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g) {
+    using namespace wr;
+    constexpr int RPB = BR / NB;        // A rows per batch per workgroup
+    constexpr int TM = 2, TN = 4;       // 32 x 32 tiles per wave
+    __shared__ __attribute__((aligned(16))) uint8_t sA[S][A_SLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t sW[S][W_SLOT];
+    __shared__ __attribute__((aligned(16))) uint32_t sS[S][BN];
+
+    const int tiles_m = (int)((g.M + RPB - 1) / RPB), tiles_n = (int)((g.N + BN - 1) / BN);
+    int tm, tn;
+    tile_coords((int)blockIdx.x, tiles_m, tiles_n, GROUP_M, tm, tn);
+    const int64_t m0 = (int64_t)tm * RPB, n0 = (int64_t)tn * BN;
+    const int nk = (int)(g.K / BK);
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int frow = lane & 31, half = lane >> 5;
+
+    // ---- DMA addressing.  A load i of wave w covers slot rows
+    // (i*NW + w)*8 .. +7: lane -> row + lane/8, LDS chunk lane%8 holding source
+    // chunk (lane%8) ^ swz(row).  All 8 rows of one instruction lie in one batch.
+    const int64_t lda_b = g.lda * 2;
+    const int arow_l = lane >> 3;
+    uint32_t a_off[XA];
+    const uint8_t *a_base[XA];
+    int64_t a_rows[XA];
+#pragma unroll
+    for (int i = 0; i < XA; ++i) {
+        const int r0 = (i * NW + wave) * 8;            // first slot row, wave-uniform
+        const int b = NB == 2 ? r0 / RPB : 0;
+        const int rb = r0 - b * RPB;                    // row inside the batch tile
+        const int row = r0 + arow_l;
+        a_off[i] = (uint32_t)(arow_l * lda_b + (((lane & 7) ^ swz(row)) << 4));
+        a_base[i] = (b ? g.a1 : g.a) + (m0 + rb) * lda_b;
+        a_rows[i] = g.M - (m0 + rb);                    // rows left in the operand from this instruction's first row
+    }
+    // W: wave w loads slot rows w*32 .. +31, lane -> row lane/2, 16-byte half lane%2
+    const uint32_t w_off = (uint32_t)((lane >> 1) * g.ldb + (lane & 1) * 16);
+    const uint8_t *w_base = g.b + (n0 + wave * 32) * g.ldb;
+    const int64_t w_rows = g.N - (n0 + wave * 32);
+    // scales: wave w loads the dwords of weight rows (w & 3)*64 + lane
+    const int64_t s_rows = g.N - n0;
+    const uint8_t *s_base = reinterpret_cast<const uint8_t *>(g.sb) + n0 * g.ld_sb;
+    const uint32_t s_off = (uint32_t)((((wave & 3) * 64) + lane) * g.ld_sb);
+
+    auto issue = [&](int kt, int slot, int q) __attribute__((always_inline)) {
+        const int64_t ko = (int64_t)kt * A_ROW_B;
+        if (q < XA) {
+            const int64_t rows = a_rows[q] < 8 ? (a_rows[q] > 0 ? a_rows[q] : 0) : 8;
+            const uint64_t bytes = rows > 0 ? (uint64_t)((rows - 1) * lda_b + g.K * 2 - ko) : 0;
+            dma_x4(a_off[q], buf_rsrc(a_base[q] + ko, bytes),
+                   lds_u32(&sA[0][0]) + slot * A_SLOT + (q * NW + wave) * 1024);
+        } else if (q == XA) {
+            const int64_t kw = (int64_t)kt * W_ROW_B;
+            const int64_t rows = w_rows < 32 ? (w_rows > 0 ? w_rows : 0) : 32;
+            const uint64_t bytes = rows > 0 ? (uint64_t)((rows - 1) * g.ldb + g.K / 2 - kw) : 0;
+            dma_x4(w_off, buf_rsrc(w_base + kw, bytes), lds_u32(&sW[0][0]) + slot * W_SLOT + wave * 1024);
+        } else {
+            // the dword holding blocks 4*(kt/2) .. +3 of each weight row (K % 128 == 0 keeps it in the row)
+            const int64_t ks = (int64_t)(kt >> 1) * 4;
+            const int64_t rows = s_rows < BN ? s_rows : BN;
+            const uint64_t bytes = (uint64_t)((rows - 1) * g.ld_sb + g.K / 32 - ks);
+            dma_x1(s_off, buf_rsrc(s_base + ks, bytes), lds_u32(&sS[0][0]) + slot * (BN * 4) + (wave & 3) * 256);
+        }
+    };
+
+
+    v16f acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // prologue: stages 0 and 1 in flight
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int q = 0; q < L; ++q) issue(p < nk ? p : nk - 1, p, q);
+
+    const int rowA[TM] = {wm * 64 + frow, wm * 64 + 32 + frow};
+    for (int u = 0; u < nk; ++u) {
+        const int slot = u % S;
+        // this thread's loads of stage u have landed (only stage u + 1's may
+        // be outstanding); after the barrier everyone's have, and slot
+        // (u + 2) % 3 = (u - 1) % 3 is no longer read
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(L) : "memory");
+        const int kn = u + 2 < nk ? u + 2 : nk - 1;
+        const int sn = (u + 2) % S;
+        // W blocks of this lane's 4 columns for the stage, dequantized per K-step
+        u32x4 wblk[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            wblk[j] = *reinterpret_cast<const u32x4 *>(&sW[slot][(wn * 128 + j * 32 + frow) * W_ROW_B + half * 16]);
+        float sc[TN];
+        const int sh = 8 * (2 * (u & 1) + half);   // byte of this stage's block h in the dword
+#pragma unroll
+        for (int j = 0; j < TN; ++j) sc[j] = e8m0_scale_f32((sS[slot][wn * 128 + j * 32 + frow] >> sh) & 0xFF);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            v8bf fa[TM];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int r = rowA[i];
+                fa[i] = *reinterpret_cast<const v8bf *>(&sA[slot][r * A_ROW_B + (((4 * half + st) ^ swz(r)) << 4)]);
+            }
+            v8bf fw[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const uint32_t p = wblk[j][st];
+                const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 0);
+                const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 1);
+                const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 2);
+                const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 3);
+                fw[j] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+            }
+            // loads of stage u + 2, spread over the K-steps
+#pragma unroll
+            for (int q = 0; q < L; ++q)
+                if ((q * 4) / L == st) issue(kn, sn, q);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fw[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    // no load may still be writing this workgroup's LDS when it exits
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // epilogue: acc element e of tile (i, j) is row i*32 + 8*(e/4) + 4*half + e%4, column j*32 + frow
+    const int b = NB == 2 ? (wm * 64) / RPB : 0;
+    void *cb = b ? g.c1 : g.c;
+    const int64_t rbase = m0 + wm * 64 - b * RPB;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int64_t col = n0 + wn * 128 + j * 32 + frow;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int64_t row = rbase + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                if (row < g.M && col < g.N) store_cw<CT>(cb, row * g.ldc + col, acc[i][j][e]);
+            }
+        }
+}
+
+template <int NB>
+static hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
+    constexpr int RPB = wr::BR / NB;
+    const int tiles = (int)(((g.M + RPB - 1) / RPB) * ((g.N + wr::BN - 1) / wr::BN));
+    const dim3 grid(tiles), blk(wr::NT);
+#define LSMX_R(CT) hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT>), grid, blk, 0, s, g)
+    if (g.c_dtype == LSMX_F32) LSMX_R(LSMX_F32);
+    else if (g.c_dtype == LSMX_BF16) LSMX_R(LSMX_BF16);
+    else LSMX_R(LSMX_F16);
+#undef LSMX_R
+    return hipGetLastError();
+}
+
+// the ring kernel reads E8M0 scales a dword at a time
+static bool ring_ok(const GemmArgs &g) {
+    return g.scale_fmt == LSMX_SCALE_E8M0 && g.ld_sb % 4 == 0 && (reinterpret_cast<uintptr_t>(g.sb) & 3) == 0 &&
+           g.K % 128 == 0;
 }
 
 // ------------------------------------------------------------------ skinny M
@@ -619,7 +823,10 @@ template <int NB>
 static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
     auto tiles = [&](int br, int bn) { return ((g.M + br / NB - 1) / (br / NB)) * ((g.N + bn - 1) / bn); };
     const int64_t cus = num_cus_w();
-    if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
+#ifndef LSMX_W4_RING
+#define LSMX_W4_RING 1
+#endif
+    if (tiles(256, 256) >= cus) return LSMX_W4_RING && ring_ok(g) ? launch_ring<NB>(g, s) : launch_w4<NB, 256, 256>(g, s);
     if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
     return launch_w4<NB, 128, 64>(g, s);
 }
