@@ -254,18 +254,20 @@ __global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(
 //   - K positions: at K-step s lane half h supplies A[row][32h + 8s .. +8]
 //     and the codes 8s .. 8s+7 of W's block h, so a lane dequantizes one
 //     16-byte block per column tile per stage with one scale.
-//   - E8M0 block scales (row-major [N, K/32]) ride in the same ring: one dword
-//     per weight row per stage holds the scales of this stage and its
-//     neighbour (scale rows must be dword-aligned; fp32 scales use the
-//     VGPR-staged kernel).  Every wave issues one scale load (waves w and
-//     w + 4 write the same bytes), so all waves count the same loads.
+//   - A W load instruction covers 32 weight rows; its 1 KiB of LDS holds the
+//     first 16-byte halves of those rows, then the second halves, so the 16
+//     lanes a ds_read_b128 serves per cycle read 256 contiguous bytes.
+//   - E8M0 block scales (row-major [N, K/32]) come 16 bytes per weight row =
+//     8 stages at a time, into a 2-deep LDS buffer; the load for stages
+//     8g .. 8g+7 is issued first in stage 8g - 2 (scale rows must be 16-byte
+//     multiples: K % 512 == 0; fp32 scales use the VGPR-staged kernel).
 namespace wr {
 constexpr int BR = 256, BN = 256, BK = 64;
 constexpr int NW = 8, NT = 64 * NW, S = 3;
 constexpr int A_ROW_B = BK * 2, W_ROW_B = BK / 2;
 constexpr int A_SLOT = BR * A_ROW_B, W_SLOT = BN * W_ROW_B;   // 32 KiB, 8 KiB
 constexpr int XA = A_SLOT / 1024 / NW;                        // A load instructions per wave per stage (4)
-constexpr int L = XA + 2;                                     // + one W load + one scale load
+constexpr int L = XA + 1;                                     // + one W load (scales: one more every 8 stages)
 constexpr int GROUP_M = 4;
 LSMX_DEV int swz(int row) { return (row >> 1) & 7; }
 }  // namespace wr
@@ -277,7 +279,7 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     constexpr int TM = 2, TN = 4;       // 32 x 32 tiles per wave
     __shared__ __attribute__((aligned(16))) uint8_t sA[S][A_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t sW[S][W_SLOT];
-    __shared__ __attribute__((aligned(16))) uint32_t sS[S][BN];
+    __shared__ __attribute__((aligned(16))) uint8_t sS[2][BN * 16];   // [group & 1][row][16 scale bytes]
 
     const int tiles_m = (int)((g.M + RPB - 1) / RPB), tiles_n = (int)((g.N + BN - 1) / BN);
     int tm, tn;
@@ -308,14 +310,21 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         a_base[i] = (b ? g.a1 : g.a) + (m0 + rb) * lda_b;
         a_rows[i] = g.M - (m0 + rb);                    // rows left in the operand from this instruction's first row
     }
-    // W: wave w loads slot rows w*32 .. +31, lane -> row lane/2, 16-byte half lane%2
-    const uint32_t w_off = (uint32_t)((lane >> 1) * g.ldb + (lane & 1) * 16);
+    // W: wave w loads slot rows w*32 .. +31, lane -> row lane%32, 16-byte half lane/32
+    const uint32_t w_off = (uint32_t)((lane & 31) * g.ldb + (lane >> 5) * 16);
     const uint8_t *w_base = g.b + (n0 + wave * 32) * g.ldb;
     const int64_t w_rows = g.N - (n0 + wave * 32);
-    // scales: wave w loads the dwords of weight rows (w & 3)*64 + lane
+    // scales: wave w loads 16 bytes of weight rows (w & 3)*64 + lane (waves w
+    // and w + 4 write the same bytes, so every wave counts the same loads)
     const int64_t s_rows = g.N - n0;
     const uint8_t *s_base = reinterpret_cast<const uint8_t *>(g.sb) + n0 * g.ld_sb;
     const uint32_t s_off = (uint32_t)((((wave & 3) * 64) + lane) * g.ld_sb);
+    auto issue_scales = [&](int grp) __attribute__((always_inline)) {
+        const int64_t ks = (int64_t)grp * 16;
+        const int64_t rows = s_rows < BN ? s_rows : BN;
+        const uint64_t bytes = (uint64_t)((rows - 1) * g.ld_sb + g.K / 32 - ks);
+        dma_x4(s_off, buf_rsrc(s_base + ks, bytes), lds_u32(&sS[grp & 1][0]) + (wave & 3) * 1024);
+    };
 
     auto issue = [&](int kt, int slot, int q) __attribute__((always_inline)) {
         const int64_t ko = (int64_t)kt * A_ROW_B;
@@ -324,17 +333,11 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
             const uint64_t bytes = rows > 0 ? (uint64_t)((rows - 1) * lda_b + g.K * 2 - ko) : 0;
             dma_x4(a_off[q], buf_rsrc(a_base[q] + ko, bytes),
                    lds_u32(&sA[0][0]) + slot * A_SLOT + (q * NW + wave) * 1024);
-        } else if (q == XA) {
+        } else {
             const int64_t kw = (int64_t)kt * W_ROW_B;
             const int64_t rows = w_rows < 32 ? (w_rows > 0 ? w_rows : 0) : 32;
             const uint64_t bytes = rows > 0 ? (uint64_t)((rows - 1) * g.ldb + g.K / 2 - kw) : 0;
             dma_x4(w_off, buf_rsrc(w_base + kw, bytes), lds_u32(&sW[0][0]) + slot * W_SLOT + wave * 1024);
-        } else {
-            // the dword holding blocks 4*(kt/2) .. +3 of each weight row (K % 128 == 0 keeps it in the row)
-            const int64_t ks = (int64_t)(kt >> 1) * 4;
-            const int64_t rows = s_rows < BN ? s_rows : BN;
-            const uint64_t bytes = (uint64_t)((rows - 1) * g.ld_sb + g.K / 32 - ks);
-            dma_x1(s_off, buf_rsrc(s_base + ks, bytes), lds_u32(&sS[0][0]) + slot * (BN * 4) + (wave & 3) * 256);
         }
     };
 
@@ -347,7 +350,8 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // prologue: stages 0 and 1 in flight
+    // prologue: scales of stages 0..7, stages 0 and 1 in flight
+    issue_scales(0);
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -362,23 +366,33 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(L) : "memory");
         const int kn = u + 2 < nk ? u + 2 : nk - 1;
         const int sn = (u + 2) % S;
-        // W blocks of this lane's 4 columns for the stage, dequantized per K-step
+        // scales of the next group of 8 stages, first of this stage's loads
+        // (the next stage's vmcnt wait then also covers it)
+        if ((u & 7) == 6 && u + 2 < nk) issue_scales((u + 2) >> 3);
+        // all of the stage's LDS reads up front (one latency per stage): W
+        // blocks and scales of this lane's 4 columns, then A fragments of the
+        // 4 K-steps
         u32x4 wblk[TN];
+        uint32_t sraw[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-            wblk[j] = *reinterpret_cast<const u32x4 *>(&sW[slot][(wn * 128 + j * 32 + frow) * W_ROW_B + half * 16]);
-        float sc[TN];
-        const int sh = 8 * (2 * (u & 1) + half);   // byte of this stage's block h in the dword
+        for (int j = 0; j < TN; ++j) {
+            const int col = wn * 128 + j * 32 + frow;
+            wblk[j] = *reinterpret_cast<const u32x4 *>(&sW[slot][(wn * 4 + j) * 1024 + half * 512 + frow * 16]);
+            sraw[j] = sS[(u >> 3) & 1][col * 16 + 2 * (u & 7) + half];
+        }
+        v8bf fa[4][TM];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) sc[j] = e8m0_scale_f32((sS[slot][wn * 128 + j * 32 + frow] >> sh) & 0xFF);
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            v8bf fa[TM];
+        for (int st = 0; st < 4; ++st)
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int r = rowA[i];
-                fa[i] = *reinterpret_cast<const v8bf *>(&sA[slot][r * A_ROW_B + (((4 * half + st) ^ swz(r)) << 4)]);
+                fa[st][i] = *reinterpret_cast<const v8bf *>(&sA[slot][r * A_ROW_B + (((4 * half + st) ^ swz(r)) << 4)]);
             }
+        float sc[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) sc[j] = e8m0_scale_f32(sraw[j]);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
             v8bf fw[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
@@ -397,7 +411,7 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fw[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[st][i], fw[j], acc[i][j], 0, 0, 0);
         }
     }
     // no load may still be writing this workgroup's LDS when it exits
@@ -433,10 +447,10 @@ static hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
-// the ring kernel reads E8M0 scales a dword at a time
+// the ring kernel reads E8M0 scales 16 bytes (8 stages) at a time
 static bool ring_ok(const GemmArgs &g) {
-    return g.scale_fmt == LSMX_SCALE_E8M0 && g.ld_sb % 4 == 0 && (reinterpret_cast<uintptr_t>(g.sb) & 3) == 0 &&
-           g.K % 128 == 0;
+    return g.scale_fmt == LSMX_SCALE_E8M0 && g.ld_sb % 16 == 0 && (reinterpret_cast<uintptr_t>(g.sb) & 15) == 0 &&
+           g.K % 512 == 0;
 }
 
 // ------------------------------------------------------------------ skinny M
