@@ -831,8 +831,9 @@ static hipError_t launch_w4(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
-// the largest tile that still gives every CU a workgroup: 256 x 256, then
-// 128 x 128, then 128 x 64 (mid M, e.g. 128 rows against 14336 columns)
+// the ring kernel (256 x 256 tiles) from half a wave of tiles on, else the
+// largest VGPR-staged tile that still gives every CU a workgroup: 256 x 256,
+// then 128 x 128, then 128 x 64 (mid M, e.g. 128 rows against 14336 columns)
 template <int NB>
 static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
     auto tiles = [&](int br, int bn) { return ((g.M + br / NB - 1) / (br / NB)) * ((g.N + bn - 1) / bn); };
@@ -840,7 +841,9 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 #ifndef LSMX_W4_RING
 #define LSMX_W4_RING 1
 #endif
-    if (tiles(256, 256) >= cus) return LSMX_W4_RING && ring_ok(g) ? launch_ring<NB>(g, s) : launch_w4<NB, 256, 256>(g, s);
+    // the ring kernel is worth it from half a wave of 256 x 256 tiles on (cfg3 M = 1024: 224 tiles)
+    if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB>(g, s);
+    if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
     if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
     return launch_w4<NB, 128, 64>(g, s);
 }
