@@ -103,7 +103,14 @@ def cpu_baseline(n: int):
             times.append(time.perf_counter() - t0)
             del C, A, B
     t = min(times)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": round(2.0 * R * n * n / t / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "cpu_model": model,
             "sample": f"full cfg4 ({R}x{n}x{n}): quantize A and B with the C oracle (OpenMP, "
                       f"{O.num_threads()} threads), dequantize, fp32 A@B^T (numpy/OpenBLAS, {cores} threads); "
                       f"{t:.2f} s per step, best of 2",
