@@ -169,13 +169,15 @@ int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0
  * (mxfp4_gemm.py:29-71), which promotes each 32-block product to fp32 and
  * multiplies fp32 scales; here the scaled MFMA applies the exponents.
  *   a [M, lda] and bt [N, ldb] E4M3 bytes (K-contiguous; the reference's
- *   b_fp8 [K, N] transposed), a_e8m0 [M, ld_sa], b_e8m0 [N, ld_sb] bytes
- *   (lsmx_scale_to_e8m0 of fp4.py's fp32 power-of-two scales),
+ *   b_fp8 [K, N] transposed); scale_fmt LSMX_SCALE_E8M0: a_e8m0 [M, ld_sa],
+ *   b_e8m0 [N, ld_sb] bytes, or LSMX_SCALE_E8M0_KMAJOR (the fast path):
+ *   [K/128, ld_sa, 4] and [K/128, ld_sb, 4] with ld_sa >= M, ld_sb >= N
+ *   (lsmx_scale_to_e8m0 of fp4.py's fp32 power-of-two scales);
  *   c [M, ldc] of c_dtype (LSMX_F32 | LSMX_BF16 | LSMX_F16).  K % 128 == 0
  *   (mxfp4_gemm.py:78). */
 int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *bt,
-                   int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, void *c, int c_dtype, int64_t ldc, int64_t M,
-                   int64_t N, int64_t K, void *stream);
+                   int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, int scale_fmt, void *c, int c_dtype,
+                   int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
 
 /* y[cols, ldy] = x[rows, ldx]^T for elements of elem_bytes = 1, 2 or 4 bytes.
  * Lays out the reference's N-contiguous B operands ([K, N], dual_gemm.py:
@@ -184,11 +186,17 @@ int lsmx_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, in
                    void *stream);
 
 /* E8M0 bytes of fp32 power-of-two scales (their exponent field), the exact
- * inverse of fp4.py:61-69's 2^e: out[r, c] = e8m0(s[r, c]), or with
- * transpose = 1 out[c, r] = e8m0(s[r, c]) (mxfp4_gemm.py:79's b_scale
- * [K/32, N] to [N, K/32]).  A scale that is not a power of two keeps only its
- * exponent. */
-int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+ * inverse of fp4.py:61-69's 2^e.  s is [rows, cols] (stride lds) of scales
+ * of (output row, block) pairs, or with LSMX_E8M0_IN_T in `layout` of
+ * (block, output row) pairs (mxfp4_gemm.py:79's b_scale [K/32, N]).  The
+ * output is row-major [out rows, ldo], or with LSMX_E8M0_OUT_KMAJOR the
+ * K-major [blocks/4, ldo, 4] (blocks % 4 == 0, ldo >= out rows) that the
+ * GEMMs stream fastest.  A scale that is not a power of two in
+ * [2^-127, 2^127] has no E8M0 form and becomes 0xFF (E8M0 NaN), so the
+ * outputs that use it are NaN. */
+#define LSMX_E8M0_IN_T 1
+#define LSMX_E8M0_OUT_KMAJOR 2
+int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, int layout, uint8_t *out,
                        int64_t ldo, void *stream);
 
 #ifdef __cplusplus

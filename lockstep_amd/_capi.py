@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "liblsmx.so"
 OK = 0
 ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_DEVICE, ERR_LAUNCH, ERR_ARG = -1, -2, -3, -4, -5, -6
 F32, BF16, F16, E4M3 = 0, 1, 2, 3
+E8M0_IN_T, E8M0_OUT_KMAJOR = 1, 2
 CODES_PACKED, CODES_UNPACKED = 0, 1
 SCALE_E8M0, SCALE_F32, SCALE_E8M0_KMAJOR = 0, 1, 2
 
@@ -42,7 +43,7 @@ SIGNATURES = {
     "lsmx_gemm_dual_bf16f4": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64,
                               _i64, _vp],
     "lsmx_gemm_dense": [_vp, _vp, _i64, _vp, _vp, _i64, _int, _int, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp],
-    "lsmx_gemm_f8f8": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _vp],
+    "lsmx_gemm_f8f8": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_transpose": [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp],
     "lsmx_scale_to_e8m0": [_vp, _i64, _i64, _i64, _int, _vp, _i64, _vp],
 }

@@ -252,24 +252,31 @@ int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0
 }
 
 int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *bt,
-                   int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, void *c, int c_dtype, int64_t ldc, int64_t M,
-                   int64_t N, int64_t K, void *stream) {
+                   int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, int scale_fmt, void *c, int c_dtype,
+                   int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
     const char *fn = "lsmx_gemm_f8f8";
     if (!a || !a_e8m0 || !bt || !b_e8m0 || !c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
     if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_E8M0_KMAJOR)
+        return fail(LSMX_ERR_DTYPE, "%s: scale_fmt must be E8M0 or K-major E8M0", fn);
     if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
     if (K % 128) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
     if (((M + 127) / 128) * ((N + 127) / 128) > 0x7FFFFFFF)
         return fail(LSMX_ERR_SHAPE, "%s: more than 2^31 - 1 output tiles", fn);
-    if (lda < K || ldb < K || ldc < N || ld_sa < K / 32 || ld_sb < K / 32)
+    const bool km = scale_fmt == LSMX_SCALE_E8M0_KMAJOR;
+    if (lda < K || ldb < K || ldc < N || ld_sa < (km ? M : K / 32) || ld_sb < (km ? N : K / 32))
         return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
     if (!rows16(a, lda, 1) || !rows16(bt, ldb, 1)) return fail(LSMX_ERR_ALIGN, "%s: operand rows must be 16-byte aligned", fn);
+    if (km && (!aligned(a_e8m0, 4) || !aligned(b_e8m0, 4))) return fail(LSMX_ERR_ALIGN, "%s: K-major scales must be 4-byte aligned", fn);
     if (!aligned(c, c_dtype == LSMX_F32 ? 4 : 2)) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (km && (lda > 0x7FFFFFFF / 256 || ldb > 0x7FFFFFFF / 256))
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
     if (int r = device_guard()) return r;
     if (M == 0 || N == 0) return LSMX_OK;
     if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
     lsmx::DenseArgs g{a, nullptr, lda, bt, nullptr, ldb, a_e8m0, b_e8m0, ld_sa, ld_sb, c, nullptr, c_dtype, ldc,
                       M, N, K, K};
+    if (km) return launched(lsmx::launch_gemm_f8f8_kmajor(g, (hipStream_t)stream), fn);
     return launched(lsmx::launch_gemm_f8f8_scaled(g, (hipStream_t)stream), fn);
 }
 
@@ -286,16 +293,20 @@ int lsmx_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, in
     return launched(lsmx::launch_transpose(x, elem_bytes, rows, cols, ldx, y, ldy, (hipStream_t)stream), fn);
 }
 
-int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, int layout, uint8_t *out,
                        int64_t ldo, void *stream) {
     const char *fn = "lsmx_scale_to_e8m0";
     if (!s || !out) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
-    if (rows < 0 || cols < 0 || lds < cols || ldo < (transpose ? rows : cols)) return fail(LSMX_ERR_SHAPE, "%s: bad shape", fn);
+    if (layout & ~(LSMX_E8M0_IN_T | LSMX_E8M0_OUT_KMAJOR)) return fail(LSMX_ERR_ARG, "%s: layout", fn);
+    const bool tin = layout & LSMX_E8M0_IN_T, km = layout & LSMX_E8M0_OUT_KMAJOR;
+    const int64_t orows = tin ? cols : rows, blocks = tin ? rows : cols;
+    if (rows < 0 || cols < 0 || lds < cols || ldo < (km ? orows : blocks)) return fail(LSMX_ERR_SHAPE, "%s: bad shape", fn);
+    if (km && blocks % 4) return fail(LSMX_ERR_SHAPE, "%s: K-major output needs a multiple of 4 blocks", fn);
     if (!aligned(s, 4)) return fail(LSMX_ERR_ALIGN, "%s: misaligned", fn);
     if (rows > 0 && cols > ((int64_t)1 << 38) / rows) return fail(LSMX_ERR_SHAPE, "%s: too large", fn);
     if (int r = device_guard()) return r;
     if (rows == 0 || cols == 0) return LSMX_OK;
-    return launched(lsmx::launch_scale_to_e8m0(s, rows, cols, lds, transpose, out, ldo, (hipStream_t)stream), fn);
+    return launched(lsmx::launch_scale_to_e8m0(s, rows, cols, lds, layout, out, ldo, (hipStream_t)stream), fn);
 }
 
 static int w4_common(const char *fn, const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,

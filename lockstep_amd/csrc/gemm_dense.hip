@@ -275,23 +275,27 @@ __global__ __launch_bounds__(256) void transpose_kernel(const T *__restrict__ x,
     }
 }
 
-// E8M0 bytes of fp32 power-of-two scales (their exponent field), optionally
-// transposed: out[r, c] = e8m0(s[r, c]) or out[c, r] = e8m0(s[r, c]).  The
-// quantizer's scales 2^e, e in [-127, 127], convert exactly (2^-127 is the
-// subnormal 0x00400000 -> 0).  A scale that is not a positive power of two in
-// that range has no E8M0 form: it becomes 0xFF, E8M0's NaN, so every output
-// that depends on it is NaN rather than silently wrong.
+// E8M0 bytes of fp32 power-of-two scales (their exponent field).  Element
+// (r, c) of s is the scale of (output row r, block c), or of (block r, output
+// row c) with LSMX_E8M0_IN_T; the output is row-major [out rows, ldo] or,
+// with LSMX_E8M0_OUT_KMAJOR, K-major [blocks/4, ldo, 4].  The quantizer's
+// scales 2^e, e in [-127, 127], convert exactly (2^-127 is the subnormal
+// 0x00400000 -> 0).  A scale that is not a positive power of two in that
+// range has no E8M0 form: it becomes 0xFF, E8M0's NaN, so every output that
+// depends on it is NaN rather than silently wrong.
 __global__ void scale_to_e8m0_kernel(const float *__restrict__ s, int64_t rows, int64_t cols, int64_t lds,
-                                     int transpose, uint8_t *__restrict__ out, int64_t ldo) {
+                                     int layout, uint8_t *__restrict__ out, int64_t ldo) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows * cols) return;
-    const int64_t r = transpose ? i % rows : i / cols, c = transpose ? i / rows : i % cols;
+    const int64_t r = i / cols, c = i - r * cols;
     const uint32_t b = f2u(s[r * lds + c]);
     const uint32_t ex = b >> 23;  // sign is bit 8: negative scales fail both tests
     const bool pow2 = ((b & 0x7FFFFFu) == 0 && ex >= 1 && ex <= 254) || b == 0x00400000u;
     const uint8_t e = pow2 ? (uint8_t)ex : (uint8_t)0xFF;
-    if (transpose) out[c * ldo + r] = e;
-    else out[r * ldo + c] = e;
+    const bool tin = layout & LSMX_E8M0_IN_T;
+    const int64_t orow = tin ? c : r, blk = tin ? r : c;
+    if (layout & LSMX_E8M0_OUT_KMAJOR) out[((blk >> 2) * ldo + orow) * 4 + (blk & 3)] = e;
+    else out[orow * ldo + blk] = e;
 }
 
 template <int DT, int MODE, bool SHB, bool SCALED, int CT, bool ATOMIC>
@@ -347,11 +351,11 @@ hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t
     return hipGetLastError();
 }
 
-hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int layout, uint8_t *out,
                                 int64_t ldo, hipStream_t s) {
     const int64_t n = rows * cols;
     hipLaunchKernelGGL(scale_to_e8m0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sc, rows, cols, lds,
-                       transpose, out, ldo);
+                       layout, out, ldo);
     return hipGetLastError();
 }
 

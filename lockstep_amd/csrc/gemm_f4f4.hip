@@ -47,6 +47,7 @@
 // slots in lane order, so the swizzle is applied by choosing each lane's
 // source address.
 #include "lsmx_dma.h"
+#include "lsmx_store.h"
 #include "lsmx_internal.h"
 #include "lsmx_sched.h"
 
@@ -73,67 +74,6 @@ template <int CPR>
 LSMX_DEV int f4_swz(int row) {
     if constexpr (CPR == 4) return ((row >> 1) ^ (row >> 3)) & 3;
     else return (row >> 1) & 7;
-}
-
-// fp32 -> bf16 with round-to-nearest-even (the reference's `acc.to(bf16)`):
-// one v_cvt_pk_bf16_f32 per pair of values on gfx950.
-typedef __bf16 v2bf16 __attribute__((ext_vector_type(2)));
-LSMX_DEV uint32_t bf16x2(float lo, float hi) { return __builtin_bit_cast(uint32_t, v2bf16{(__bf16)lo, (__bf16)hi}); }
-LSMX_DEV uint32_t bf16_rne(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f); }
-
-LSMX_DEV uint32_t f16_bits(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f); }
-
-template <int CT>
-LSMX_DEV void store_c(void *c, int64_t idx, float v) {
-    if constexpr (CT == LSMX_F32) reinterpret_cast<float *>(c)[idx] = v;
-    else if constexpr (CT == LSMX_BF16) reinterpret_cast<uint16_t *>(c)[idx] = (uint16_t)bf16_rne(v);
-    else reinterpret_cast<uint16_t *>(c)[idx] = (uint16_t)f16_bits(v);
-}
-
-// 4 consecutive columns of one row from one lane.
-template <int CT>
-LSMX_DEV void store_c4(void *c, int64_t idx, float v0, float v1, float v2, float v3) {
-    if constexpr (CT == LSMX_F32) {
-        *reinterpret_cast<u32x4 *>(reinterpret_cast<float *>(c) + idx) = u32x4{f2u(v0), f2u(v1), f2u(v2), f2u(v3)};
-    } else if constexpr (CT == LSMX_BF16) {
-        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(c) + idx) =
-            u32x2{bf16x2(v0, v1), bf16x2(v2, v3)};
-    } else {
-        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(c) + idx) =
-            u32x2{f16_bits(v0) | (f16_bits(v1) << 16), f16_bits(v2) | (f16_bits(v3) << 16)};
-    }
-}
-
-// Value held by the lane `D` away inside each quad (D = 1: 1,0,3,2; D = 2: 2,3,0,1).
-template <int D>
-LSMX_DEV float quad_xor(float v) {
-    constexpr int ctrl = D == 1 ? 0xB1 : 0x4E;
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
-}
-
-// 4x4 transpose inside each quad of lanes: on entry lane q holds x[r] =
-// M[r][q] (rows r of column q); on exit x[c] = M[q][c] (columns c of row q).
-// Two butterfly stages: at distance d, x[k] with bit d of k different from
-// bit d of q is replaced by the partner lane's x[k ^ d].
-LSMX_DEV void quad_transpose(float (&x)[4], int q) {
-    float y[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float o = quad_xor<1>(x[k ^ 1]);
-        y[k] = ((k ^ q) & 1) ? o : x[k];
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float o = quad_xor<2>(y[k ^ 2]);
-        x[k] = ((k ^ q) & 2) ? o : y[k];
-    }
-}
-
-template <int N>
-LSMX_DEV void wait_vm_barrier() {
-    // all of this thread's loads except the newest N have landed, then sync
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // Scale formats (SFMT = LSMX_SCALE_*): F32 scales arrive as fp32 powers of two

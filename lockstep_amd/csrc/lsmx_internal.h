@@ -76,9 +76,10 @@ hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_dense(const DenseArgs &g, int dtype, int mode, hipStream_t s);
 hipError_t launch_gemm_f8f8_scaled(const DenseArgs &g, hipStream_t s);
+hipError_t launch_gemm_f8f8_kmajor(const DenseArgs &g, hipStream_t s);
 hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, int64_t ldx, void *y,
                             int64_t ldy, hipStream_t s);
-hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int transpose, uint8_t *out,
+hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int layout, uint8_t *out,
                                 int64_t ldo, hipStream_t s);
 
 }  // namespace lsmx

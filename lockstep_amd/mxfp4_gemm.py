@@ -126,6 +126,25 @@ def _e8m0_rows(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torch.
     return out
 
 
+def _e8m0_kmajor(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torch.Tensor:
+    """fp32 block scales [rows, nkb] (or [nkb, rows] when transposed) as K-major
+    E8M0 bytes [nkb//4, rows, 4] (lsmx_scale_to_e8m0), the layout the E4M3
+    GEMM streams fastest; non-powers of two become E8M0 NaN as above."""
+    shape = (nkb, rows) if transposed else (rows, nkb)
+    assert tuple(s.shape) == shape
+    out = torch.empty((nkb // 4, rows, 4), device=s.device, dtype=torch.uint8)
+    if rows == 0 or nkb == 0:
+        return out
+    if s.dtype != torch.float32:
+        s = s.float()
+    if s.stride(-1) != 1:
+        s = s.contiguous()
+    layout = C.E8M0_OUT_KMAJOR | (C.E8M0_IN_T if transposed else 0)
+    C.call("lsmx_scale_to_e8m0", s.data_ptr(), shape[0], shape[1], s.stride(0) if shape[0] > 1 else shape[1],
+           layout, out.data_ptr(), rows, C.stream_of(out))
+    return out
+
+
 def kmajor_operand(b: torch.Tensor) -> torch.Tensor:
     """B [K, N] -> the K-contiguous [N, K] operand the kernels read: B.T itself
     when it already is K-contiguous with 16-byte aligned rows, else a
@@ -171,9 +190,18 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
         return c.zero_()
     a = _rows16(a_fp8.view(torch.uint8))
     bt = kmajor_operand(b_fp8.view(torch.uint8))
-    sa = _e8m0_rows(a_scale, M, K // 32, transposed=False)
-    sb = _e8m0_rows(b_scale, N, K // 32, transposed=True)
-    C.call("lsmx_gemm_f8f8", a.data_ptr(), a.stride(0) if M > 1 else K, sa.data_ptr(), K // 32,
-           bt.data_ptr(), bt.stride(0) if N > 1 else K, sb.data_ptr(), K // 32, c.data_ptr(),
+    if a_scale.dtype == torch.uint8 or b_scale.dtype == torch.uint8:
+        # E8M0 bytes given: row-major scales (the 128 x 128-tile kernel)
+        sa = _e8m0_rows(a_scale, M, K // 32, transposed=False)
+        sb = _e8m0_rows(b_scale, N, K // 32, transposed=True)
+        fmt, lsa, lsb = C.SCALE_E8M0, K // 32, K // 32
+    else:
+        # fp32 scales (the reference's form): K-major E8M0, the persistent
+        # 256 x 256-tile kernel (lockstep_amd/csrc/gemm_f8f8.hip)
+        sa = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
+        sb = _e8m0_kmajor(b_scale, N, K // 32, transposed=True)
+        fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
+    C.call("lsmx_gemm_f8f8", a.data_ptr(), a.stride(0) if M > 1 else K, sa.data_ptr(), lsa,
+           bt.data_ptr(), bt.stride(0) if N > 1 else K, sb.data_ptr(), lsb, fmt, c.data_ptr(),
            _out_code(out_dtype), N, M, N, K, C.stream_of(c))
     return c

@@ -157,13 +157,20 @@ def test_dense_entry_points_validate_before_launch():
     rc = _rc("lsmx_gemm_dense", ctypes.c_void_p(0x1008), None, 64, FAKE, None, 64, bf, 0, FAKE, None, 8, 8, 8,
              64, 1, None)
     assert rc == C.ERR_ALIGN
-    rc = _rc("lsmx_gemm_f8f8", FAKE, 64, FAKE, 2, FAKE, 64, FAKE, 2, FAKE, C.BF16, 8, 8, 8, 64, None)
+    rc = _rc("lsmx_gemm_f8f8", FAKE, 64, FAKE, 2, FAKE, 64, FAKE, 2, C.SCALE_E8M0, FAKE, C.BF16, 8, 8, 8, 64, None)
     assert rc == C.ERR_SHAPE and "K must be a multiple of 128" in C.last_error()     # mxfp4_gemm.py:78
-    assert _rc("lsmx_gemm_f8f8", FAKE, 128, FAKE, 4, FAKE, 128, FAKE, 4, FAKE, 7, 8, 8, 8, 128,
+    assert _rc("lsmx_gemm_f8f8", FAKE, 128, FAKE, 4, FAKE, 128, FAKE, 4, C.SCALE_E8M0, FAKE, 7, 8, 8, 8, 128,
                None) == C.ERR_DTYPE
+    assert _rc("lsmx_gemm_f8f8", FAKE, 128, FAKE, 4, FAKE, 128, FAKE, 4, C.SCALE_F32, FAKE, C.BF16, 8, 8, 8, 128,
+               None) == C.ERR_DTYPE
+    # K-major scales need ld >= rows
+    assert _rc("lsmx_gemm_f8f8", FAKE, 128, FAKE, 4, FAKE, 128, FAKE, 8, C.SCALE_E8M0_KMAJOR, FAKE, C.BF16, 8, 8,
+               8, 128, None) == C.ERR_SHAPE
     assert _rc("lsmx_transpose", FAKE, 3, 4, 4, 4, FAKE, 4, None) == C.ERR_DTYPE
     assert _rc("lsmx_transpose", FAKE, 2, 4, 8, 4, FAKE, 4, None) == C.ERR_SHAPE
     assert _rc("lsmx_scale_to_e8m0", None, 4, 4, 4, 0, FAKE, 4, None) == C.ERR_ARG
+    assert _rc("lsmx_scale_to_e8m0", FAKE, 4, 6, 6, C.E8M0_OUT_KMAJOR, FAKE, 4, None) == C.ERR_SHAPE   # 6 blocks
+    assert _rc("lsmx_scale_to_e8m0", FAKE, 4, 8, 8, 4, FAKE, 8, None) == C.ERR_ARG
 
 
 def test_dense_python_api_asserts_then_refuses_cpu():

@@ -269,3 +269,28 @@ def test_fp8_non_power_of_two_scale_poisons_its_outputs(dev, mods):
     keep = torch.ones(M, dtype=torch.bool)
     keep[5] = False
     assert torch.equal(bad[keep], clean[keep])
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 768, 1024), (300, 200, 384), (1, 256, 128), (2048, 2048, 2048)])
+def test_fp8_kmajor_kernel_matches_rowmajor_kernel(dev, mods, M, N, K):
+    """The persistent 256 x 256 E4M3 kernel (K-major scales) and the 128 x 128
+    one (row-major scales) accumulate the same 64-deep K-steps in the same
+    order: identical bits, on random E4M3 bytes (finite) and scales 2^[-4,4]."""
+    C = mods[3]
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    def e4m3(rows):
+        x = torch.randint(0, 256, (rows, K), dtype=torch.uint8, device=dev, generator=g)
+        return torch.where((x & 0x7F) == 0x7F, x ^ 1, x)          # no NaN encodings
+    a, bt = e4m3(M), e4m3(N)
+    ea = torch.randint(123, 132, (M, K // 32), dtype=torch.uint8, device=dev, generator=g)
+    eb = torch.randint(123, 132, (N, K // 32), dtype=torch.uint8, device=dev, generator=g)
+    eak = ea.reshape(M, K // 128, 4).transpose(0, 1).contiguous()
+    ebk = eb.reshape(N, K // 128, 4).transpose(0, 1).contiguous()
+    out = []
+    for fmt, sa, sb, la, lb in ((C.SCALE_E8M0, ea, eb, K // 32, K // 32), (C.SCALE_E8M0_KMAJOR, eak, ebk, M, N)):
+        c = torch.full((M, N), float("nan"), device=dev)
+        C.call("lsmx_gemm_f8f8", a.data_ptr(), K, sa.data_ptr(), la, bt.data_ptr(), K, sb.data_ptr(), lb, fmt,
+               c.data_ptr(), C.F32, N, M, N, K, C.stream_of(c))
+        out.append(c)
+    assert not out[1].isnan().any()
+    assert torch.equal(out[0], out[1])
