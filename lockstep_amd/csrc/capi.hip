@@ -287,7 +287,7 @@ int lsmx_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, in
     if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) return fail(LSMX_ERR_DTYPE, "%s: elem_bytes", fn);
     if (rows < 0 || cols < 0 || ldx < cols || ldy < rows) return fail(LSMX_ERR_SHAPE, "%s: bad shape", fn);
     if (!aligned(x, elem_bytes) || !aligned(y, elem_bytes)) return fail(LSMX_ERR_ALIGN, "%s: misaligned", fn);
-    if (rows > (int64_t)65535 * 32 || cols > (int64_t)0x7FFFFFFF * 32) return fail(LSMX_ERR_SHAPE, "%s: too large", fn);
+    if (rows > (int64_t)65535 * 64 || cols > (int64_t)0x7FFFFFFF * 64) return fail(LSMX_ERR_SHAPE, "%s: too large", fn);
     if (int r = device_guard()) return r;
     if (rows == 0 || cols == 0) return LSMX_OK;
     return launched(lsmx::launch_transpose(x, elem_bytes, rows, cols, ldx, y, ldy, (hipStream_t)stream), fn);

@@ -255,23 +255,43 @@ __global__ __launch_bounds__(dn::NT, (dense_lds_bytes<DT, MODE, SHB>() <= 80 * 1
     }
 }
 
-// y[cols, ldy] = x[rows, ldx]^T for elements of ES bytes, through a 32 x 32 LDS tile.
+// y[cols, ldy] = x[rows, ldx]^T through a 64 x 64 LDS tile.  Full tiles of
+// 16-byte aligned rows move 16 bytes per load and per store (a thread gathers
+// 16/sizeof(T) elements of a column from LDS into one store); edge tiles and
+// unaligned operands go element by element.
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_kernel(const T *__restrict__ x, int64_t rows, int64_t cols,
-                                                        int64_t ldx, T *__restrict__ y, int64_t ldy) {
-    __shared__ T tile[32][33];
-    const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+                                                        int64_t ldx, T *__restrict__ y, int64_t ldy, int vec) {
+    constexpr int V = 16 / (int)sizeof(T);   // elements per 16 bytes
+    constexpr int CPR = 64 / V;              // 16-byte chunks per tile row
+    constexpr int P = 64 + V;                // padded LDS row (keeps 16-byte alignment)
+    __shared__ __attribute__((aligned(16))) T tile[64][P];
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const int t = threadIdx.x;
+    const bool full = vec && r0 + 64 <= rows && c0 + 64 <= cols;
+    for (int q = t; q < 64 * CPR; q += 256) {
+        const int r = q / CPR, cc = (q % CPR) * V;
+        if (full) {
+            *reinterpret_cast<uint4 *>(&tile[r][cc]) = *reinterpret_cast<const uint4 *>(x + (r0 + r) * ldx + c0 + cc);
+        } else {
 #pragma unroll
-    for (int k = 0; k < 32; k += 8) {
-        const int64_t r = r0 + ty + k, c = c0 + tx;
-        if (r < rows && c < cols) tile[ty + k][tx] = x[r * ldx + c];
+            for (int k = 0; k < V; ++k)
+                if (r0 + r < rows && c0 + cc + k < cols) tile[r][cc + k] = x[(r0 + r) * ldx + c0 + cc + k];
+        }
     }
     __syncthreads();
+    for (int q = t; q < 64 * CPR; q += 256) {
+        const int oc = q / CPR, rr = (q % CPR) * V;   // output row oc = input column, elements rr .. rr+V-1
+        if (full) {
+            T v[V];
 #pragma unroll
-    for (int k = 0; k < 32; k += 8) {
-        const int64_t c = c0 + ty + k, r = r0 + tx;
-        if (r < rows && c < cols) y[c * ldy + r] = tile[tx][ty + k];
+            for (int k = 0; k < V; ++k) v[k] = tile[rr + k][oc];
+            *reinterpret_cast<uint4 *>(y + (c0 + oc) * ldy + r0 + rr) = *reinterpret_cast<const uint4 *>(v);
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; ++k)
+                if (c0 + oc < cols && r0 + rr + k < rows) y[(c0 + oc) * ldy + r0 + rr + k] = tile[rr + k][oc];
+        }
     }
 }
 
@@ -338,16 +358,18 @@ hipError_t launch_gemm_f8f8_scaled(const DenseArgs &g, hipStream_t s) {
 
 hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, int64_t ldx, void *y,
                             int64_t ldy, hipStream_t s) {
-    const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)), blk(256);
+    const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64)), blk(256);
+    const int vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
+                    (ldx * elem_bytes) % 16 == 0 && (ldy * elem_bytes) % 16 == 0;
     if (elem_bytes == 1)
         hipLaunchKernelGGL(transpose_kernel<uint8_t>, grid, blk, 0, s, reinterpret_cast<const uint8_t *>(x), rows, cols,
-                           ldx, reinterpret_cast<uint8_t *>(y), ldy);
+                           ldx, reinterpret_cast<uint8_t *>(y), ldy, vec);
     else if (elem_bytes == 2)
         hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, blk, 0, s, reinterpret_cast<const uint16_t *>(x), rows,
-                           cols, ldx, reinterpret_cast<uint16_t *>(y), ldy);
+                           cols, ldx, reinterpret_cast<uint16_t *>(y), ldy, vec);
     else
         hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, blk, 0, s, reinterpret_cast<const uint32_t *>(x), rows,
-                           cols, ldx, reinterpret_cast<uint32_t *>(y), ldy);
+                           cols, ldx, reinterpret_cast<uint32_t *>(y), ldy, vec);
     return hipGetLastError();
 }
 

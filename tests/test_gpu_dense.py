@@ -177,11 +177,13 @@ def test_empty_and_zero_k(dev, mods):
 
 
 @pytest.mark.parametrize("elem", [1, 2, 4])
-@pytest.mark.parametrize("rows,cols", [(1, 1), (33, 65), (256, 96), (1000, 3)])
-def test_transpose_exact(dev, mods, elem, rows, cols):
+@pytest.mark.parametrize("rows,cols,pad", [(1, 1, 5), (33, 65, 5), (256, 96, 5), (1000, 3, 5), (128, 192, 0),
+                                           (192, 320, 0), (100, 80, 0)])
+def test_transpose_exact(dev, mods, elem, rows, cols, pad):
+    """Element-by-element (pad 5: unaligned rows) and 16-byte (pad 0) paths, full and edge tiles."""
     C = mods[3]
     dt = {1: torch.uint8, 2: torch.int16, 4: torch.int32}[elem]
-    x = torch.randint(0, 100, (rows, cols + 5), dtype=torch.int32).to(dt).to(dev)[:, :cols]
+    x = torch.randint(0, 100, (rows, cols + pad), dtype=torch.int32).to(dt).to(dev)[:, :cols]
     y = torch.full((cols, rows), -1, dtype=dt, device=dev)
     C.call("lsmx_transpose", x.data_ptr(), elem, rows, cols, x.stride(0), y.data_ptr(), rows, C.stream_of(y))
     assert torch.equal(y.cpu(), x.t().cpu())
