@@ -158,47 +158,85 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
         m0 = (int64_t)tm * BM;
         n0 = (int64_t)tn * BN;
     };
-    auto set_refill_tile = [&](int ti) { tile_of(ti, rm0, rn0); };
-    // one memory op (q = 0..L-1) of loading k-step kt of the refill tile into ring slot s
-    auto issue_op = [&](int kt, int s, int q) {
+    // Refill panels: first byte and byte count, at k-step 0 of the refill
+    // tile, of its A and B code rows and of the scale slices this wave loads,
+    // and the scale bytes one stage advances.  Wave-uniform; recomputed only
+    // when the refill target moves on to the next tile.
+    constexpr int NSD = SX4 ? 1 : LS;  // scale descriptors per stage
+    struct Panel {
+        const uint8_t *p;
+        int64_t n;
+    };
+    Panel pA, pB, pS[NSD];
+    int64_t sstep[NSD];
+#pragma unroll
+    for (int r = 0; r < NSD; ++r) {
+        const bool to_b = SX4 ? ((wave >> 1) & 1) : NW == 4 ? (r & 1) : s_is_b;
+        const int64_t sld = to_b ? g.ld_sb : g.ld_sa;
+        sstep[r] = SKM ? NSL * sld * 4 : SF32 ? NSL * 16 : NSL * 4;
+    }
+    auto set_refill_origin = [&](int64_t m0, int64_t n0) {
+        rm0 = m0;
+        rn0 = n0;
+        pA = Panel{g.a + rm0 * g.lda, min(g.M - rm0, (int64_t)BM) * g.lda};
+        pB = Panel{g.b + rn0 * g.ldb, min(g.N - rn0, (int64_t)BN) * g.ldb};
+#pragma unroll
+        for (int r = 0; r < NSD; ++r) {
+            // SX4: operand (wave >> 1) & 1, slice wave & 1
+            const bool to_b = SX4 ? ((wave >> 1) & 1) : NW == 4 ? (r & 1) : s_is_b;
+            const int j = SX4 ? (wave & 1) : NW == 4 ? (r >> 1) : r;  // scale slice within the stage
+            const int64_t r0 = to_b ? rn0 : rm0, sld = to_b ? g.ld_sb : g.ld_sa;
+            // scalar part of this slice's address; the lane adds its row
+            // offset.  Rows past the operand read other scales or zeros:
+            // their products only reach outputs that are not stored.
+            const int64_t sb0 = SKM ? (j * sld + r0) * 4 : SF32 ? r0 * sld * 4 + j * 16 : r0 * sld + j * 4;
+            pS[r] = Panel{reinterpret_cast<const uint8_t *>(to_b ? g.sb : g.sa) + sb0,
+                          (int64_t)(to_b ? sbytes_b : sbytes_a) - sb0};
+        }
+    };
+    auto set_refill_tile = [&](int ti) {
+        int64_t m0, n0;
+        tile_of(ti, m0, n0);
+        set_refill_origin(m0, n0);
+    };
+    // buffer descriptors of k-step kt of the refill tile
+    v4i_rsrc rsA, rsB, rsS[NSD];
+    auto make_desc_a = [&](int kt) {
         const int64_t ko = (int64_t)kt * BKB;
+        rsA = buf_rsrc(pA.p + ko, (uint64_t)(pA.n - ko));
+    };
+    auto make_desc_b = [&](int kt) {
+        const int64_t ko = (int64_t)kt * BKB;
+        rsB = buf_rsrc(pB.p + ko, (uint64_t)(pB.n - ko));
+    };
+    auto make_desc_s = [&](int kt) {
+#pragma unroll
+        for (int r = 0; r < NSD; ++r) {
+            const int64_t so = (int64_t)kt * sstep[r];
+            rsS[r] = buf_rsrc(pS[r].p + so, (uint64_t)(pS[r].n - so));
+        }
+    };
+    // one memory op (q = 0..L-1) of loading the refill stage into ring slot s
+    auto issue_op = [&](int s, int q) {
         if (q < 2 * XA) {
             const int i = q >> 1;
             const uint32_t m0 = lds_u32((q & 1) ? &sB[0][0] : &sA[0][0]) + s * TILE_B + (i * NW + wave) * 1024;
-            if ((q & 1) == 0) {
-                const int64_t rows = min(g.M - rm0, (int64_t)BM);
-                dma_x4(offA0 + i * stepA, buf_rsrc(g.a + rm0 * g.lda + ko, (uint64_t)(rows * g.lda - ko)), m0);
-            } else {
-                const int64_t rows = min(g.N - rn0, (int64_t)BN);
-                dma_x4(offB0 + i * stepB, buf_rsrc(g.b + rn0 * g.ldb + ko, (uint64_t)(rows * g.ldb - ko)), m0);
-            }
+            if ((q & 1) == 0) dma_x4(offA0 + i * stepA, rsA, m0);
+            else dma_x4(offB0 + i * stepB, rsB, m0);
             return;
         }
         if constexpr (SX4) {
-            // q == 2*XA: operand (wave >> 1) & 1, slice wave & 1
             const bool xb = (wave >> 1) & 1;
             const int j = wave & 1;
-            const int64_t sld = xb ? g.ld_sb : g.ld_sa;
-            const int64_t sb0 = (((int64_t)kt * NSL + j) * sld + (xb ? rn0 : rm0)) * 4;
-            const v4i_rsrc rs = buf_rsrc(reinterpret_cast<const uint8_t *>(xb ? g.sb : g.sa) + sb0,
-                                         (xb ? sbytes_b : sbytes_a) - (uint64_t)sb0);
-            dma_x4((uint32_t)lane * 16, rs, lds_u32(xb ? &sSB[s][j][0] : &sSA[s][j][0]));
+            dma_x4((uint32_t)lane * 16, rsS[0], lds_u32(xb ? &sSB[s][j][0] : &sSA[s][j][0]));
             return;
         }
         const int r = q - 2 * XA;
         const bool to_b = NW == 4 ? (r & 1) : s_is_b;
-        const int j = NW == 4 ? (r >> 1) : r;  // scale slice within the stage
-        const int64_t slice = (int64_t)kt * NSL + j;
-        const uint8_t *src = reinterpret_cast<const uint8_t *>(to_b ? g.sb : g.sa);
-        const int64_t r0 = to_b ? rn0 : rm0, sld = to_b ? g.ld_sb : g.ld_sa;
-        // scalar part of this slice's address; the lane adds its row offset.
-        // Rows past the operand read other scales or zeros: their products
-        // only reach outputs that are not stored.
-        const int64_t sb0 = SKM ? (slice * sld + r0) * 4 : SF32 ? r0 * sld * 4 + slice * 16 : r0 * sld + slice * 4;
-        const v4i_rsrc rs = buf_rsrc(src + sb0, (to_b ? sbytes_b : sbytes_a) - (uint64_t)sb0);
+        const int j = NW == 4 ? (r >> 1) : r;
         const uint32_t m0 = lds_u32(to_b ? &sSB[s][j][(wave & 3) * 64 * SSL] : &sSA[s][j][(wave & 3) * 64 * SSL]);
-        if constexpr (SF32) dma_x4(to_b ? offSB : offSA, rs, m0);
-        else dma_x1(to_b ? offSB : offSA, rs, m0);
+        if constexpr (SF32) dma_x4(to_b ? offSB : offSA, rsS[SX4 ? 0 : r], m0);
+        else dma_x1(to_b ? offSB : offSA, rsS[SX4 ? 0 : r], m0);
     };
 
     // K positions: at K-step st, lane half h supplies 16-byte chunk
@@ -249,8 +287,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                 set_refill_tile(ti);
                 cur = ti;
             }
+            make_desc_a(p % nk);
+            make_desc_b(p % nk);
+            make_desc_s(p % nk);
 #pragma unroll
-            for (int q = 0; q < L; ++q) issue_op(p % nk, p, q);
+            for (int q = 0; q < L; ++q) issue_op(p, q);
         }
     }
     wait_vm_barrier<(S - 1) * L>();
@@ -260,12 +301,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     for (int q = 0; q < NRD; ++q) read_frag(0, 0, q, fa[0], fb[0]);
 
     const bool vec_c = ((reinterpret_cast<uintptr_t>(g.c) & 15) == 0) && (g.ldc % 4 == 0);
-    // Stage u + S refills slot u % S.  Stages past the last one re-load the
+    // Stage u + S refills slot u % S.  Stage kt of tile iteration ti
+    // refills k-step kt + ra of tile ti + qa while kt + ra < nk (phase A)
+    // and k-step kt + ra - nk of tile ti + qa + 1 after (phase B), with
+    // qa = S / nk and ra = S % nk; the refill panels are set once per phase,
+    // outside the stage loops.  Stages past the last one re-load the
     // workgroup's last tile (tile_of clamps), so the loads stay inside the
     // operands and land in slots that are never read again.
-    const DivU32 div_nk = make_div((uint32_t)nk);
+    const int qa = S / nk, ra = S % nk;
     int u = 0;
     for (int ti = 0; ti < my_tiles; ++ti) {
+        int64_t mb0, nb0;  // origin of the phase B refill tile
+        tile_of(ti + qa + 1, mb0, nb0);
+        set_refill_tile(ti + qa);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -273,13 +321,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-        for (int kt = 0; kt < nk; ++kt, ++u) {
+        // one pipeline stage (stage u, ring slot u % S) whose refill loads
+        // k-step rk of the current refill tile
+        auto run_stage = [&](const int rk) {
             const int s = u % S;
             const int sn = (u + 1) % S;
-            // refill target: tile iteration and k-step of stage u + S
-            const int rt = (int)udiv((uint32_t)(u + S), div_nk);
-            const int rk = u + S - rt * nk;
-            set_refill_tile(rt);
+            // Descriptors of the refill stage.  With KS = 4 part c is built
+            // after the stage's MFMA c, so that its scalar arithmetic overlaps
+            // the matrix core instead of delaying the stage's first MFMA on
+            // both waves of a SIMD.  The empty asm passes rk through an SGPR
+            // so that the IR optimizer cannot hoist a part above the
+            // scheduling fence in front of it.
+            constexpr int NPART = 3;
+            auto refill_desc_part = [&](int c) {
+                int k = rk;
+                asm volatile("" : "+s"(k));
+                if (c == 0) make_desc_a(k);
+                else if (c == 1) make_desc_b(k);
+                else make_desc_s(k);
+            };
+            if constexpr (KS != 4)
+                for (int c = 0; c < NPART; ++c) refill_desc_part(c);
             if constexpr (KS == 4) {
                 // K-step 0 reads step 1's fragments, step 1 reads steps 2 and
                 // 3's, so slot s is fully read before step 2.  The barrier
@@ -309,6 +371,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                         acc[i][j] = mfma_scale_f4(fa[BUF[st]][i], fb[BUF[st]][j], acc[i][j], 4, 4, st, (int)scA[i], st,
                                                   (int)scB[j]);
                         if (st == 0) {
+                            if (idx < NPART) {
+                                __builtin_amdgcn_sched_barrier(0);
+                                refill_desc_part(idx);
+                            }
                             if (idx < NRD) read_frag(s, 1, idx, fa[1], fb[1]);
                         } else if (st == 1) {
 #pragma unroll
@@ -319,12 +385,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                         } else if (st == 2) {
 #pragma unroll
                             for (int o = idx * OPH; o < (idx + 1) * OPH; ++o)
-                                if (o < LH) issue_op(rk, s, o);
+                                if (o < LH) issue_op(s, o);
                             if (idx < NRD) read_scale(sn, idx, nA, nB);
                         } else {
 #pragma unroll
                             for (int o = LH + idx * OPH; o < LH + (idx + 1) * OPH; ++o)
-                                if (o < L) issue_op(rk, s, o);
+                                if (o < L) issue_op(s, o);
                             if (idx < NRD) read_frag(sn, 0, idx, fa[1], fb[1]);
                         }
                         // Pin this slot's LDS reads here: the MFMA is a pure
@@ -365,7 +431,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                             // K-step-0 fragments
     #pragma unroll
                             for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
-                                if (o < L) issue_op(rk, s, o);
+                                if (o < L) issue_op(s, o);
     #pragma unroll
                             for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
                                 if (r < NRD) read_scale(sn, r, nA, nB);
@@ -385,7 +451,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             for (int i = 0; i < TM; ++i) scA[i] = nA[i];
 #pragma unroll
             for (int j = 0; j < TN; ++j) scB[j] = nB[j];
-        }
+        };
+        for (int kt = 0; kt < nk - ra; ++kt, ++u) run_stage(kt + ra);
+        set_refill_origin(mb0, nb0);
+        for (int kt = nk - ra; kt < nk; ++kt, ++u) run_stage(kt + ra - nk);
 
         // ---- epilogue of tile ti.  acc element e of tile (i, j) sits at
         //      row = i*32 + 8*(e/4) + 4*half + e%4,  col = j*32 + frow;
