@@ -271,6 +271,8 @@ int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t
     if (!aligned(c, c_dtype == LSMX_F32 ? 4 : 2)) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
     if (km && (lda > 0x7FFFFFFF / 256 || ldb > 0x7FFFFFFF / 256))
         return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
+    if (km && (M > 0x7FFFFFFF || N > 0x7FFFFFFF || ld_sa > 0x7FFFFFFF || ld_sb > 0x7FFFFFFF))
+        return fail(LSMX_ERR_SHAPE, "%s: M, N and scale leading dimensions must be below 2^31", fn);
     if (int r = device_guard()) return r;
     if (M == 0 || N == 0) return LSMX_OK;
     if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);

@@ -93,27 +93,43 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
         m0 = (int64_t)tm * BM;
         n0 = (int64_t)tn * BN;
     };
-    // one memory op (q = 0..L-1) of loading stage kt of the refill tile into slot s
-    auto issue_op = [&](int kt, int s, int q) __attribute__((always_inline)) {
-        const int64_t ko = (int64_t)kt * BKB;
+    auto set_refill_tile = [&](int ti) __attribute__((always_inline)) { tile_of(ti, rm0, rn0); };
+    // buffer descriptors of k-step kt of the refill tile, in three parts.
+    // 32-bit factors (the host bounds M, N and the leading dimensions below
+    // 2^31 and a 256-row panel below 2^31 bytes), so every product is one
+    // 32 x 32 -> 64-bit multiply.
+    const uint32_t M32 = (uint32_t)g.M, N32 = (uint32_t)g.N;
+    const uint32_t lda32 = (uint32_t)g.lda, ldb32 = (uint32_t)g.ldb;
+    const uint32_t ldsa32 = (uint32_t)g.ld_sa, ldsb32 = (uint32_t)g.ld_sb;
+    v4i_rsrc rsA, rsB, rsSA, rsSB;
+    auto make_desc = [&](int part, int kt) __attribute__((always_inline)) {
+        const uint32_t ko = (uint32_t)kt * BKB;
+        if (part == 0) {
+            const uint32_t m0 = (uint32_t)rm0, rows = min(M32 - m0, (uint32_t)BM);
+            rsA = buf_rsrc(g.a0 + (uint64_t)m0 * lda32 + ko, rows * lda32 - ko);
+        } else if (part == 1) {
+            const uint32_t n0 = (uint32_t)rn0, rows = min(N32 - n0, (uint32_t)BN);
+            rsB = buf_rsrc(g.b0 + (uint64_t)n0 * ldb32 + ko, rows * ldb32 - ko);
+        } else {
+            // K-major scale slice kt: rows past the operand read later slices
+            // or zeros; their products only reach outputs that are not stored
+            const uint64_t oa = ((uint64_t)kt * ldsa32 + (uint32_t)rm0) * 4;
+            const uint64_t ob = ((uint64_t)kt * ldsb32 + (uint32_t)rn0) * 4;
+            rsSA = buf_rsrc(g.sa + oa, sbytes_a - oa);
+            rsSB = buf_rsrc(g.sb + ob, sbytes_b - ob);
+        }
+    };
+    // one memory op (q = 0..L-1) of loading the refill stage into slot s
+    auto issue_op = [&](int s, int q) __attribute__((always_inline)) {
         if (q < 2 * XA) {
             const int i = q >> 1;
             const uint32_t m0 = lds_u32((q & 1) ? &sB[0][0] : &sA[0][0]) + s * TILE_B + (i * NW + wave) * 1024;
-            if ((q & 1) == 0) {
-                const int64_t rows = min(g.M - rm0, (int64_t)BM);
-                dma_x4(offA0 + i * stepA, buf_rsrc(g.a0 + rm0 * g.lda + ko, (uint64_t)(rows * g.lda - ko)), m0);
-            } else {
-                const int64_t rows = min(g.N - rn0, (int64_t)BN);
-                dma_x4(offB0 + i * stepB, buf_rsrc(g.b0 + rn0 * g.ldb + ko, (uint64_t)(rows * g.ldb - ko)), m0);
-            }
+            if ((q & 1) == 0) dma_x4(offA0 + i * stepA, rsA, m0);
+            else dma_x4(offB0 + i * stepB, rsB, m0);
             return;
         }
-        // K-major scale slice kt: rows past the operand read later slices or
-        // zeros; their products only reach outputs that are not stored
         const bool to_b = q == 2 * XA + 1;
-        const int64_t sb0 = ((int64_t)kt * (to_b ? g.ld_sb : g.ld_sa) + (to_b ? rn0 : rm0)) * 4;
-        const v4i_rsrc rs = buf_rsrc((to_b ? g.sb : g.sa) + sb0, (to_b ? sbytes_b : sbytes_a) - (uint64_t)sb0);
-        dma_x1(offS, rs, lds_u32(to_b ? &sSB[s][wave * 256] : &sSA[s][wave * 256]));
+        dma_x1(offS, to_b ? rsSB : rsSA, lds_u32(to_b ? &sSB[s][wave * 256] : &sSA[s][wave * 256]));
     };
 
     // K-step st: lane half h supplies chunks 4st + h (block 0 part) and
@@ -147,11 +163,13 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
         for (int p = 0; p < S; ++p) {
             const int ti = stage_tile_iter(p, nk, my_tiles);
             if (ti != cur) {
-                tile_of(ti, rm0, rn0);
+                set_refill_tile(ti);
                 cur = ti;
             }
 #pragma unroll
-            for (int q = 0; q < L; ++q) issue_op(p % nk, p, q);
+            for (int c = 0; c < 3; ++c) make_desc(c, p % nk);
+#pragma unroll
+            for (int q = 0; q < L; ++q) issue_op(p, q);
         }
     }
     wait_vm_barrier<(S - 1) * L>();
@@ -161,12 +179,19 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
     for (int q = 0; q < NRD; ++q) read_frag(0, 0, q, fa[0], fb[0]);
 
     const bool vec_c = ((reinterpret_cast<uintptr_t>(g.c0) & 15) == 0) && (g.ldc % 4 == 0);
-    // Stage u + S refills slot u % S.  Stages past the last one re-load the
-    // workgroup's last tile (tile_of clamps): the loads stay inside the
-    // operands and land in slots that are never read again.
-    const DivU32 div_nk = make_div((uint32_t)nk);
+    // Stage u + S refills slot u % S.  Stage kt of tile iteration ti
+    // refills k-step kt + ra of tile ti + qa while kt + ra < nk and k-step
+    // kt + ra - nk of tile ti + qa + 1 after, with qa = S / nk and
+    // ra = S % nk; both tiles' coordinates are found once per tile, and each
+    // stage only selects between them.  Stages past the last one re-load the
+    // workgroup's last tile (tile coordinates are clamped): the loads stay
+    // inside the operands and land in slots that are never read again.
+    const int qa = S / nk, ra = S % nk;
     int u = 0;
     for (int ti = 0; ti < my_tiles; ++ti) {
+        int tma, tna, tmb, tnb;
+        tile_coords((int)blockIdx.x + imin(ti + qa, my_tiles - 1) * (int)gridDim.x, tmap, tma, tna);
+        tile_coords((int)blockIdx.x + imin(ti + qa + 1, my_tiles - 1) * (int)gridDim.x, tmap, tmb, tnb);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -177,9 +202,8 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
         for (int kt = 0; kt < nk; ++kt, ++u) {
             const int s = u % S;
             const int sn = (u + 1) % S;
-            const int rt = (int)udiv((uint32_t)(u + S), div_nk);
-            const int rk = u + S - rt * nk;
-            tile_of(rt, rm0, rn0);
+            const bool pb = kt + ra >= nk;
+            const int rk = pb ? kt + ra - nk : kt + ra;
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 if (st == 1) {
@@ -195,11 +219,26 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
                     acc[i][j] = mfma_scale_f8(fa[st][i], fb[st][j], acc[i][j], 0, 0, 2 * st, (int)scA[i], 2 * st,
                                               (int)scB[j]);
                     if (st == 0) {
+                        // descriptors of the refill stage, one part after each
+                        // of the first MFMAs so that their scalar arithmetic
+                        // overlaps the matrix core; the empty asm passes rk
+                        // through an SGPR so that the IR optimizer cannot
+                        // hoist a part above the fence in front of it
+                        if (idx < 3) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            int k = rk;
+                            asm volatile("" : "+s"(k));
+                            if (idx == 0) {
+                                rm0 = (int64_t)(pb ? tmb : tma) * BM;
+                                rn0 = (int64_t)(pb ? tnb : tna) * BN;
+                            }
+                            make_desc(idx, k);
+                        }
                         if (idx < NRD) read_frag(s, 1, idx, fa[1], fb[1]);
                     } else {
 #pragma unroll
                         for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
-                            if (o < L) issue_op(rk, s, o);
+                            if (o < L) issue_op(s, o);
                         if (idx < NRD) read_frag(sn, 0, idx, fa[0], fb[0]);
                         // the next stage's scales go straight into the registers
                         // whose last MFMA has just issued: scA[i] after MFMA
