@@ -64,6 +64,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ v16f mfma_scale_f4(v4i a, v4i b, v16f c, int cbsz, int blgp, int opsel_a, int scale_a, int opsel_b,
                               int scale_b) __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v4i32.v4i32");
 
+// a compile-time ring slot for the stage code
+template <int V>
+struct SlotC {
+    static constexpr int value = V;
+};
+
 namespace f4 {
 constexpr int BM = 256, BN = 256;
 constexpr int GROUP_M = 4;
@@ -323,9 +329,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 
         // one pipeline stage (stage u, ring slot u % S) whose refill loads
         // k-step rk of the current refill tile
-        auto run_stage = [&](const int rk) {
-            const int s = u % S;
-            const int sn = (u + 1) % S;
+        // SLOT < 0: ring slot u % S computed at run time; SLOT >= 0: the
+        // caller knows u % S == SLOT, so every LDS address of the stage is a
+        // loop-invariant register plus an immediate offset.
+        auto run_stage = [&](const int rk, auto slot_c) __attribute__((always_inline)) {
+            constexpr int SLOT = decltype(slot_c)::value;
+            const int s = SLOT >= 0 ? SLOT : u % S;
+            const int sn = SLOT >= 0 ? (SLOT + 1) % S : (u + 1) % S;
             // Descriptors of the refill stage.  With KS = 4 part c is built
             // after the stage's MFMA c, so that its scalar arithmetic overlaps
             // the matrix core instead of delaying the stage's first MFMA on
@@ -334,7 +344,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             // scheduling fence in front of it.
             constexpr int NPART = 3;
             auto refill_desc_part = [&](int c) {
-                int k = rk;
+                int k = __builtin_amdgcn_readfirstlane(rk);
                 asm volatile("" : "+s"(k));
                 if (c == 0) make_desc_a(k);
                 else if (c == 1) make_desc_b(k);
@@ -452,9 +462,32 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 #pragma unroll
             for (int j = 0; j < TN; ++j) scB[j] = nB[j];
         };
-        for (int kt = 0; kt < nk - ra; ++kt, ++u) run_stage(kt + ra);
+        // stages kt0 .. kt1-1 of this tile, refilling k-step kt + rk_off;
+        // with a 2-slot ring, pairs of stages with compile-time slots
+        auto run_range = [&](int kt0, int kt1, int rk_off) __attribute__((always_inline)) {
+            if constexpr (S == 2) {
+                int kt = kt0;
+                if (kt < kt1 && (u & 1)) {
+                    run_stage(kt + rk_off, SlotC<1>{});
+                    ++kt, ++u;
+                }
+                for (; kt + 1 < kt1; kt += 2) {
+                    run_stage(kt + rk_off, SlotC<0>{});
+                    ++u;
+                    run_stage(kt + 1 + rk_off, SlotC<1>{});
+                    ++u;
+                }
+                if (kt < kt1) {
+                    run_stage(kt + rk_off, SlotC<0>{});
+                    ++u;
+                }
+            } else {
+                for (int kt = kt0; kt < kt1; ++kt, ++u) run_stage(kt + rk_off, SlotC<-1>{});
+            }
+        };
+        run_range(0, nk - ra, ra);
         set_refill_origin(mb0, nb0);
-        for (int kt = nk - ra; kt < nk; ++kt, ++u) run_stage(kt + ra - nk);
+        run_range(nk - ra, nk, ra - nk);
 
         // ---- epilogue of tile ti.  acc element e of tile (i, j) sits at
         //      row = i*32 + 8*(e/4) + 4*half + e%4,  col = j*32 + frow;
