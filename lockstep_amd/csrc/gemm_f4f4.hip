@@ -505,15 +505,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                 for (int gq = 0; gq < 4; ++gq) {
                     float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
                                   acc[i][j][4 * gq + 3]};
-                    quad_transpose(x, q);
                     const int64_t row = m0 + wm * (TM * 32) + i * 32 + 8 * gq + 4 * half + q;
                     const int64_t col = n0 + wn * (TN * 32) + j * 32 + (frow & ~3);
                     if (full) {
-                        store_c4<CT>(g.c, row * g.ldc + col, x[0], x[1], x[2], x[3]);
-                    } else if (row < g.M) {
+                        if constexpr (CT == LSMX_F32) {
+                            quad_transpose(x, q);
+                            store_c4<CT>(g.c, row * g.ldc + col, x[0], x[1], x[2], x[3]);
+                        } else {
+                            store_c4_quad<CT>(g.c, row * g.ldc + col, x, q);
+                        }
+                    } else {
+                        // all four lanes of a quad take part in the
+                        // exchanges, so the row test comes after them
+                        quad_transpose(x, q);
+                        if (row < g.M)
 #pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            if (col + c < g.N) store_c<CT>(g.c, row * g.ldc + col + c, x[c]);
+                            for (int c = 0; c < 4; ++c)
+                                if (col + c < g.N) store_c<CT>(g.c, row * g.ldc + col + c, x[c]);
                     }
                 }
     }

@@ -67,6 +67,40 @@ LSMX_DEV void quad_transpose(float (&x)[4], int q) {
     }
 }
 
+// Value held by the lane `D` away inside each quad, for 32-bit words.
+template <int D>
+LSMX_DEV uint32_t quad_xor_u(uint32_t v) {
+    constexpr int ctrl = D == 1 ? 0xB1 : 0x4E;
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
+}
+
+// Store of a 4x4 block of 16-bit outputs held one column per lane of each
+// quad (lane q: x[r] = M[r][q]) as rows (lane q writes M[q][0..3] at idx).
+// The values are rounded first and the transpose moves packed pairs: two
+// exchanges of one word each and four byte permutes, instead of eight
+// exchanges and eight selects of fp32 values.
+//   1. words: lane q keeps rows {2qh, 2qh+1} (qh = q >> 1) of its column and
+//      takes the same rows of column q ^ 2 from lane q ^ 2;
+//   2. halves: lane q keeps row q of both columns and takes row q of columns
+//      q ^ 1 and q ^ 3 from lane q ^ 1;
+//   3. bytes: put the four columns of row q in order.
+template <int CT>
+LSMX_DEV void store_c4_quad(void *c, int64_t idx, const float (&x)[4], int q) {
+    static_assert(CT == LSMX_BF16 || CT == LSMX_F16, "16-bit outputs");
+    const uint32_t p0 = CT == LSMX_BF16 ? bf16x2(x[0], x[1]) : f16_bits(x[0]) | (f16_bits(x[1]) << 16);
+    const uint32_t p1 = CT == LSMX_BF16 ? bf16x2(x[2], x[3]) : f16_bits(x[2]) | (f16_bits(x[3]) << 16);
+    const bool qh = (q & 2) != 0, ql = (q & 1) != 0;
+    const uint32_t t0 = qh ? p1 : p0;
+    const uint32_t t1 = quad_xor_u<2>(qh ? p0 : p1);
+    // v_perm_b32: selector bytes 0-3 pick bytes of the second operand, 4-7 of the first
+    const uint32_t keep = __builtin_amdgcn_perm(t1, t0, ql ? 0x07060302u : 0x05040100u);
+    const uint32_t recv = quad_xor_u<1>(__builtin_amdgcn_perm(t1, t0, ql ? 0x05040100u : 0x07060302u));
+    // keep = (col q, col q^2), recv = (col q^1, col q^3) of row q
+    const uint32_t lo = ql ? 0x01000504u : 0x05040100u, hi = lo + 0x02020202u;
+    *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(c) + idx) =
+        u32x2{__builtin_amdgcn_perm(recv, keep, qh ? hi : lo), __builtin_amdgcn_perm(recv, keep, qh ? lo : hi)};
+}
+
 template <int N>
 LSMX_DEV void wait_vm_barrier() {
     // all of this thread's loads except the newest N have landed, then sync
