@@ -64,10 +64,14 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ v16f mfma_scale_f4(v4i a, v4i b, v16f c, int cbsz, int blgp, int opsel_a, int scale_a, int opsel_b,
                               int scale_b) __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v4i32.v4i32");
 
-// a compile-time ring slot for the stage code
+// compile-time arguments of the stage code: ring slot, loader wave or not
 template <int V>
 struct SlotC {
     static constexpr int value = V;
+};
+template <bool V>
+struct BoolC {
+    static constexpr bool value = V;
 };
 
 namespace f4 {
@@ -103,17 +107,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     constexpr int TILE_B = BM * BKB;           // bytes per operand per stage
     constexpr int NSL = KS / 2;                // 128-code scale slices per stage
     constexpr int SSL = SF32 ? 16 : 4;         // scale bytes per row per slice
-    constexpr int XA = (TILE_B / 16) / NTH;    // 16-byte DMA slots per thread per operand
+    // The ring's loads are issued by waves 0-3 only ("loader waves").  With
+    // 8 waves the other four run nothing but MFMAs and LDS reads: the two
+    // waves of a SIMD share its matrix core, the older one (0-3) wins issue
+    // arbitration and then waits at the stage barrier for the younger one,
+    // so the younger one's instruction stream sets the pace and is kept
+    // short.
+    constexpr int NLW = 4;
+    constexpr int XA = (TILE_B / 16) / (64 * NLW);  // 16-byte DMA slots per loader lane per operand
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     static_assert(KS == 2 || KS == 4, "2 or 4 K-steps per stage");
-    // scale loads: with 4 waves every wave loads 64 rows of A's and of B's
-    // scales per slice; with 8 waves waves 0-3 load A's and waves 4-7 B's.
-    // K-major E8M0 scales with KS = 4 and 8 waves: one 1 KiB slice (256 rows)
-    // per dwordx4 load; wave w takes operand (w >> 1) & 1, slice w & 1, so
-    // waves w and w + 4 write the same bytes to the same place (8 scale loads
-    // per stage instead of 16, and no branch in the stage loop).
-    constexpr bool SX4 = SKM && KS == 4 && NW == 8;
-    constexpr int LS = SX4 ? 1 : (NW == 4 ? 2 : 1) * NSL;
+    // scale loads: every loader wave loads 64 rows of A's and of B's scales
+    // per slice, except for K-major E8M0 scales with KS = 4: one 1 KiB slice
+    // (256 rows) per dwordx4 load, loader wave w takes operand (w >> 1) & 1,
+    // slice w & 1.
+    constexpr bool SX4 = SKM && KS == 4;
+    constexpr int LS = SX4 ? 1 : 2 * NSL;
     constexpr int L = 2 * XA + LS;                   // loads per thread per stage
     constexpr int NRD = TM + TN;                     // fragment (and scale) reads per K-step / stage
     constexpr int OPM = (L + NMF - 1) / NMF;         // refill ops per MFMA, last K-step
@@ -136,17 +145,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     const int frow = lane & 31, half = lane >> 5;
     const int rowA0 = wm * (TM * 32) + frow, rowB0 = wn * (TN * 32) + frow;
 
-    // ---- DMA addressing.  Data load i of this lane reads row
-    // (i*NW + wave)*RPI + lane/CPR of the refill tile; the chunk swizzle of
+    // ---- DMA addressing (loader waves).  Data load i of this lane reads row
+    // (i*NLW + wave)*RPI + lane/CPR of the refill tile; the chunk swizzle of
     // those rows does not depend on i, so the byte offset is off0 + i*step.
     // Descriptors start at the refill tile's first row and K offset and end
     // at the operand's last row: rows past it read zeros.
     const int drow0 = wave * RPI + lane / CPR;
     const uint32_t offA0 = (uint32_t)(drow0 * g.lda + ((lane % CPR) ^ f4_swz<CPR>(drow0)) * 16);
     const uint32_t offB0 = (uint32_t)(drow0 * g.ldb + ((lane % CPR) ^ f4_swz<CPR>(drow0)) * 16);
-    const uint32_t stepA = (uint32_t)(NW * RPI * g.lda), stepB = (uint32_t)(NW * RPI * g.ldb);
+    const uint32_t stepA = (uint32_t)(NLW * RPI * g.lda), stepB = (uint32_t)(NLW * RPI * g.ldb);
     const int srow = (wave & 3) * 64 + lane;
-    const bool s_is_b = NW == 8 && wave >= 4;
     // scale arrays: total bytes, and this lane's row offset inside a slice
     const uint64_t sbytes_a = SKM ? ((g.K / 128 - 1) * g.ld_sa + g.M) * 4
                                   : ((g.M - 1) * g.ld_sa + g.K / 32) * (SF32 ? 4 : 1);
@@ -177,7 +185,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     int64_t sstep[NSD];
 #pragma unroll
     for (int r = 0; r < NSD; ++r) {
-        const bool to_b = SX4 ? ((wave >> 1) & 1) : NW == 4 ? (r & 1) : s_is_b;
+        const bool to_b = SX4 ? ((wave >> 1) & 1) : (r & 1);
         const int64_t sld = to_b ? g.ld_sb : g.ld_sa;
         sstep[r] = SKM ? NSL * sld * 4 : SF32 ? NSL * 16 : NSL * 4;
     }
@@ -189,8 +197,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 #pragma unroll
         for (int r = 0; r < NSD; ++r) {
             // SX4: operand (wave >> 1) & 1, slice wave & 1
-            const bool to_b = SX4 ? ((wave >> 1) & 1) : NW == 4 ? (r & 1) : s_is_b;
-            const int j = SX4 ? (wave & 1) : NW == 4 ? (r >> 1) : r;  // scale slice within the stage
+            const bool to_b = SX4 ? ((wave >> 1) & 1) : (r & 1);
+            const int j = SX4 ? (wave & 1) : (r >> 1);  // scale slice within the stage
             const int64_t r0 = to_b ? rn0 : rm0, sld = to_b ? g.ld_sb : g.ld_sa;
             // scalar part of this slice's address; the lane adds its row
             // offset.  Rows past the operand read other scales or zeros:
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     auto issue_op = [&](int s, int q) {
         if (q < 2 * XA) {
             const int i = q >> 1;
-            const uint32_t m0 = lds_u32((q & 1) ? &sB[0][0] : &sA[0][0]) + s * TILE_B + (i * NW + wave) * 1024;
+            const uint32_t m0 = lds_u32((q & 1) ? &sB[0][0] : &sA[0][0]) + s * TILE_B + (i * NLW + wave) * 1024;
             if ((q & 1) == 0) dma_x4(offA0 + i * stepA, rsA, m0);
             else dma_x4(offB0 + i * stepB, rsB, m0);
             return;
@@ -238,8 +246,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             return;
         }
         const int r = q - 2 * XA;
-        const bool to_b = NW == 4 ? (r & 1) : s_is_b;
-        const int j = NW == 4 ? (r >> 1) : r;
+        const bool to_b = r & 1;
+        const int j = r >> 1;
         const uint32_t m0 = lds_u32(to_b ? &sSB[s][j][(wave & 3) * 64 * SSL] : &sSA[s][j][(wave & 3) * 64 * SSL]);
         if constexpr (SF32) dma_x4(to_b ? offSB : offSA, rsS[SX4 ? 0 : r], m0);
         else dma_x1(to_b ? offSB : offSA, rsS[SX4 ? 0 : r], m0);
@@ -278,13 +286,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
         else sb[q - TM] = v;
     };
 
+    // The main loop, instantiated for loader and non-loader waves.
+    auto body = [&](auto loader_c) __attribute__((always_inline)) {
+    constexpr bool LOADER = decltype(loader_c)::value;
     v16f acc[TM][TN];
     uint32_t scA[TM], scB[TN], nA[TM], nB[TN];
     // fragment buffers: KS = 4 keeps three K-steps' fragments at once (see the stage loop)
     v4i fa[KS == 4 ? 3 : 2][TM], fb[KS == 4 ? 3 : 2][TN];
 
     // ---- prologue: fill the ring, publish stage 0, read its step-0 operands
-    {
+    if constexpr (LOADER) {
         int cur = -1;
 #pragma unroll
         for (int p = 0; p < S; ++p) {
@@ -317,9 +328,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     const int qa = S / nk, ra = S % nk;
     int u = 0;
     for (int ti = 0; ti < my_tiles; ++ti) {
-        int64_t mb0, nb0;  // origin of the phase B refill tile
-        tile_of(ti + qa + 1, mb0, nb0);
-        set_refill_tile(ti + qa);
+        int64_t mb0 = 0, nb0 = 0;  // origin of the phase B refill tile
+        if constexpr (LOADER) {
+            tile_of(ti + qa + 1, mb0, nb0);
+            set_refill_tile(ti + qa);
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -350,7 +363,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                 else if (c == 1) make_desc_b(k);
                 else make_desc_s(k);
             };
-            if constexpr (KS != 4)
+            if constexpr (KS != 4 && LOADER)
                 for (int c = 0; c < NPART; ++c) refill_desc_part(c);
             if constexpr (KS == 4) {
                 // K-step 0 reads step 1's fragments, step 1 reads steps 2 and
@@ -381,7 +394,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                         acc[i][j] = mfma_scale_f4(fa[BUF[st]][i], fb[BUF[st]][j], acc[i][j], 4, 4, st, (int)scA[i], st,
                                                   (int)scB[j]);
                         if (st == 0) {
-                            if (idx < NPART) {
+                            if (LOADER && idx < NPART) {
                                 __builtin_amdgcn_sched_barrier(0);
                                 refill_desc_part(idx);
                             }
@@ -395,12 +408,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                         } else if (st == 2) {
 #pragma unroll
                             for (int o = idx * OPH; o < (idx + 1) * OPH; ++o)
-                                if (o < LH) issue_op(s, o);
+                                if (LOADER && o < LH) issue_op(s, o);
                             if (idx < NRD) read_scale(sn, idx, nA, nB);
                         } else {
 #pragma unroll
                             for (int o = LH + idx * OPH; o < LH + (idx + 1) * OPH; ++o)
-                                if (o < L) issue_op(s, o);
+                                if (LOADER && o < L) issue_op(s, o);
                             if (idx < NRD) read_frag(sn, 0, idx, fa[1], fb[1]);
                         }
                         // Pin this slot's LDS reads here: the MFMA is a pure
@@ -441,7 +454,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                             // K-step-0 fragments
     #pragma unroll
                             for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
-                                if (o < L) issue_op(s, o);
+                                if (LOADER && o < L) issue_op(s, o);
     #pragma unroll
                             for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
                                 if (r < NRD) read_scale(sn, r, nA, nB);
@@ -486,7 +499,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             }
         };
         run_range(0, nk - ra, ra);
-        set_refill_origin(mb0, nb0);
+        if constexpr (LOADER) set_refill_origin(mb0, nb0);
         run_range(nk - ra, nk, ra - nk);
 
         // ---- epilogue of tile ti.  acc element e of tile (i, j) sits at
@@ -525,6 +538,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                     }
                 }
     }
+    };
+    if (NW == NLW || wave < NLW) body(BoolC<true>{});
+    else body(BoolC<false>{});
     // no load may still be writing this workgroup's LDS when it exits
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
