@@ -74,18 +74,18 @@ LSMX_DEV uint32_t quad_xor_u(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
 }
 
-// Store of a 4x4 block of 16-bit outputs held one column per lane of each
-// quad (lane q: x[r] = M[r][q]) as rows (lane q writes M[q][0..3] at idx).
-// The values are rounded first and the transpose moves packed pairs: two
-// exchanges of one word each and four byte permutes, instead of eight
-// exchanges and eight selects of fp32 values.
+// A 4x4 block of 16-bit outputs held one column per lane of each quad
+// (lane q: x[r] = M[r][q]), rounded and transposed so that lane q holds row
+// q: the two words of M[q][0..3].  The values are rounded first and the
+// transpose moves packed pairs: two exchanges of one word each and four byte
+// permutes, instead of eight exchanges and eight selects of fp32 values.
 //   1. words: lane q keeps rows {2qh, 2qh+1} (qh = q >> 1) of its column and
 //      takes the same rows of column q ^ 2 from lane q ^ 2;
 //   2. halves: lane q keeps row q of both columns and takes row q of columns
 //      q ^ 1 and q ^ 3 from lane q ^ 1;
 //   3. bytes: put the four columns of row q in order.
 template <int CT>
-LSMX_DEV void store_c4_quad(void *c, int64_t idx, const float (&x)[4], int q) {
+LSMX_DEV u32x2 quad_pack16(const float (&x)[4], int q) {
     static_assert(CT == LSMX_BF16 || CT == LSMX_F16, "16-bit outputs");
     const uint32_t p0 = CT == LSMX_BF16 ? bf16x2(x[0], x[1]) : f16_bits(x[0]) | (f16_bits(x[1]) << 16);
     const uint32_t p1 = CT == LSMX_BF16 ? bf16x2(x[2], x[3]) : f16_bits(x[2]) | (f16_bits(x[3]) << 16);
@@ -97,8 +97,13 @@ LSMX_DEV void store_c4_quad(void *c, int64_t idx, const float (&x)[4], int q) {
     const uint32_t recv = quad_xor_u<1>(__builtin_amdgcn_perm(t1, t0, ql ? 0x05040100u : 0x07060302u));
     // keep = (col q, col q^2), recv = (col q^1, col q^3) of row q
     const uint32_t lo = ql ? 0x01000504u : 0x05040100u, hi = lo + 0x02020202u;
-    *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(c) + idx) =
-        u32x2{__builtin_amdgcn_perm(recv, keep, qh ? hi : lo), __builtin_amdgcn_perm(recv, keep, qh ? lo : hi)};
+    return u32x2{__builtin_amdgcn_perm(recv, keep, qh ? hi : lo), __builtin_amdgcn_perm(recv, keep, qh ? lo : hi)};
+}
+
+// quad_pack16's row stored at idx: lane q writes M[q][0..3].
+template <int CT>
+LSMX_DEV void store_c4_quad(void *c, int64_t idx, const float (&x)[4], int q) {
+    *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(c) + idx) = quad_pack16<CT>(x, q);
 }
 
 template <int N>
