@@ -272,12 +272,10 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
                     const int64_t row = m0 + wm * (TM * 32) + i * 32 + 8 * gq + 4 * half + q;
                     const int64_t col = n0 + wn * (TN * 32) + j * 32 + (frow & ~3);
                     if (full) {
-                        if constexpr (CT == LSMX_F32) {
-                            quad_transpose(x, q);
-                            store_c4<CT>(g.c0, row * g.ldc + col, x[0], x[1], x[2], x[3]);
-                        } else {
-                            store_c4_quad<CT>(g.c0, row * g.ldc + col, x, q);
-                        }
+                        // the fp32 transpose: the packed one (store_c4_quad)
+                        // needs more registers than this kernel has left
+                        quad_transpose(x, q);
+                        store_c4<CT>(g.c0, row * g.ldc + col, x[0], x[1], x[2], x[3]);
                     } else {
                         // all four lanes of a quad take part in the
                         // exchanges, so the row test comes after them
