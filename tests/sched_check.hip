@@ -2,8 +2,8 @@
 //
 // Replays, for many shapes and grid sizes, the stage sequence the f4 x f4 GEMM
 // kernel walks (stages of 64 or 128 bytes per row, rings of 2-4 slots) --
-// prologue refills of stages 0..S-1, then per iteration the
-// refill of stage u + S tracked by (rt, rk) -- and checks that
+// prologue refills of stages 0..S-1, then per stage the refill of stage
+// u + S in the two-phase form the kernels use -- and checks that
 //   * every tile is computed by exactly one (workgroup, iteration) pair,
 //   * every stage's tile iteration clamps into [0, my_tiles), its tile origin
 //     lies inside the operands, and its K offset stays inside a row,
@@ -66,14 +66,19 @@ static void check_shape(long M, long N, long K, int grid_cap, int S, int group_m
         }
         // prologue refills
         for (int p = 0; p < S; ++p) check_stage(lsmx::stage_tile_iter(p, nk, my_tiles), p % nk);
-        // steady-state refills of stage u + S
-        int rt = S / nk, rk = S % nk;
-        for (int u = 0; u < my_tiles * nk; ++u) {
-            check_stage(rt, rk);
-            const bool wrap = rk + 1 == nk;
-            rk = wrap ? 0 : rk + 1;
-            rt += wrap ? 1 : 0;
-        }
+        // steady-state refills, as the kernels walk them: stage kt of tile
+        // iteration ti refills k-step kt + ra of tile ti + qa (phase A,
+        // kt < nk - ra) or k-step kt + ra - nk of tile ti + qa + 1 (phase B),
+        // qa = S / nk, ra = S % nk -- which must be stage u + S, u = ti*nk + kt
+        const int qa = S / nk, ra = S % nk;
+        for (int ti = 0; ti < my_tiles; ++ti)
+            for (int kt = 0; kt < nk; ++kt) {
+                const bool pb = kt >= nk - ra;
+                const int rt = ti + qa + (pb ? 1 : 0), rk = pb ? kt + ra - nk : kt + ra;
+                const int u = ti * nk + kt;
+                CHECK(rt == (u + S) / nk && rk == (u + S) % nk, "phase refill (%d,%d) is not stage u+S\n", rt, rk);
+                check_stage(rt, rk);
+            }
     }
     for (int t = 0; t < tiles; ++t) CHECK(seen[t] == 1, "tile %d computed %d times (M=%ld N=%ld grid=%d)\n", t, seen[t], M, N, grid);
 }
