@@ -317,7 +317,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 #pragma unroll
     for (int q = 0; q < NRD; ++q) read_frag(0, 0, q, fa[0], fb[0]);
 
-    const bool vec_c = ((reinterpret_cast<uintptr_t>(g.c) & 15) == 0) && (g.ldc % 4 == 0);
+    // full-tile stores: 16-byte aligned rows, and 8 rows of C within a
+    // 32-bit byte offset of a lane's row
+    const bool vec_c = ((reinterpret_cast<uintptr_t>(g.c) & 15) == 0) && (g.ldc % 4 == 0) && g.ldc < ((int64_t)1 << 26);
     // Stage u + S refills slot u % S.  Stage kt of tile iteration ti
     // refills k-step kt + ra of tile ti + qa while kt + ra < nk (phase A)
     // and k-step kt + ra - nk of tile ti + qa + 1 after (phase B), with
@@ -509,34 +511,52 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
         int64_t m0, n0;
         tile_of(ti, m0, n0);
         const int q = frow & 3;
-        const bool full = vec_c && m0 + BM <= g.M && n0 + BN <= g.N;
+        if (vec_c && m0 + BM <= g.M && n0 + BN <= g.N) {
+            // Full tile: one branch for the whole tile, and each store's
+            // address is a wave-uniform row pointer (scalar arithmetic) plus
+            // this lane's fixed byte offset plus an immediate for column block j.
+            constexpr int EB = CT == LSMX_F32 ? 4 : 2;  // bytes per output element
+            const uint8_t *cw = reinterpret_cast<const uint8_t *>(g.c) +
+                                ((m0 + wm * (TM * 32)) * g.ldc + n0 + wn * (TN * 32)) * EB;
+            const uint32_t loff = (uint32_t)(((4 * half + q) * g.ldc + (frow & ~3)) * EB);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int gq = 0; gq < 4; ++gq) {
-                    float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
-                                  acc[i][j][4 * gq + 3]};
-                    const int64_t row = m0 + wm * (TM * 32) + i * 32 + 8 * gq + 4 * half + q;
-                    const int64_t col = n0 + wn * (TN * 32) + j * 32 + (frow & ~3);
-                    if (full) {
+                    uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 8 * gq) * g.ldc * EB;
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                      acc[i][j][4 * gq + 3]};
+                        uint8_t *p = crow + loff + j * 32 * EB;
                         if constexpr (CT == LSMX_F32) {
                             quad_transpose(x, q);
-                            store_c4<CT>(g.c, row * g.ldc + col, x[0], x[1], x[2], x[3]);
+                            *reinterpret_cast<u32x4 *>(p) = u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
                         } else {
-                            store_c4_quad<CT>(g.c, row * g.ldc + col, x, q);
+                            *reinterpret_cast<u32x2 *>(p) = quad_pack16<CT>(x, q);
                         }
-                    } else {
-                        // all four lanes of a quad take part in the
-                        // exchanges, so the row test comes after them
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int gq = 0; gq < 4; ++gq) {
+                        float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                      acc[i][j][4 * gq + 3]};
+                        // all four lanes of a quad take part in the exchanges,
+                        // so the bounds tests come after them
                         quad_transpose(x, q);
+                        const int64_t row = m0 + wm * (TM * 32) + i * 32 + 8 * gq + 4 * half + q;
+                        const int64_t col = n0 + wn * (TN * 32) + j * 32 + (frow & ~3);
                         if (row < g.M)
 #pragma unroll
                             for (int c = 0; c < 4; ++c)
                                 if (col + c < g.N) store_c<CT>(g.c, row * g.ldc + col + c, x[c]);
                     }
-                }
+        }
     }
     };
     if (NW == NLW || wave < NLW) body(BoolC<true>{});

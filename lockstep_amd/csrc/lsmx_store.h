@@ -46,7 +46,8 @@ LSMX_DEV void store_c4(void *c, int64_t idx, float v0, float v1, float v2, float
 template <int D>
 LSMX_DEV float quad_xor(float v) {
     constexpr int ctrl = D == 1 ? 0xB1 : 0x4E;
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+    // every lane of a quad is a valid source, so bound_ctrl needs no "old" value
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, true));
 }
 
 // 4x4 transpose inside each quad of lanes: on entry lane q holds x[r] =
@@ -71,7 +72,7 @@ LSMX_DEV void quad_transpose(float (&x)[4], int q) {
 template <int D>
 LSMX_DEV uint32_t quad_xor_u(uint32_t v) {
     constexpr int ctrl = D == 1 ? 0xB1 : 0x4E;
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, true);
 }
 
 // A 4x4 block of 16-bit outputs held one column per lane of each quad
