@@ -24,6 +24,7 @@
 // 128 rows of A0 followed by the same 128 rows of A1: one weight tile in LDS
 // feeds both batches and is read from memory once per stage.
 #include "lsmx_dma.h"
+#include "lsmx_store.h"
 #include "lsmx_internal.h"
 #include "lsmx_sched.h"
 
@@ -421,11 +422,42 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     const int b = NB == 2 ? (wm * 64) / RPB : 0;
     void *cb = b ? g.c1 : g.c;
     const int64_t rbase = m0 + wm * 64 - b * RPB;
+    const int64_t cbase = n0 + wn * 128;
+    if (((reinterpret_cast<uintptr_t>(cb) & 15) == 0) && g.ldc % 4 == 0 && g.ldc < ((int64_t)1 << 26) &&
+        rbase + 64 <= g.M && cbase + 128 <= g.N) {
+        // this wave's 64 x 128 block lies inside C: a 4x4 transpose inside
+        // each quad of lanes gives every lane 4 consecutive columns of one
+        // row, one 8-byte (16-bit C) or 16-byte (fp32 C) store each, at a
+        // wave-uniform row pointer plus a fixed lane offset
+        constexpr int EB = CT == LSMX_F32 ? 4 : 2;
+        const int q = frow & 3;
+        const uint8_t *cw = reinterpret_cast<const uint8_t *>(cb) + (rbase * g.ldc + cbase) * EB;
+        const uint32_t loff = (uint32_t)(((4 * half + q) * g.ldc + (frow & ~3)) * EB);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 8 * gq) * g.ldc * EB;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                  acc[i][j][4 * gq + 3]};
+                    uint8_t *p = crow + loff + j * 32 * EB;
+                    if constexpr (CT == LSMX_F32) {
+                        quad_transpose(x, q);
+                        *reinterpret_cast<u32x4 *>(p) = u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
+                    } else {
+                        *reinterpret_cast<u32x2 *>(p) = quad_pack16<CT>(x, q);
+                    }
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int64_t col = n0 + wn * 128 + j * 32 + frow;
+            const int64_t col = cbase + j * 32 + frow;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int64_t row = rbase + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
