@@ -31,15 +31,24 @@
 // would otherwise wait for every outstanding load before each LDS read.
 //
 // Per stage and wave: while the MFMAs of K-step st run, the fragments of
-// K-step st + 1 are read from LDS between them.  Before the last K-step, one
-// s_barrier (after the stage's own reads completed and the next stage's
-// loads landed) frees the slot; the last K-step's MFMAs then run with the
-// refill of that slot and the next stage's scale and K-step-0 fragment reads
-// interleaved, so the matrix core never waits on a burst of memory
-// instructions.  Refills past the last stage re-load the workgroup's last
-// tile (tile indices are clamped, lsmx_sched.h) into a slot that is never
-// read again, which keeps the loop free of branches and the outstanding-load
-// count constant.
+// K-step st + 1 are read from LDS between them.  Once the slot has been read
+// (before K-step 2 with KS = 4, the last K-step with KS = 2), one s_barrier
+// (after the stage's own reads completed and the next stage's loads landed)
+// frees it; the remaining MFMAs then run with the refill of that slot and the
+// next stage's scale and K-step-0 fragment reads interleaved, so the matrix
+// core never waits on a burst of memory instructions.  Refills past the last
+// stage re-load the workgroup's last tile (tile indices are clamped,
+// lsmx_sched.h) into a slot that is never read again, which keeps the loop
+// free of branches and the outstanding-load count constant.
+//
+// Only waves 0-3 issue the refill loads.  The two waves of a SIMD share its
+// matrix core; the older one (0-3) wins issue arbitration and reaches the
+// stage barrier first, so the younger one's instruction stream sets the pace
+// and is kept to MFMAs and LDS reads.  The refill tile changes only in the
+// last S stages of a tile, so each tile runs two stage loops ("phases") and
+// the refill panels are computed between them, not per stage; with a 2-slot
+// ring, stages run in pairs with compile-time slots, which makes every LDS
+// address a loop-invariant register plus an immediate.
 //
 // LDS layout per stage: rows of 16*CPR bytes (CPR = 2*KS chunks of 16 bytes);
 // chunk c of row r lives at r*16*CPR + 16*(c ^ swz(r)), which keeps the 16
