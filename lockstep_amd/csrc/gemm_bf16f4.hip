@@ -263,24 +263,34 @@ __global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(
 //     8g .. 8g+7 is issued first in stage 8g - 2 (scale rows must be 16-byte
 //     multiples: K % 512 == 0; fp32 scales use the VGPR-staged kernel).
 namespace wr {
-constexpr int BR = 256, BN = 256, BK = 64;
-constexpr int NW = 8, NT = 64 * NW, S = 3;
+constexpr int BK = 64;
+constexpr int NW = 8, NT = 64 * NW;
 constexpr int A_ROW_B = BK * 2, W_ROW_B = BK / 2;
-constexpr int A_SLOT = BR * A_ROW_B, W_SLOT = BN * W_ROW_B;   // 32 KiB, 8 KiB
-constexpr int XA = A_SLOT / 1024 / NW;                        // A load instructions per wave per stage (4)
-constexpr int L = XA + 1;                                     // + one W load (scales: one more every 8 stages)
 constexpr int GROUP_M = 4;
 LSMX_DEV int swz(int row) { return (row >> 1) & 7; }
 }  // namespace wr
 
-template <int NB, int CT>
+// BR x BN tile (256 x 256 for large M; 128 x 64 and 128 x 128 for M of a few
+// hundred rows, where a 256-row tile would leave most CUs idle and every CU
+// streams all of A), S-slot ring.
+template <int NB, int CT, int BR, int BN, int S>
 __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g) {
     using namespace wr;
     constexpr int RPB = BR / NB;        // A rows per batch per workgroup
-    constexpr int TM = 2, TN = 4;       // 32 x 32 tiles per wave
+    constexpr int TM = BR / 128, TN = BN / 64;   // 32 x 32 tiles per wave (4 x 2 waves)
+    constexpr int A_SLOT = BR * A_ROW_B, W_SLOT = BN * W_ROW_B;
+    constexpr int XA = A_SLOT / 1024 / NW;       // A load instructions per wave per stage
+    constexpr int L = XA + 1;                    // + one W load (scales: one more every 8 stages)
+    constexpr int WW = BN / 32;                  // waves with a W load of their own (32 rows each)
+    constexpr int SWV = BN >= 64 ? BN / 64 : 1;  // distinct scale loads (64 rows each)
+    static_assert(TM >= 1 && TN >= 1 && XA >= 1 && S >= 3, "tile");
     __shared__ __attribute__((aligned(16))) uint8_t sA[S][A_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t sW[S][W_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t sS[2][BN * 16];   // [group & 1][row][16 scale bytes]
+    // landing place of the W loads of waves past WW: they read nothing (an
+    // empty buffer descriptor: every lane out of range) and write zeros here,
+    // so that every wave counts the same loads
+    __shared__ __attribute__((aligned(16))) uint8_t sNull[WW < NW ? 1024 : 16];
 
     const int tiles_m = (int)((g.M + RPB - 1) / RPB), tiles_n = (int)((g.N + BN - 1) / BN);
     int tm, tn;
@@ -298,9 +308,12 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     // chunk (lane%8) ^ swz(row).  All 8 rows of one instruction lie in one batch.
     const int64_t lda_b = g.lda * 2;
     const int arow_l = lane >> 3;
+    // Per load: the first byte and byte count of its rows at K offset 0,
+    // loop-invariant, so that a stage's descriptors cost a 64-bit add and
+    // subtract each (the scalar unit is shared by the CU's 8 waves).
     uint32_t a_off[XA];
     const uint8_t *a_base[XA];
-    int64_t a_rows[XA];
+    uint64_t a_bytes[XA];
 #pragma unroll
     for (int i = 0; i < XA; ++i) {
         const int r0 = (i * NW + wave) * 8;            // first slot row, wave-uniform
@@ -309,36 +322,42 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         const int row = r0 + arow_l;
         a_off[i] = (uint32_t)(arow_l * lda_b + (((lane & 7) ^ swz(row)) << 4));
         a_base[i] = (b ? g.a1 : g.a) + (m0 + rb) * lda_b;
-        a_rows[i] = g.M - (m0 + rb);                    // rows left in the operand from this instruction's first row
+        // rows left in the operand from this instruction's first row, at most 8
+        const int64_t left = g.M - (m0 + rb), rows = left < 8 ? (left > 0 ? left : 0) : 8;
+        a_bytes[i] = rows > 0 ? (uint64_t)((rows - 1) * lda_b + g.K * 2) : 0;
     }
-    // W: wave w loads slot rows w*32 .. +31, lane -> row lane%32, 16-byte half lane/32
+    // W: wave w < WW loads slot rows w*32 .. +31, lane -> row lane%32,
+    // 16-byte half lane/32
+    const bool w_real = wave < WW;
     const uint32_t w_off = (uint32_t)((lane & 31) * g.ldb + (lane >> 5) * 16);
-    const uint8_t *w_base = g.b + (n0 + wave * 32) * g.ldb;
-    const int64_t w_rows = g.N - (n0 + wave * 32);
-    // scales: wave w loads 16 bytes of weight rows (w & 3)*64 + lane (waves w
-    // and w + 4 write the same bytes, so every wave counts the same loads)
+    const uint8_t *w_base = g.b + (n0 + (w_real ? wave : 0) * 32) * g.ldb;
+    const int64_t w_left = w_real ? g.N - (n0 + wave * 32) : 0, w_rows = w_left < 32 ? (w_left > 0 ? w_left : 0) : 32;
+    const uint64_t w_bytes = w_rows > 0 ? (uint64_t)((w_rows - 1) * g.ldb + g.K / 2) : 0;
+    const uint32_t w_lds = w_real ? lds_u32(&sW[0][0]) + wave * 1024 : lds_u32(&sNull[0]);
+    const uint32_t w_slot = w_real ? W_SLOT : 0;
+    // scales: wave w loads 16 bytes of weight rows (w % SWV)*64 + lane (waves
+    // w and w + SWV write the same bytes, so every wave counts the same loads)
+    const int s_w = wave % SWV;
     const int64_t s_rows = g.N - n0;
     const uint8_t *s_base = reinterpret_cast<const uint8_t *>(g.sb) + n0 * g.ld_sb;
-    const uint32_t s_off = (uint32_t)((((wave & 3) * 64) + lane) * g.ld_sb);
+    const uint32_t s_off = (uint32_t)(((s_w * 64) + lane) * g.ld_sb);
     auto issue_scales = [&](int grp) __attribute__((always_inline)) {
         const int64_t ks = (int64_t)grp * 16;
         const int64_t rows = s_rows < BN ? s_rows : BN;
         const uint64_t bytes = (uint64_t)((rows - 1) * g.ld_sb + g.K / 32 - ks);
-        dma_x4(s_off, buf_rsrc(s_base + ks, bytes), lds_u32(&sS[grp & 1][0]) + (wave & 3) * 1024);
+        dma_x4(s_off, buf_rsrc(s_base + ks, bytes), lds_u32(&sS[grp & 1][0]) + s_w * 1024);
     };
 
     auto issue = [&](int kt, int slot, int q) __attribute__((always_inline)) {
         const int64_t ko = (int64_t)kt * A_ROW_B;
         if (q < XA) {
-            const int64_t rows = a_rows[q] < 8 ? (a_rows[q] > 0 ? a_rows[q] : 0) : 8;
-            const uint64_t bytes = rows > 0 ? (uint64_t)((rows - 1) * lda_b + g.K * 2 - ko) : 0;
+            const uint64_t bytes = a_bytes[q] > 0 ? a_bytes[q] - (uint64_t)ko : 0;
             dma_x4(a_off[q], buf_rsrc(a_base[q] + ko, bytes),
                    lds_u32(&sA[0][0]) + slot * A_SLOT + (q * NW + wave) * 1024);
         } else {
             const int64_t kw = (int64_t)kt * W_ROW_B;
-            const int64_t rows = w_rows < 32 ? (w_rows > 0 ? w_rows : 0) : 32;
-            const uint64_t bytes = rows > 0 ? (uint64_t)((rows - 1) * g.ldb + g.K / 2 - kw) : 0;
-            dma_x4(w_off, buf_rsrc(w_base + kw, bytes), lds_u32(&sW[0][0]) + slot * W_SLOT + wave * 1024);
+            const uint64_t bytes = w_bytes > 0 ? w_bytes - (uint64_t)kw : 0;
+            dma_x4(w_off, buf_rsrc(w_base + kw, bytes), w_lds + slot * w_slot);
         }
     };
 
@@ -351,22 +370,25 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // prologue: scales of stages 0..7, stages 0 and 1 in flight
+    // prologue: scales of stages 0..7, stages 0 .. S-2 in flight
     issue_scales(0);
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < S - 1; ++p)
 #pragma unroll
         for (int q = 0; q < L; ++q) issue(p < nk ? p : nk - 1, p, q);
 
-    const int rowA[TM] = {wm * 64 + frow, wm * 64 + 32 + frow};
+    int rowA[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) rowA[i] = wm * (TM * 32) + i * 32 + frow;
     for (int u = 0; u < nk; ++u) {
         const int slot = u % S;
-        // this thread's loads of stage u have landed (only stage u + 1's may
-        // be outstanding); after the barrier everyone's have, and slot
-        // (u + 2) % 3 = (u - 1) % 3 is no longer read
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(L) : "memory");
-        const int kn = u + 2 < nk ? u + 2 : nk - 1;
-        const int sn = (u + 2) % S;
+        // this thread's loads of stage u have landed (only stages u + 1 ..
+        // u + S - 2 may be outstanding, and a scale load issued before the
+        // newest of them is waited for too); after the barrier everyone's
+        // have, and slot (u + S - 1) % S = (u - 1) % S is no longer read
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((S - 2) * L) : "memory");
+        const int kn = u + S - 1 < nk ? u + S - 1 : nk - 1;
+        const int sn = (u + S - 1) % S;
         // scales of the next group of 8 stages, first of this stage's loads
         // (the next stage's vmcnt wait then also covers it)
         if ((u & 7) == 6 && u + 2 < nk) issue_scales((u + 2) >> 3);
@@ -377,8 +399,8 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         uint32_t sraw[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int col = wn * 128 + j * 32 + frow;
-            wblk[j] = *reinterpret_cast<const u32x4 *>(&sW[slot][(wn * 4 + j) * 1024 + half * 512 + frow * 16]);
+            const int col = wn * (TN * 32) + j * 32 + frow;
+            wblk[j] = *reinterpret_cast<const u32x4 *>(&sW[slot][(wn * TN + j) * 1024 + half * 512 + frow * 16]);
             sraw[j] = sS[(u >> 3) & 1][col * 16 + 2 * (u & 7) + half];
         }
         v8bf fa[4][TM];
@@ -419,13 +441,13 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // epilogue: acc element e of tile (i, j) is row i*32 + 8*(e/4) + 4*half + e%4, column j*32 + frow
-    const int b = NB == 2 ? (wm * 64) / RPB : 0;
+    const int b = NB == 2 ? (wm * TM * 32) / RPB : 0;
     void *cb = b ? g.c1 : g.c;
-    const int64_t rbase = m0 + wm * 64 - b * RPB;
-    const int64_t cbase = n0 + wn * 128;
+    const int64_t rbase = m0 + wm * (TM * 32) - b * RPB;
+    const int64_t cbase = n0 + wn * (TN * 32);
     if (((reinterpret_cast<uintptr_t>(cb) & 15) == 0) && g.ldc % 4 == 0 && g.ldc < ((int64_t)1 << 26) &&
-        rbase + 64 <= g.M && cbase + 128 <= g.N) {
-        // this wave's 64 x 128 block lies inside C: a 4x4 transpose inside
+        rbase + TM * 32 <= g.M && cbase + TN * 32 <= g.N) {
+        // this wave's block lies inside C: a 4x4 transpose inside
         // each quad of lanes gives every lane 4 consecutive columns of one
         // row, one 8-byte (16-bit C) or 16-byte (fp32 C) store each, at a
         // wave-uniform row pointer plus a fixed lane offset
@@ -466,12 +488,12 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         }
 }
 
-template <int NB>
+template <int NB, int BR, int BN, int S>
 static hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
-    constexpr int RPB = wr::BR / NB;
-    const int tiles = (int)(((g.M + RPB - 1) / RPB) * ((g.N + wr::BN - 1) / wr::BN));
+    constexpr int RPB = BR / NB;
+    const int tiles = (int)(((g.M + RPB - 1) / RPB) * ((g.N + BN - 1) / BN));
     const dim3 grid(tiles), blk(wr::NT);
-#define LSMX_R(CT) hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT>), grid, blk, 0, s, g)
+#define LSMX_R(CT) hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT, BR, BN, S>), grid, blk, 0, s, g)
     if (g.c_dtype == LSMX_F32) LSMX_R(LSMX_F32);
     else if (g.c_dtype == LSMX_BF16) LSMX_R(LSMX_BF16);
     else LSMX_R(LSMX_F16);
@@ -486,7 +508,7 @@ static bool ring_ok(const GemmArgs &g) {
 }
 
 // ------------------------------------------------------------------ skinny M
-// For few activation rows (decode, M <= 64 per batch) the weight stream is the
+// For few activation rows (decode, M <= 32 per batch) the weight stream is the
 // whole cost: N*K/2 bytes of codes against 2*M*K bytes of activations.  The
 // 256-row tile above would leave most CUs idle, so this kernel spreads the
 // weight over the chip instead:
@@ -801,8 +823,10 @@ static hipError_t launch_gemv(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
+// up to 32 rows per batch (cfg3 M = 16: 20 us against 34 us for the 128-row
+// ring tile, whose MFMAs would be 7/8 padding; from M = 64 the ring is faster)
 #ifndef LSMX_SKINNY_MAX_M
-#define LSMX_SKINNY_MAX_M 64
+#define LSMX_SKINNY_MAX_M 32
 #endif
 
 static int num_cus_w() {
@@ -874,9 +898,12 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 #define LSMX_W4_RING 1
 #endif
     // the ring kernel is worth it from half a wave of 256 x 256 tiles on (cfg3 M = 1024: 224 tiles)
-    if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB>(g, s);
+    if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3>(g, s);
     if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
     if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
+    // a few hundred rows: 128 x 64 tiles through a 4-slot DMA ring (cfg3
+    // M = 128: 48 -> 38 us; M = 64: 44 -> 35 us against the skinny kernel)
+    if (LSMX_W4_RING && ring_ok(g)) return launch_ring<NB, 128, 64, 4>(g, s);
     return launch_w4<NB, 128, 64>(g, s);
 }
 
