@@ -248,6 +248,7 @@ int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0
     lsmx::DenseArgs g{reinterpret_cast<const uint8_t *>(a0), reinterpret_cast<const uint8_t *>(a1), lda,
                       reinterpret_cast<const uint8_t *>(bt0), reinterpret_cast<const uint8_t *>(bt1), ldb,
                       nullptr, nullptr, 0, 0, c0, c1, LSMX_F32, ldc, M, N, K, K / splits};
+    if (lsmx::dense_ring_ok(g, dtype)) return launched(lsmx::launch_gemm_dense_ring(g, dtype, mode, (hipStream_t)stream), fn);
     return launched(lsmx::launch_gemm_dense(g, dtype, mode, (hipStream_t)stream), fn);
 }
 

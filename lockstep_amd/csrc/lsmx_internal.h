@@ -75,6 +75,8 @@ hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
 hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_dense(const DenseArgs &g, int dtype, int mode, hipStream_t s);
+bool dense_ring_ok(const DenseArgs &g, int dtype);
+hipError_t launch_gemm_dense_ring(const DenseArgs &g, int dtype, int mode, hipStream_t s);
 hipError_t launch_gemm_f8f8_scaled(const DenseArgs &g, hipStream_t s);
 hipError_t launch_gemm_f8f8_kmajor(const DenseArgs &g, hipStream_t s);
 hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, int64_t ldx, void *y,

@@ -53,12 +53,9 @@ struct TileMap {
 LSMX_HD TileMap make_tile_map(int tiles_m, int tiles_n, int group_m) {
     return TileMap{tiles_m, tiles_n, tiles_m * tiles_n, group_m, make_div((uint32_t)(group_m * tiles_n))};
 }
-LSMX_HD void tile_coords(int pid, const TileMap &t, int &tm, int &tn) {
-    // written without branches so that it stays inside one basic block of a
-    // kernel's main loop (the scheduling fences there only act within one)
-    pid = imax(0, imin(pid, t.total - 1));
-    const int xcd = (pid & 7) * (t.total >> 3) + (pid >> 3);
-    pid = (t.total & 7) == 0 ? xcd : pid;
+// The group-of-rows part of tile_coords alone, for an id already remapped
+// per XCD (or deliberately not remapped); id in [0, total).
+LSMX_HD void group_coords(int pid, const TileMap &t, int &tm, int &tn) {
     const int group = (int)udiv((uint32_t)pid, t.per_group);
     const int first_m = group * t.group_m;
     const int gsz = imin(t.tiles_m - first_m, t.group_m);
@@ -68,6 +65,14 @@ LSMX_HD void tile_coords(int pid, const TileMap &t, int &tm, int &tn) {
     const int q = (int)udiv((uint32_t)in_group, DivU32{(uint32_t)gsz, gm});
     tm = first_m + (in_group - q * gsz);
     tn = q;
+}
+LSMX_HD void tile_coords(int pid, const TileMap &t, int &tm, int &tn) {
+    // written without branches so that it stays inside one basic block of a
+    // kernel's main loop (the scheduling fences there only act within one)
+    pid = imax(0, imin(pid, t.total - 1));
+    const int xcd = (pid & 7) * (t.total >> 3) + (pid >> 3);
+    pid = (t.total & 7) == 0 ? xcd : pid;
+    group_coords(pid, t, tm, tn);
 }
 
 // Number of tiles a persistent workgroup `wg` of `grid` processes.

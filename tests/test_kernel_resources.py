@@ -26,7 +26,7 @@ def _hipcc():
     return h
 
 
-@pytest.mark.parametrize("src", ["gemm_f4f4.hip", "gemm_bf16f4.hip", "quantize.hip", "gemm_dense.hip", "gemm_f8f8.hip"])
+@pytest.mark.parametrize("src", ["gemm_f4f4.hip", "gemm_bf16f4.hip", "quantize.hip", "gemm_dense.hip", "gemm_dense_ring.hip", "gemm_f8f8.hip"])
 def test_kernels_use_no_scratch(src, tmp_path):
     from lockstep_amd import build as B
     flags = [f for f in B.FLAGS if f not in ("-shared", "-fPIC")]
