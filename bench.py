@@ -309,7 +309,7 @@ def bench_reference_rows(torch, dev, n=4096):
         _time_events(lambda: mg.mxfp4_gemm_fp8(a_f8, b_f8, a_s, b_s)), fl1, PEAK_FP8_TFLOPS)
     row("mxfp4_gemm_fp8 (B passed as a view of K-contiguous rows)",
         _time_events(lambda: mg.mxfp4_gemm_fp8(a_f8, bt_f8.t(), a_s, bt_s.t())), fl1, PEAK_FP8_TFLOPS)
-    row("mxfp4_gemm_fp8 (E8M0 byte scales: row-major-scale kernel)",
+    row("mxfp4_gemm_fp8 (E8M0 byte scales, regrouped to K-major on the device)",
         _time_events(lambda: mg.mxfp4_gemm_fp8(a_f8, bt_f8.t(), a_e8, bt_e8.t())), fl1, PEAK_FP8_TFLOPS)
     row("mxfp4_gemm_packed (f4 x f4)", _time_events(lambda: mg.mxfp4_gemm_packed(a_pk, bt_pk, a_e8, bt_e8)),
         fl1, PEAK_FP4_TFLOPS)

@@ -114,6 +114,8 @@ def _e8m0_rows(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torch.
     if s.dtype == torch.uint8:
         if not transposed:
             return s.contiguous()
+        if s.t().is_contiguous():
+            return s.t()  # a transposed view of row-major bytes
         s = s.contiguous()
         C.call("lsmx_transpose", s.data_ptr(), 1, nkb, rows, rows, out.data_ptr(), nkb, C.stream_of(out))
         return out
@@ -127,13 +129,22 @@ def _e8m0_rows(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torch.
 
 
 def _e8m0_kmajor(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torch.Tensor:
-    """fp32 block scales [rows, nkb] (or [nkb, rows] when transposed) as K-major
-    E8M0 bytes [nkb//4, rows, 4] (lsmx_scale_to_e8m0), the layout the E4M3
-    GEMM streams fastest; non-powers of two become E8M0 NaN as above."""
+    """Block scales [rows, nkb] (or [nkb, rows] when transposed) as K-major
+    E8M0 bytes [nkb//4, rows, 4], the layout the E4M3 GEMM streams fastest.
+    fp32 scales go through lsmx_scale_to_e8m0 (non-powers of two become E8M0
+    NaN as above); E8M0 bytes are regrouped with lsmx_transpose: row-major
+    bytes [rows, nkb] are [rows, nkb/4] dwords, and their transpose
+    [nkb/4, rows] is the K-major layout."""
     shape = (nkb, rows) if transposed else (rows, nkb)
     assert tuple(s.shape) == shape
     out = torch.empty((nkb // 4, rows, 4), device=s.device, dtype=torch.uint8)
     if rows == 0 or nkb == 0:
+        return out
+    if s.dtype == torch.uint8:
+        rm = _e8m0_rows(s, rows, nkb, transposed).contiguous()
+        if rm.data_ptr() % 4:
+            rm = rm.clone()  # dword view: 4-byte aligned storage
+        C.call("lsmx_transpose", rm.data_ptr(), 4, rows, nkb // 4, nkb // 4, out.data_ptr(), rows, C.stream_of(out))
         return out
     if s.dtype != torch.float32:
         s = s.float()
@@ -190,17 +201,11 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
         return c.zero_()
     a = _rows16(a_fp8.view(torch.uint8))
     bt = kmajor_operand(b_fp8.view(torch.uint8))
-    if a_scale.dtype == torch.uint8 or b_scale.dtype == torch.uint8:
-        # E8M0 bytes given: row-major scales (the 128 x 128-tile kernel)
-        sa = _e8m0_rows(a_scale, M, K // 32, transposed=False)
-        sb = _e8m0_rows(b_scale, N, K // 32, transposed=True)
-        fmt, lsa, lsb = C.SCALE_E8M0, K // 32, K // 32
-    else:
-        # fp32 scales (the reference's form): K-major E8M0, the persistent
-        # 256 x 256-tile kernel (lockstep_amd/csrc/gemm_f8f8.hip)
-        sa = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
-        sb = _e8m0_kmajor(b_scale, N, K // 32, transposed=True)
-        fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
+    # fp32 scales (the reference's form) or E8M0 bytes, either way as K-major
+    # E8M0 for the persistent 256 x 256-tile kernel (csrc/gemm_f8f8.hip)
+    sa = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
+    sb = _e8m0_kmajor(b_scale, N, K // 32, transposed=True)
+    fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
     C.call("lsmx_gemm_f8f8", a.data_ptr(), a.stride(0) if M > 1 else K, sa.data_ptr(), lsa,
            bt.data_ptr(), bt.stride(0) if N > 1 else K, sb.data_ptr(), lsb, fmt, c.data_ptr(),
            _out_code(out_dtype), N, M, N, K, C.stream_of(c))
