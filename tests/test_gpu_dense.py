@@ -67,6 +67,26 @@ def test_dual_separate_integer_grid_exact(dev, mods, dt, shared, M, N, K):
     assert np.array_equal(f64(c1), a1 @ b1) and np.array_equal(f64(c2), a2 @ b2)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=str)
+def test_ring_kernel_walks_several_tiles_per_workgroup(dev, mods, dt):
+    """More 256 x 256 tiles than CUs: the persistent ring kernel's workgroups
+    take several tiles each, across both problems of dual_separate and both K
+    halves of dual_packed, with ragged edge tiles; exact on the integer grid."""
+    dg = mods[0]
+    rng = np.random.default_rng(77)
+    M, N, K = 4352 + 40, 4352 + 24, 128   # 18 x 18 = 324 tiles
+    a1, a2 = q_grid(rng, (M, K)), q_grid(rng, (M, K))
+    b1, b2 = q_grid(rng, (K, N)), q_grid(rng, (K, N))
+    ta1, ta2, tb1, tb2 = on(dev, a1, dt), on(dev, a2, dt), on(dev, b1, dt), on(dev, b2, dt)
+    r1, r2 = a1 @ b1, a2 @ b2
+    assert np.array_equal(f64(dg.gemm(ta1, tb1)), r1)
+    c1, c2 = dg.dual_separate(ta1, ta2, tb1, tb2)
+    assert np.array_equal(f64(c1), r1) and np.array_equal(f64(c2), r2)
+    s1, s2 = dg.dual_separate(ta1, ta2, tb1, tb1)
+    assert np.array_equal(f64(s1), r1) and np.array_equal(f64(s2), a2 @ b1)
+    assert np.array_equal(f64(dg.dual_packed(ta1, ta2, tb1, tb2)), r1 + r2)
+
+
 @pytest.mark.parametrize("dt", DTYPES, ids=str)
 @pytest.mark.parametrize("shared", [False, True], ids=["b1!=b2", "shared-W"])
 def test_dual_packed_is_concatenated_k_gemm(dev, mods, dt, shared):
