@@ -333,6 +333,14 @@ def bench_reference_rows(torch, dev, n=4096):
     bt1 = b1.t().contiguous()
     row("gemm (bf16, B a view of K-contiguous rows)", _time_events(lambda: dg.gemm(a1, bt1.t())), fl1,
         PEAK_BF16_TFLOPS)
+    # FP4 -> E4M3 expansion throughput (cuda/mxfp4_mma_gemm.cu:270-287): 64 Mi
+    # words of 8 codes, 4 bytes read and 8 written per word, source bytes 0x5A
+    n32 = 64 << 20
+    up = torch.full((n32,), 0x5A5A5A5A, dtype=torch.int32, device=dev)
+    ms = _time_events(lambda: fp4.fp4_to_e4m3_words(up))
+    by = 12.0 * n32
+    rows.append({"config": "ref-bench fp4 -> e4m3 expansion, 64 Mi words (512 Mi codes)", "ms": ms,
+                 "gbs": by / ms / 1e6, "frac_hbm": by / ms / 1e6 / PEAK_HBM_GBS})
     return rows
 
 

@@ -194,6 +194,21 @@ def test_e4m3_expansion_exhaustive(dev, fp4mod, oracle):
     assert torch.equal(e4.float().cpu(), fp4mod.E2M1_VALUES)
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 255, 1027, 4096 * 3 + 2])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_e4m3_expansion_ragged_and_unaligned(dev, fp4mod, oracle, n, offset):
+    """Word counts that leave 1-3 words after the last whole quad (the
+    16-byte kernel's tail lane), and a source starting 4 bytes past a 16-byte
+    boundary (the one-word-per-lane kernel)."""
+    rng = np.random.default_rng(n * 7 + offset)
+    words = rng.integers(0, 1 << 32, size=n + offset, dtype=np.uint64).astype(np.uint32)
+    src = torch.from_numpy(words.view(np.int32)).to(dev)[offset:]
+    assert (src.data_ptr() % 16 == 0) == (offset == 0)
+    got = fp4mod.fp4_to_e4m3_words(src).cpu().numpy().view(np.uint32)
+    lo, hi = oracle.fp4x8_to_e4m3x8(words[offset:])
+    assert np.array_equal(got[0::2], lo) and np.array_equal(got[1::2], hi)
+
+
 def test_repeat_runs_are_bitwise_identical(dev, fp4mod):
     x = torch.randn(512, 4096, device=dev)
     a = fp4mod.quantize_pack_mxfp4(x)
