@@ -323,11 +323,21 @@ def bench_reference_rows(torch, dev, n=4096):
         fl2, PEAK_BF16_TFLOPS)
     row("dual: fused, one packed accumulator (dual_packed)",
         _time_events(lambda: dg.dual_packed(a1, a2, b1, b2)), fl2, PEAK_BF16_TFLOPS)
+    # splitk_*: at 4096^2 the 256 x 256 output tiles already fill every CU, so
+    # the library runs the whole K per tile; the sliced, atomic form is the
+    # one it takes for small outputs (timed below at M = N = 512)
     for splits in (4, 8):
-        row(f"dual: split-K={splits}, two accumulators",
+        row(f"dual: split-K={splits}, two accumulators (whole K per tile: the tiles fill the GPU)",
             _time_events(lambda s=splits: dg.splitk_separate(a1, a2, b1, b2, s)), fl2, PEAK_BF16_TFLOPS)
-        row(f"dual: split-K={splits}, one accumulator",
+        row(f"dual: split-K={splits}, one accumulator (whole K per tile: the tiles fill the GPU)",
             _time_events(lambda s=splits: dg.splitk_packed(a1, a2, b1, b2, s)), fl2, PEAK_BF16_TFLOPS)
+    sm = 512
+    fls = 4.0 * sm * sm * n
+    for splits in (4, 8):
+        rows.append({"config": f"ref-bench dual: split-K={splits}, two accumulators, {sm}x{sm}x{n} (K slices, atomics)",
+                     "ms": (ms := _time_events(lambda s=splits: dg.splitk_separate(a1[:sm], a2[:sm], b1[:, :sm],
+                                                                                   b2[:, :sm], s))),
+                     "tflops": fls / ms / 1e9, "frac_peak": fls / ms / 1e9 / PEAK_BF16_TFLOPS})
     row("dual_separate, shared weight (b1 is b2)", _time_events(lambda: dg.dual_separate(a1, a2, b1, b1)),
         fl2, PEAK_BF16_TFLOPS)
     bt1 = b1.t().contiguous()

@@ -155,24 +155,48 @@ def _splitk_check(K, splits, p):
         raise ValueError(f"each split's K ({K // splits}) must be a multiple of {_BK} on gfx950")
 
 
+_RING_TILE = 256
+
+
+def _launch_splits(a1, N, mode, splits):
+    """K slices to launch.  The reference splits K to give a small output
+    enough workgroups (dual_gemm.py:258-289); the sum is the same either way.
+    When the 256 x 256 output tiles of the persistent bf16/fp16 kernel already
+    number at least one per CU, the slices would only add atomic traffic, so
+    each tile takes the whole K (one summation order, no atomics)."""
+    M = a1.shape[0]
+    if a1.dtype not in (torch.bfloat16, torch.float16):
+        return splits
+    C.require_device(a1)
+    tiles = -(-M // _RING_TILE) * -(-N // _RING_TILE) * (2 if mode == 2 else 1)
+    cus = torch.cuda.get_device_properties(a1.device).multi_processor_count
+    return 1 if tiles >= cus else splits
+
+
 def splitk_packed(a1, a2s, b1, b2, splits=8, **kw):
-    """Packed accumulator over `splits` K slices, fp32 atomic adds into a zeroed output."""
+    """Packed accumulator over `splits` K slices, fp32 atomic adds into a zeroed
+    output (or the whole K per tile when the output tiles fill the GPU)."""
     p = {**_SK, **kw}
     M, K = a1.shape
     N = b1.shape[1]
     _splitk_check(K, splits, p)
-    out = torch.zeros((M, N), device=a1.device, dtype=torch.float32)
-    _dense(1, a1, a2s, b1, b2, (out,), splits)
+    ls = _launch_splits(a1, N, 1, splits)
+    # slices add into zeros; a whole-K launch writes every element
+    out = (torch.zeros if ls > 1 else torch.empty)((M, N), device=a1.device, dtype=torch.float32)
+    _dense(1, a1, a2s, b1, b2, (out,), ls)
     return out
 
 
 def splitk_separate(a1, a2, b1, b2, splits=8, **kw):
-    """Two accumulators over `splits` K slices, fp32 atomic adds into zeroed outputs."""
+    """Two accumulators over `splits` K slices, fp32 atomic adds into zeroed
+    outputs (or the whole K per tile when the output tiles fill the GPU)."""
     p = {**_SK, **kw}
     M, K = a1.shape
     N = b1.shape[1]
     _splitk_check(K, splits, p)
-    o1 = torch.zeros((M, N), device=a1.device, dtype=torch.float32)
-    o2 = torch.zeros_like(o1)
-    _dense(2, a1, a2, b1, b2, (o1, o2), splits)
+    ls = _launch_splits(a1, N, 2, splits)
+    alloc = torch.zeros if ls > 1 else torch.empty
+    o1 = alloc((M, N), device=a1.device, dtype=torch.float32)
+    o2 = alloc((M, N), device=a1.device, dtype=torch.float32)
+    _dense(2, a1, a2, b1, b2, (o1, o2), ls)
     return o1, o2

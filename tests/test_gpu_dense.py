@@ -146,6 +146,25 @@ def test_splitk_integer_grid_exact(dev, mods, dt, splits):
     assert np.array_equal(f64(s1), a1 @ b1) and np.array_equal(f64(s2), a2 @ b1)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=str)
+def test_splitk_with_tiles_for_every_cu(dev, mods, dt):
+    """An output with at least one 256 x 256 tile per CU runs the whole K per
+    tile (no slices, no atomics); the sums are those of the sliced form,
+    exact on the integer grid."""
+    dg = mods[0]
+    assert dg._launch_splits(torch.empty((4096, 64), device=dev, dtype=dt), 4096, 2, 4) == 1
+    assert dg._launch_splits(torch.empty((200, 64), device=dev, dtype=dt), 260, 2, 4) == 4
+    rng = np.random.default_rng(79)
+    M, N, K = 4096, 4352 + 24, 256
+    a1, a2 = q_grid(rng, (M, K)), q_grid(rng, (M, K))
+    b1, b2 = q_grid(rng, (K, N)), q_grid(rng, (K, N))
+    t = [on(dev, x, dt) for x in (a1, a2, b1, b2)]
+    r1, r2 = a1 @ b1, a2 @ b2
+    o1, o2 = dg.splitk_separate(*t, splits=4)
+    assert np.array_equal(f64(o1), r1) and np.array_equal(f64(o2), r2)
+    assert np.array_equal(f64(dg.splitk_packed(*t, 2)), r1 + r2)
+
+
 def test_splitk_keeps_reference_assert(dev, mods):
     dg = mods[0]
     a = torch.zeros((128, 192), device=dev, dtype=torch.bfloat16)
