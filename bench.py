@@ -40,8 +40,10 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=50)
+    # ~10 ms of untimed steps: the first few milliseconds of load after idle
+    # run ~5% slower while the clocks settle
+    p.add_argument("--warmup", type=int, default=30)
     p.add_argument("--size", type=int, default=8192)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--suite", default=None, help="also bench cfg2/cfg3, one JSON line each to this file")
