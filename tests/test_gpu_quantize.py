@@ -126,6 +126,32 @@ def test_quantize_transposed_axis_matches_oracle(dev, fp4mod, oracle, dtype, blo
         assert np.array_equal(scale.cpu().numpy().view(np.uint32), rs.view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_quantize_transposed_axis_column_pairs(dev, fp4mod, oracle, dtype):
+    """16-bit inputs read in place along the column axis: odd and even
+    leading dimensions, starts 2 bytes past a 4-byte boundary and odd and
+    even column counts all match the oracle."""
+    K, W = 256, 131
+    x = gen.normal(97, (K, W), std=0.03)
+    xh = gen.to_bf16_bits(x) if dtype == "bf16" else x.astype(np.float16).view(np.uint16)
+    big = to_dev(xh, dtype, dev)                              # [256, 131]: ldx odd
+    for lo, hi in [(0, 130), (1, 129), (2, 130), (0, 131)]:
+        view = big[:, lo:hi] if (lo, hi) != (0, 131) else big
+        if (lo, hi) == (2, 130):
+            view = big[:, :130].contiguous()[:, lo:hi]       # ldx 130, start 4 bytes in
+        rc, rs = oracle.quantize_mxfp4(np.ascontiguousarray(view.cpu().view(torch.int16).numpy().view(np.uint16).T),
+                                       32, dtype)
+        pk, e8 = fp4mod.quantize_mxfp4_t(view, 32)
+        assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(rc)), (lo, hi)
+        assert np.array_equal(e8.cpu().numpy(), oracle.scale_to_e8m0(rs)), (lo, hi)
+    xc = big[:, :130].contiguous()
+    rc, rs = oracle.quantize_mxfp4(np.ascontiguousarray(xc.cpu().view(torch.int16).numpy().view(np.uint16).T),
+                                   32, dtype)
+    pk, e8 = fp4mod.quantize_mxfp4_t(xc, 32)
+    assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(rc))
+    assert np.array_equal(e8.cpu().numpy(), oracle.scale_to_e8m0(rs))
+
+
 def test_quantize_full_size_cfg4_operand(dev, fp4mod, oracle):
     """BASELINE cfg4 operand at full size: A [8192, 8192] = 0.05 * t3, fp32."""
     g = torch.Generator(device=dev).manual_seed(4001)
