@@ -119,9 +119,13 @@ int lsmx_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n_words, void *s
  *   a_pk  [M, lda] bytes (lda >= K/2),   a_scale [M, ld_sa] (E8M0 or fp32)
  *   bt_pk [N, ldb] bytes (ldb >= K/2),   b_scale [N, ld_sb]
  *   c     [M, ldc] of c_dtype (LSMX_F32 | LSMX_BF16 | LSMX_F16), fp32 accumulate.
- *   K % 128 == 0 (mxfp4_gemm.py:166); any M, N >= 1.
- * fp32 scales must hold powers of two (what fp4.py produces); they are read
- * as their exponent field. */
+ *   K % 128 == 0 (mxfp4_gemm.py:166); any M, N >= 1; lda, ldb and the
+ *   row-major scale rows (in bytes) below 2^24.
+ * fp32 scales are the powers of two fp4.py produces.  A scale with no E8M0
+ * form (not a positive power of two in [2^-127, 2^127]) is taken as E8M0
+ * NaN: the outputs that use it are NaN, where the reference's fp32
+ * multiply (mxfp4_gemm.py:148-150) would scale by it.  E8M0 byte 0 is
+ * 2^-127. */
 int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_t ld_sa,
                    const uint8_t *bt_pk, int64_t ldb, const void *b_scale, int64_t ld_sb,
                    int scale_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N,
@@ -131,11 +135,28 @@ int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_
  *   C[M, N] = A[M, K] . deq(W)[N, K]^T, fp32 accumulate.
  * Replaces the forward of fp4_linear.py:34-40 for an unquantized activation
  * (the fake-quant F.linear on dequantized weights) at LLM MLP shapes.
- *   a [M, lda] bf16;  w_pk [N, ldw] bytes;  w_scale [N, ld_sw] E8M0 or fp32.
- *   c [M, ldc] of c_dtype.  K % 128 == 0. */
+ *   a [M, lda] bf16;  w_pk [N, ldw] bytes;  w_scale [N, ld_sw] E8M0 or fp32
+ *   (fp32 scales with no E8M0 form give NaN outputs, as lsmx_gemm_f4f4).
+ *   c [M, ldc] of c_dtype.  K % 128 == 0; lda, ldw < 2^27, scale rows
+ *   (in bytes) < 2^24. */
 int lsmx_gemm_bf16f4(const void *a, int64_t lda, const uint8_t *w_pk, int64_t ldw,
                      const void *w_scale, int64_t ld_sw, int scale_fmt, void *c, int c_dtype,
                      int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* Weight-only GEMM for any activation type: C[M, N] = A[M, K] . deq(W)^T.
+ * Replaces the fp32 product of BASELINE cfg1, Y = X @ dequantize_mxfp4(W)^T
+ * (fp4.py:75-78 inside fp4_linear.py:40's fake-quant F.linear, with X left
+ * unquantized), which the reference computes in fp32 on the CPU.
+ *   a_dtype LSMX_BF16: the same kernels as lsmx_gemm_bf16f4.
+ *   a_dtype LSMX_F32 | LSMX_F16: each activation is split exactly into three
+ *   (fp32) or two (fp16) bf16 terms, each multiplied with the exact bf16
+ *   weight on the MFMA: exact products, fp32 accumulation -- the arithmetic
+ *   of an fp32 matmul, without narrowing X to bf16 (exact for |x| >= 2^-110).
+ *   a [M, lda] of a_dtype with 16-byte aligned rows; other arguments as
+ *   lsmx_gemm_bf16f4. */
+int lsmx_gemm_wonly_f4(const void *a, int a_dtype, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                       const void *w_scale, int64_t ld_sw, int scale_fmt, void *c, int c_dtype, int64_t ldc,
+                       int64_t M, int64_t N, int64_t K, void *stream);
 
 /* Dual-batch weight-only GEMM: C0 = A0 . deq(W)^T and C1 = A1 . deq(W)^T in
  * ONE launch, each W tile loaded and dequantized once for both batches.
@@ -151,7 +172,8 @@ int lsmx_gemm_dual_bf16f4(const void *a0, const void *a1, int64_t lda, const uin
  *   a0, a1 [M, lda] and bt0, bt1 [N, ldb] of dtype LSMX_BF16 | LSMX_F16 | LSMX_E4M3.
  *   mode 0: c0 = a0 . bt0^T                       dual_gemm.py:189-226 gemm
  *   mode 1: c0 = a0 . bt0^T + a1 . bt1^T          dual_gemm.py:43-72, 230-241 dual_packed
- *           (one accumulator; the caller pre-scales a1 by 2^s as the reference does)
+ *           (one accumulator; the caller pre-scales a1 by 2^s as the reference does;
+ *           64-deep K blocks of the two products alternate, as in its loop)
  *   mode 2: c0 = a0 . bt0^T,  c1 = a1 . bt1^T     dual_gemm.py:79-110, 244-255 dual_separate
  * splits > 1: K is cut into `splits` equal slices whose partial sums are added
  * into c0 (and c1) with fp32 atomics, so the outputs must hold zeros on entry

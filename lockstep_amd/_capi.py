@@ -40,6 +40,7 @@ SIGNATURES = {
     "lsmx_fp4_to_e4m3": [_vp, _vp, _i64, _vp],
     "lsmx_gemm_f4f4": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_bf16f4": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
+    "lsmx_gemm_wonly_f4": [_vp, _int, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_dual_bf16f4": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64,
                               _i64, _vp],
     "lsmx_gemm_dense": [_vp, _vp, _i64, _vp, _vp, _i64, _int, _int, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp],

@@ -36,14 +36,32 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: ROCm is required to build liblsmx.so")
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES]]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every source to an object in parallel (each kernel is launched
+    from its own translation unit, so no relocatable device code is needed),
+    then link liblsmx.so."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    cc = hipcc()
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objs = [objdir / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [[cc, *compile_flags, "-c", "-o", str(o), str(CSRC / s)] for s, o in zip(SOURCES, objs)]
+    jobs = jobs or min(len(cmds), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as ex:
+        for f in [ex.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

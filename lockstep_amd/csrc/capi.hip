@@ -211,6 +211,12 @@ int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_
         return fail(LSMX_ERR_ALIGN, "%s: packed rows must be 16-byte aligned", fn);
     if (int r = check_scale(fn, a_scale, ld_sa, scale_fmt, 4, M, K)) return r;
     if (int r = check_scale(fn, b_scale, ld_sb, scale_fmt, 4, N, K)) return r;
+    // the kernel's per-lane buffer offsets are 32-bit: up to 256 rows of
+    // codes, and of row-major scales, past a descriptor's base
+    const int64_t sbw = scale_fmt == LSMX_SCALE_F32 ? 4 : 1;
+    if (lda >= ((int64_t)1 << 24) || ldb >= ((int64_t)1 << 24) ||
+        (scale_fmt != LSMX_SCALE_E8M0_KMAJOR && (ld_sa * sbw >= ((int64_t)1 << 24) || ld_sb * sbw >= ((int64_t)1 << 24))))
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
     if (!aligned(c, c_dtype == LSMX_F32 ? 4 : 2)) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
     if (int r = device_guard()) return r;
     if (M == 0 || N == 0) return LSMX_OK;
@@ -312,21 +318,29 @@ int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, 
     return launched(lsmx::launch_scale_to_e8m0(s, rows, cols, lds, layout, out, ldo, (hipStream_t)stream), fn);
 }
 
-static int w4_common(const char *fn, const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
-                     const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype, int64_t ldc,
-                     int64_t M, int64_t N, int64_t K, void *stream) {
+static int w4_common(const char *fn, const void *a0, const void *a1, int a_dtype, int64_t lda, const uint8_t *w_pk,
+                     int64_t ldw, const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype,
+                     int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
     if (!a0 || !w_pk || !w_scale || !c0) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (a_dtype != LSMX_BF16 && a_dtype != LSMX_F32 && a_dtype != LSMX_F16)
+        return fail(LSMX_ERR_DTYPE, "%s: a_dtype %d unsupported", fn, a_dtype);
+    if (a1 && a_dtype != LSMX_BF16) return fail(LSMX_ERR_DTYPE, "%s: the dual form takes bf16 activations", fn);
     if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_F32) return fail(LSMX_ERR_DTYPE, "%s: scale_fmt", fn);
     if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
     if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
     if (K % 128 != 0) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
     if (M > (int64_t)1 << 30 || N > (int64_t)1 << 30) return fail(LSMX_ERR_SHAPE, "%s: M, N must be < 2^30", fn);
     if (lda < K || ldw < K / 2 || ldc < N) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
-    if (!aligned(a0, 16) || (a1 && !aligned(a1, 16)) || (lda * 2) % 16)
+    if (!aligned(a0, 16) || (a1 && !aligned(a1, 16)) || (lda * elem_size(a_dtype)) % 16)
         return fail(LSMX_ERR_ALIGN, "%s: activation rows must be 16-byte aligned", fn);
     if (!aligned(w_pk, 16) || ldw % 16) return fail(LSMX_ERR_ALIGN, "%s: packed weight rows must be 16-byte aligned", fn);
     if (scale_fmt == LSMX_SCALE_E8M0_KMAJOR) return fail(LSMX_ERR_DTYPE, "%s: K-major scales are not supported here", fn);
     if (int r = check_scale(fn, w_scale, ld_sw, scale_fmt, 2, N, K)) return r;
+    // 32-bit per-lane buffer offsets: 8 activation rows, 32 weight rows and
+    // 256 rows of scales past a descriptor's base
+    if (lda >= ((int64_t)1 << 27) || ldw >= ((int64_t)1 << 27) ||
+        ld_sw * (scale_fmt == LSMX_SCALE_F32 ? 4 : 1) >= ((int64_t)1 << 24))
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
     const int cb = c_dtype == LSMX_F32 ? 4 : 2;
     if (!aligned(c0, cb) || (c1 && !aligned(c1, cb))) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
     if (int r = device_guard()) return r;
@@ -334,12 +348,13 @@ static int w4_common(const char *fn, const void *a0, const void *a1, int64_t lda
     if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
     lsmx::GemmArgs g{reinterpret_cast<const uint8_t *>(a0), reinterpret_cast<const uint8_t *>(a1), lda, nullptr, 0,
                      w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype, ldc, M, N, K};
+    if (a_dtype != LSMX_BF16) return launched(lsmx::launch_gemm_xf4(g, a_dtype, (hipStream_t)stream), fn);
     return launched(lsmx::launch_gemm_bf16f4(g, (hipStream_t)stream), fn);
 }
 
 int lsmx_gemm_bf16f4(const void *a, int64_t lda, const uint8_t *w_pk, int64_t ldw, const void *w_scale, int64_t ld_sw,
                      int scale_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
-    return w4_common("lsmx_gemm_bf16f4", a, nullptr, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c, nullptr, c_dtype,
+    return w4_common("lsmx_gemm_bf16f4", a, nullptr, LSMX_BF16, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c, nullptr, c_dtype,
                      ldc, M, N, K, stream);
 }
 
@@ -347,8 +362,15 @@ int lsmx_gemm_dual_bf16f4(const void *a0, const void *a1, int64_t lda, const uin
                           const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype,
                           int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
     if (!a1 || !c1) return fail(LSMX_ERR_ARG, "lsmx_gemm_dual_bf16f4: null pointer");
-    return w4_common("lsmx_gemm_dual_bf16f4", a0, a1, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype,
+    return w4_common("lsmx_gemm_dual_bf16f4", a0, a1, LSMX_BF16, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype,
                      ldc, M, N, K, stream);
+}
+
+int lsmx_gemm_wonly_f4(const void *a, int a_dtype, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                       const void *w_scale, int64_t ld_sw, int scale_fmt, void *c, int c_dtype, int64_t ldc,
+                       int64_t M, int64_t N, int64_t K, void *stream) {
+    return w4_common("lsmx_gemm_wonly_f4", a, nullptr, a_dtype, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c, nullptr,
+                     c_dtype, ldc, M, N, K, stream);
 }
 
 }  // extern "C"

@@ -76,7 +76,7 @@ LSMX_DEV uint32_t load_scale2(const void *s, int64_t off) {
     // 2 consecutive block scales as E8M0 bytes in the low 16 bits
     if constexpr (SF32) {
         const u32x2 v = *reinterpret_cast<const u32x2 *>(reinterpret_cast<const float *>(s) + off);
-        return ((v[0] >> 23) & 0xFF) | (((v[1] >> 23) & 0xFF) << 8);
+        return f32_scale_e8m0(v[0]) | (f32_scale_e8m0(v[1]) << 8);
     } else {
         return *reinterpret_cast<const uint16_t *>(reinterpret_cast<const uint8_t *>(s) + off);
     }
@@ -236,6 +236,206 @@ __global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(
                 }
             }
     }
+}
+
+// ------------------------------------------------------------------ fp32 / fp16 activations
+// Weight-only GEMM with wider activations: Y = X . deq(W)^T for X in fp32
+// (BASELINE cfg1: the fake-quant forward of fp4_linear.py:40 with an
+// unquantized fp32 X, deq(W) of fp4.py:75-78) or fp16.  Each activation is
+// split exactly into NTERM bf16 terms, each the bf16 truncation of what the
+// terms before it leave,
+//     hi = tr(x),  mid = tr(x - hi),  lo = x - hi - mid     (fp32: NTERM = 3)
+// (x has 24 significant bits and each term holds 8; every subtraction and
+// the last term are exact; fp16's 11 bits need hi and mid only), and each
+// term runs through v_mfma_f32_32x32x16_bf16 against the exact bf16 weight.
+// The products are exact in fp32, so only the fp32 accumulation rounds, as
+// in an fp32 matmul.  Per K-step the terms are added hi, mid, lo.
+// Tile: 128 rows x 128 weight columns per workgroup of 4 waves (2 x 2, 64 x
+// 64 per wave), 64-deep K stages staged through VGPRs into a double-buffered
+// LDS tile (256 bytes of fp32 per row per stage).  The K positions are those
+// of the bf16 kernel above: at K-step s lane half h supplies X[row][32h + 8s
+// .. +8] and codes 8s .. 8s+7 of the weight's block h of the stage.
+namespace xf {
+constexpr int BR = 128, BN = 128, BK = 64, NT = 256;
+constexpr int RT = 2, CTW = 2;     // 32 x 32 MFMA tiles per wave (rows, columns)
+}  // namespace xf
+
+template <int AT, bool SF32, int CT>
+__global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
+    using namespace xf;
+    constexpr int ES = AT == LSMX_F32 ? 4 : 2;        // activation bytes
+    constexpr int NTERM = AT == LSMX_F32 ? 3 : 2;     // bf16 terms per activation
+    constexpr int ROW_B = BK * ES;                    // bytes per row per stage
+    constexpr int CPR = ROW_B / 16;                   // 16-byte chunks per row (16 or 8)
+    constexpr int XA = BR * CPR / NT;                 // A chunks per thread per stage
+    constexpr int XW = BN * 2 / NT;                   // W chunks per thread per stage (1)
+    __shared__ __attribute__((aligned(16))) uint8_t sA[2][BR * ROW_B];   // 2 x 32 / 16 KiB
+    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * 32];      // [half][col][16 B]
+    __shared__ uint32_t sS[2][BN];
+
+    const int tiles_m = (int)((g.M + BR - 1) / BR), tiles_n = (int)((g.N + BN - 1) / BN);
+    int tm, tn;
+    tile_coords_w(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * BR, n0 = (int64_t)tn * BN;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int frow = lane & 31, half = lane >> 5;
+    const int nk = (int)(g.K / BK);
+
+    // 16-byte chunk c of row r sits at chunk c ^ swz(r) of the LDS row; the
+    // swizzle moves whole 32-byte pairs for fp32 (a fragment is two chunks)
+    auto swz = [](int r) { return ES == 4 ? (a_swz(r) << 1) : a_swz(r); };
+    const uint8_t *ga[XA];
+    int a_off[XA];
+#pragma unroll
+    for (int i = 0; i < XA; ++i) {
+        const int q = i * NT + t;
+        const int row = q / CPR, c = q % CPR;
+        ga[i] = g.a + min(m0 + row, g.M - 1) * g.lda * ES + c * 16;
+        a_off[i] = row * ROW_B + ((c ^ swz(row)) << 4);
+    }
+    const uint8_t *gw[XW];
+    int w_off[XW];
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+        const int q = i * NT + t;
+        const int row = q >> 1, h = q & 1;
+        gw[i] = g.b + min(n0 + row, g.N - 1) * g.ldb + h * 16;
+        w_off[i] = h * (BN * 16) + row * 16;
+    }
+    const int64_t s_row = min(n0 + (t % BN), g.N - 1) * g.ld_sb;
+
+    u32x4 ra[XA], rw[XW];
+    uint32_t rs;
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < XA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(ga[i] + (int64_t)kt * ROW_B);
+#pragma unroll
+        for (int i = 0; i < XW; ++i) rw[i] = *reinterpret_cast<const u32x4 *>(gw[i] + (int64_t)kt * 32);
+        rs = load_scale2<SF32>(g.sb, s_row + (int64_t)kt * 2);
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XA; ++i) *reinterpret_cast<u32x4 *>(&sA[buf][a_off[i]]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < XW; ++i) *reinterpret_cast<u32x4 *>(&sW[buf][w_off[i]]) = rw[i];
+        if (t < BN) sS[buf][t] = rs;
+    };
+
+    v16f acc[RT][CTW];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < CTW; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    gload(0);
+    swrite(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+        v8bf fw[CTW][4];
+#pragma unroll
+        for (int j = 0; j < CTW; ++j) {
+            const int col = wn * 64 + j * 32 + frow;
+            const u32x4 pw = *reinterpret_cast<const u32x4 *>(&sW[buf][half * (BN * 16) + col * 16]);
+            const float sc = e8m0_scale_f32((sS[buf][col] >> (8 * half)) & 0xFF);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 0);
+                const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 1);
+                const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 2);
+                const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 3);
+                fw[j][s] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            v8bf fa[RT][NTERM];
+#pragma unroll
+            for (int i = 0; i < RT; ++i) {
+                const int row = wm * 64 + i * 32 + frow;
+                float x[8];
+                if constexpr (ES == 4) {
+                    const int c = 2 * (4 * half + s);   // fp32 chunks 2c', 2c'+1: X[row][32h + 8s .. +8]
+                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(&sA[buf][row * ROW_B + ((c ^ swz(row)) << 4)]);
+                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(&sA[buf][row * ROW_B + (((c + 1) ^ swz(row)) << 4)]);
+                    x[0] = u2f(v0.x); x[1] = u2f(v0.y); x[2] = u2f(v0.z); x[3] = u2f(v0.w);
+                    x[4] = u2f(v1.x); x[5] = u2f(v1.y); x[6] = u2f(v1.z); x[7] = u2f(v1.w);
+                } else {
+                    const int c = 4 * half + s;
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(&sA[buf][row * ROW_B + ((c ^ swz(row)) << 4)]);
+                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        x[2 * p] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[p] & 0xFFFFu));
+                        x[2 * p + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[p] >> 16));
+                    }
+                }
+                v8bf hi, mid, lo;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    // truncation split: hi keeps the top 8 significant bits,
+                    // mid the next 8, lo the rest (exact for |x| >= 2^-110,
+                    // where lo is at least a bf16 subnormal's ulp); inf and
+                    // NaN pass through hi alone
+                    const uint32_t xb = f2u(x[e]);
+                    const bool special = (xb & 0x7F800000u) == 0x7F800000u;
+                    const uint32_t hb = (xb >> 16) | (special && (xb & 0xFFFFu) ? 0x40u : 0u);
+                    const float r1 = special ? 0.0f : x[e] - u2f(hb << 16);
+                    const uint32_t mb = f2u(r1) >> 16;
+                    const float r2 = r1 - u2f(mb << 16);
+                    hi[e] = __builtin_bit_cast(__bf16, (uint16_t)hb);
+                    mid[e] = __builtin_bit_cast(__bf16, (uint16_t)mb);
+                    lo[e] = __builtin_bit_cast(__bf16, (uint16_t)(f2u(r2) >> 16));
+                }
+                fa[i][0] = hi;
+                fa[i][1] = mid;
+                if constexpr (NTERM == 3) fa[i][NTERM - 1] = lo;
+            }
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+#pragma unroll
+                for (int j = 0; j < CTW; ++j)
+#pragma unroll
+                    for (int p = 0; p < NTERM; ++p)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][p], fw[j][s], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) swrite(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < CTW; ++j) {
+            const int64_t col = n0 + wn * 64 + j * 32 + frow;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int64_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                if (row < g.M && col < g.N) store_cw<CT>(g.c, row * g.ldc + col, acc[i][j][e]);
+            }
+        }
+}
+
+hipError_t launch_gemm_xf4(const GemmArgs &g, int a_dtype, hipStream_t s) {
+    const int tiles = (int)(((g.M + xf::BR - 1) / xf::BR) * ((g.N + xf::BN - 1) / xf::BN));
+    const dim3 grid(tiles), blk(xf::NT);
+    const bool f = g.scale_fmt == LSMX_SCALE_F32;
+#define LSMX_X(AT, F, CT) hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT>), grid, blk, 0, s, g)
+#define LSMX_XC(AT, F)                                           \
+    do {                                                         \
+        if (g.c_dtype == LSMX_F32) LSMX_X(AT, F, LSMX_F32);      \
+        else if (g.c_dtype == LSMX_BF16) LSMX_X(AT, F, LSMX_BF16); \
+        else LSMX_X(AT, F, LSMX_F16);                            \
+    } while (0)
+    if (a_dtype == LSMX_F32) { if (f) LSMX_XC(LSMX_F32, true); else LSMX_XC(LSMX_F32, false); }
+    else { if (f) LSMX_XC(LSMX_F16, true); else LSMX_XC(LSMX_F16, false); }
+#undef LSMX_XC
+#undef LSMX_X
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ ring
@@ -587,7 +787,7 @@ __global__ __launch_bounds__(64 * sk::WK, MT <= 2 ? 4 : 2) void gemm_bf16f4_skin
                 for (int ct = 0; ct < CT; ++ct) {
                     wv[u][ct] = *reinterpret_cast<const u32x4 *>(wrow[ct] + (int64_t)c * 64);
                     const int64_t so = srow[ct] + (int64_t)c * 4;
-                    sv[u][ct] = sf32 ? (f2u(reinterpret_cast<const float *>(g.sb)[so]) >> 23) & 0xFF
+                    sv[u][ct] = sf32 ? f32_scale_e8m0(f2u(reinterpret_cast<const float *>(g.sb)[so]))
                                      : reinterpret_cast<const uint8_t *>(g.sb)[so];
                 }
 #pragma unroll
@@ -727,7 +927,7 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) {
                     w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow[r] + (int64_t)b * 16));
-                    e[u][r] = SF32 ? (f2u(reinterpret_cast<const float *>(srow[r])[b]) >> 23) & 0xFF : srow[r][b];
+                    e[u][r] = SF32 ? f32_scale_e8m0(f2u(reinterpret_cast<const float *>(srow[r])[b])) : srow[r][b];
                 }
             }
         }

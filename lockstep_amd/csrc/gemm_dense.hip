@@ -207,24 +207,24 @@ __global__ __launch_bounds__(dn::NT, (dense_lds_bytes<DT, MODE, SHB>() <= 80 * 1
             gload(kt + 1);
             sload(kt + 1, nsa, nsb);
         }
+        // product by product over the 64-deep stage: in MODE 1 the stage's
+        // A0.B0 block is added before its A1.B1 block, the order of the
+        // reference's loop (dual_gemm.py:59-61)
 #pragma unroll
-        for (int s = 0; s < T::KS; ++s) {
-            u32x4 fb[NOB][TN][2];
+        for (int o = 0; o < NO; ++o) {
+            const int ai = MODE == 2 ? o : 0, bi = SHB ? 0 : o;
 #pragma unroll
-            for (int o = 0; o < NOB; ++o)
+            for (int s = 0; s < T::KS; ++s) {
+                u32x4 fa[TM][2], fb[TN][2];
 #pragma unroll
-                for (int j = 0; j < TN; ++j) frag(sB[buf][o], wn * 64 + j * 32 + frow, s, fb[o][j]);
-#pragma unroll
-            for (int o = 0; o < NO; ++o) {
-                u32x4 fa[TM][2];
+                for (int j = 0; j < TN; ++j) frag(sB[buf][bi], wn * 64 + j * 32 + frow, s, fb[j]);
 #pragma unroll
                 for (int i = 0; i < TM; ++i) frag(sA[buf][o], wm * 64 + i * 32 + frow, s, fa[i]);
-                const int ai = MODE == 2 ? o : 0, bi = SHB ? 0 : o;
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        acc[ai][i][j] = mma<DT>(fa[i], fb[bi][j], acc[ai][i][j], sa[i], sb[j]);
+                        acc[ai][i][j] = mma<DT>(fa[i], fb[j], acc[ai][i][j], sa[i], sb[j]);
             }
         }
         if (kt + 1 < nk) {
@@ -308,10 +308,7 @@ __global__ void scale_to_e8m0_kernel(const float *__restrict__ s, int64_t rows, 
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows * cols) return;
     const int64_t r = i / cols, c = i - r * cols;
-    const uint32_t b = f2u(s[r * lds + c]);
-    const uint32_t ex = b >> 23;  // sign is bit 8: negative scales fail both tests
-    const bool pow2 = ((b & 0x7FFFFFu) == 0 && ex >= 1 && ex <= 254) || b == 0x00400000u;
-    const uint8_t e = pow2 ? (uint8_t)ex : (uint8_t)0xFF;
+    const uint8_t e = (uint8_t)f32_scale_e8m0(f2u(s[r * lds + c]));
     const bool tin = layout & LSMX_E8M0_IN_T;
     const int64_t orow = tin ? c : r, blk = tin ? r : c;
     if (layout & LSMX_E8M0_OUT_KMAJOR) out[((blk >> 2) * ldo + orow) * 4 + (blk & 3)] = e;

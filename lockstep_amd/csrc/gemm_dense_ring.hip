@@ -4,8 +4,9 @@
 //   MODE 0  C0 = A0 . B0^T                      gemm          (dual_gemm.py:188-226)
 //   MODE 1  C0 = A0 . B0^T + A1 . B1^T          dual_packed   (dual_gemm.py:42-72, 230-241)
 //   MODE 2  C0 = A0 . B0^T,  C1 = A1 . B1^T     dual_separate (dual_gemm.py:78-110, 244-255)
-// MODE 1 is one GEMM over the concatenated K (the reference pre-scales A1 on
-// the host; the kernel only adds the products).  MODE 2 is two GEMM problems
+// MODE 1 is one GEMM over the interleaved K (the reference pre-scales A1 on
+// the host; the kernel only adds the products): 64-deep K blocks of A0.B0
+// and A1.B1 alternate, in the order of the reference's loop.  MODE 2 is two GEMM problems
 // in one launch: the persistent workgroups walk the tiles of both, ordered so
 // that the two tiles sharing (m, n) run side by side on one XCD, so a shared
 // B (b0 == b1) is read once per XCD from HBM and hit in L2 the second time.
@@ -73,7 +74,7 @@ template <int DT, int MODE>
 __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g) {
     using namespace dr;
     constexpr int P = MODE == 2 ? 2 : 1;      // GEMM problems
-    constexpr int KC = MODE == 1 ? 2 : 1;     // K halves per tile (MODE 1: A0.B0 then A1.B1)
+    constexpr int KC = MODE == 1 ? 2 : 1;     // products per tile (MODE 1: A0.B0 and A1.B1, alternating)
     __shared__ __attribute__((aligned(16))) uint8_t sA[S][TILE_B];
     __shared__ __attribute__((aligned(16))) uint8_t sB[S][TILE_B];
 
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g)
     const int tiles = tiles_m * tiles_n;
     const int total = P * tiles;
     const int my_tiles = (total - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int nkh = (int)(g.K * 2 / BKB);     // stages per K half
+    const int nkh = (int)(g.K * 2 / BKB);     // stages per product
     const int nk = KC * nkh;                  // stages per tile
 
     const int t = threadIdx.x, lane = t & 63;
@@ -132,10 +133,13 @@ __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g)
         nb = min(g.N - n0, (int64_t)BN) * ldb_b;
     };
     v4i_rsrc rsA, rsB;
-    // descriptors of stage kt of the refill tile, in two parts
+    // descriptors of stage kt of the refill tile, in two parts.  MODE 1
+    // alternates the two products every 64-deep K block, as the reference's
+    // loop does (dual_gemm.py:59-61): stage kt is K block kt/2 of A0.B0
+    // (kt even) or of A1.B1 (kt odd).
     auto make_desc = [&](int part, int kt) __attribute__((always_inline)) {
-        const int h = KC == 2 && kt >= nkh ? 1 : 0;
-        const int64_t ko = (int64_t)(kt - h * nkh) * BKB;
+        const int h = KC == 2 ? (kt & 1) : 0;
+        const int64_t ko = (int64_t)(KC == 2 ? kt >> 1 : kt) * BKB;
         if (part == 0) rsA = buf_rsrc((h ? pa[KC - 1] : pa[0]) + ko, (uint64_t)(na - ko));
         else rsB = buf_rsrc((h ? pb[KC - 1] : pb[0]) + ko, (uint64_t)(nb - ko));
     };

@@ -284,8 +284,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
         uint32_t v;
         if constexpr (SF32) {
             const u32x4 f = *reinterpret_cast<const u32x4 *>(tab + r * 16);
-            v = (((f[0] >> 23) & 0xFF) | (((f[1] >> 23) & 0xFF) << 8) | (((f[2] >> 23) & 0xFF) << 16) |
-                 (((f[3] >> 23) & 0xFF) << 24)) >> (16 * half);
+            v = (f32_scale_e8m0(f[0]) | (f32_scale_e8m0(f[1]) << 8) | (f32_scale_e8m0(f[2]) << 16) |
+                 (f32_scale_e8m0(f[3]) << 24)) >> (16 * half);
         } else if constexpr (KS == 4) {
             v = *reinterpret_cast<const uint32_t *>(tab + r * 4);
         } else {

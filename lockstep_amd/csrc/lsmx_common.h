@@ -67,7 +67,21 @@ LSMX_DEV uint32_t e2m1_code(uint32_t xbits, uint32_t e8m0) {
     return mag | (sign << 3);
 }
 
-LSMX_HD float e8m0_to_f32(uint32_t e) { return e == 255u ? u2f(0x7FC00000u) : u2f(e << 23); }
+// E8M0 byte -> fp32 scale: 2^(e - 127); byte 0 is 2^-127 (the fp32
+// subnormal 0x00400000) and 0xFF is NaN.
+LSMX_HD float e8m0_to_f32(uint32_t e) {
+    return e == 255u ? u2f(0x7FC00000u) : (e == 0u ? u2f(0x00400000u) : u2f(e << 23));
+}
+
+// E8M0 byte of an fp32 block scale (bits b): its biased exponent when the
+// scale is a positive power of two in [2^-127, 2^127], else 0xFF (E8M0 NaN).
+// A scale with no E8M0 form (1.5, -2, 0, inf) thus turns the outputs that
+// use it into NaN rather than being truncated to its exponent field.
+LSMX_HD uint32_t f32_scale_e8m0(uint32_t b) {
+    const uint32_t ex = b >> 23;  // the sign is bit 8: negative scales fail both tests
+    const bool pow2 = ((b & 0x7FFFFFu) == 0u && ex >= 1u && ex <= 254u) || b == 0x00400000u;
+    return pow2 ? (b == 0x00400000u ? 0u : ex) : 0xFFu;
+}
 
 // E2M1 code -> value (fp4.py:24).
 LSMX_HD float e2m1_value(uint32_t code) {

@@ -74,6 +74,7 @@ hipError_t launch_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n, hipS
 hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
 hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s);
+hipError_t launch_gemm_xf4(const GemmArgs &g, int a_dtype, hipStream_t s);
 hipError_t launch_gemm_dense(const DenseArgs &g, int dtype, int mode, hipStream_t s);
 bool dense_ring_ok(const DenseArgs &g, int dtype);
 hipError_t launch_gemm_dense_ring(const DenseArgs &g, int dtype, int mode, hipStream_t s);

@@ -19,7 +19,7 @@ import torch
 
 from . import _capi as C
 from . import fp4 as _fp4
-from .mxfp4_gemm import _rows16, _scales, kmajor_operand
+from .mxfp4_gemm import _rows16, _scales, kmajor_operand, mxfp4_gemm_bf16
 
 
 def slot_offset(K: int) -> int:
@@ -34,8 +34,14 @@ def unpack_dual(acc: torch.Tensor, s: int):
     return acc - c2 * w, c2
 
 
-# Tile configuration of the gfx950 dense kernels (the reference's CFG keys).
-CFG = dict(BLOCK_M=128, BLOCK_N=128, BLOCK_K=64, num_warps=4, num_stages=2)
+# Tile configuration of the gfx950 dense kernels under the reference's CFG
+# keys: the persistent ring kernel that gemm / dual_packed / dual_separate
+# run on (csrc/gemm_dense_ring.hip: 256 x 256 tiles, 64-deep K stages,
+# 8 waves, a 2-slot LDS ring) ...
+CFG = dict(BLOCK_M=256, BLOCK_N=256, BLOCK_K=64, num_warps=8, num_stages=2)
+# ... and the 128 x 128 kernel that runs K slices with fp32 atomics when the
+# output has fewer 256 x 256 tiles than the GPU has CUs (csrc/gemm_dense.hip:
+# 4 waves, double-buffered LDS).
 _SK = dict(BM=128, BN=128, BK=64, warps=4, stages=2)
 
 
@@ -43,14 +49,24 @@ def dual_mxfp4(a0, a1, w_pk, w_scale, out_dtype=torch.bfloat16):
     """C0 = a0 @ deq(W).T and C1 = a1 @ deq(W).T in one launch.
 
     a0, a1 [M, K] bf16; w_pk [N, K//2] packed MXFP4; w_scale [N, K//32]
-    (fp32 powers of two or E8M0 bytes).  Returns (C0, C1), [M, N] each."""
+    (fp32 powers of two or E8M0 bytes).  Returns (C0, C1), [M, N] each.
+    fp32 / fp16 batches are not narrowed to bf16: they run as two launches
+    of the exact-split weight-only kernel (mxfp4_gemm_bf16), which reads W
+    once per batch."""
     M, K = a0.shape
     N, Kh = w_pk.shape
     assert a1.shape == a0.shape, "a0 and a1 must have the same shape"
     assert K == 2 * Kh and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
+    if w_scale.dim() != 2 or tuple(w_scale.shape) != (N, K // 32):
+        raise AssertionError(f"scale must be [{N}, {K // 32}] (rows, K//32), got {list(w_scale.shape)}")
+    if a0.dtype != a1.dtype:
+        raise TypeError(f"a0 and a1 dtypes differ: {a0.dtype} and {a1.dtype}")
     C.require_device(a0, a1, w_pk, w_scale)
-    a0 = _rows16(a0.to(torch.bfloat16))
-    a1 = _rows16(a1.to(torch.bfloat16))
+    if a0.dtype != torch.bfloat16:
+        return (mxfp4_gemm_bf16(a0, w_pk, w_scale, out_dtype=out_dtype),
+                mxfp4_gemm_bf16(a1, w_pk, w_scale, out_dtype=out_dtype))
+    a0 = _rows16(a0)
+    a1 = _rows16(a1)
     if a0.stride(0) != a1.stride(0):
         a0, a1 = a0.contiguous(), a1.contiguous()
     w_pk = _rows16(w_pk)

@@ -174,15 +174,24 @@ def quantize_mxfp4_t(x: torch.Tensor, block: int = 32, packed: bool = True, e8m0
 
 
 def e8m0_to_scale(e8m0: torch.Tensor) -> torch.Tensor:
-    """E8M0 bytes -> fp32 powers of two (0xFF -> NaN).  Exact."""
-    s = (e8m0.to(torch.int32) << 23).view(torch.float32)
+    """E8M0 bytes -> fp32 powers of two 2^(e - 127) (0xFF -> NaN; byte 0 ->
+    2^-127, the fp32 subnormal 0x00400000).  Exact."""
+    e = e8m0.to(torch.int32)
+    s = torch.where(e == 0, torch.full_like(e, 0x00400000), e << 23).view(torch.float32)
     return torch.where(e8m0 == 255, torch.full_like(s, float("nan")), s)
 
 
 def scale_to_e8m0(scale: torch.Tensor) -> torch.Tensor:
-    """fp32 powers of two -> E8M0 bytes (the exponent field; NaN -> 0xFF).  Exact."""
-    e = ((scale.contiguous().view(torch.int32) >> 23) & 0xFF).to(torch.uint8)
-    return torch.where(torch.isnan(scale), torch.full_like(e, 255), e)
+    """fp32 powers of two in [2^-127, 2^127] -> E8M0 bytes (the biased
+    exponent; 2^-127 -> 0).  Exact inverse of e8m0_to_scale.  A scale with no
+    E8M0 form (NaN, not a positive power of two) -> 0xFF (NaN), as the GEMMs
+    treat it."""
+    b = scale.contiguous().view(torch.int32)
+    ex = (b >> 23) & 0x1FF                          # sign in bit 8: negatives fail
+    pow2 = ((b & 0x7FFFFF) == 0) & (ex >= 1) & (ex <= 254)
+    sub = b == 0x00400000
+    e = torch.where(pow2, ex, torch.where(sub, torch.zeros_like(ex), torch.full_like(ex, 255)))
+    return e.to(torch.uint8)
 
 
 def _scale_fmt(scale: torch.Tensor) -> int:
@@ -280,8 +289,12 @@ def unpack_fp4(packed: torch.Tensor) -> torch.Tensor:
 def reference_mxfp4_gemm(a_codes, a_scale, b_codes, b_scale, block=32):
     """float64 reference for C = A @ B with A [M,K], B [K,N] (fp4.py:103-112).
 
-    b_codes is [K, N] and b_scale is [K//block, N], so B is quantized along K."""
-    A = dequantize_mxfp4(a_codes, a_scale, block).double()                  # [M,K]
+    b_codes is [K, N] and b_scale is [K//block, N], so B is quantized along K.
+    A test helper: plain torch in float64, on whatever device its inputs
+    live (CPU included), independent of the HIP kernels it checks."""
+    M, Ka = a_codes.shape
+    Av = E2M1_VALUES.to(a_codes.device)[a_codes.long()].double()            # [M,K]
+    A = (Av.reshape(M, Ka // block, block) * a_scale.double().unsqueeze(-1)).reshape(M, Ka)
     Bv = E2M1_VALUES.to(b_codes.device)[b_codes.long()].double()            # [K,N]
     K, N = Bv.shape
     B = (Bv.reshape(K // block, block, N) * b_scale.double().unsqueeze(1)).reshape(K, N)

@@ -18,8 +18,11 @@ import torch
 from . import _capi as C
 from . import fp4 as _fp4
 
-# Tile configuration of the gfx950 kernel (the reference's CFG keys).
-CFG = dict(BLOCK_M=256, BLOCK_N=256, SUB=4, GROUP_M=4, num_warps=4, num_stages=2)
+# Tile configuration of the f4 x f4 kernel that runs at K % 256 == 0 with
+# E8M0 scales (csrc/gemm_f4f4.hip), under the reference's CFG keys:
+# 256 x 256 tiles, SUB*32 = 256 K codes (four 64-code MFMA K-steps) per
+# stage, 4-row tile groups, 8 waves of 64 lanes, a 2-slot LDS ring.
+CFG = dict(BLOCK_M=256, BLOCK_N=256, SUB=8, GROUP_M=4, num_warps=8, num_stages=2)
 
 
 def _out_code(dt: torch.dtype) -> int:
@@ -34,6 +37,11 @@ def _rows16(t: torch.Tensor) -> torch.Tensor:
 
 
 def _scales(s: torch.Tensor, rows: int, nkb: int) -> torch.Tensor:
+    """Row-major block scales [rows, nkb] with unit stride along the blocks
+    and 4-byte aligned rows.  The kernels size their scale reads from the GEMM
+    shape, so a tensor of any other shape is refused before any launch."""
+    assert s.dim() == 2 and tuple(s.shape) == (rows, nkb), \
+        f"scale must be [{rows}, {nkb}] (rows, K//32), got {list(s.shape)}"
     fmt_bytes = 4 if s.dtype == torch.float32 else 1
     if s.stride(-1) != 1 or (rows > 1 and (s.stride(0) * fmt_bytes) % (4 * fmt_bytes)) \
             or s.data_ptr() % (4 * fmt_bytes):
@@ -53,9 +61,13 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
     N, Kh2 = bt_pk.shape
     K = Kh * 2
     assert Kh == Kh2 and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
-    C.require_device(a_pk, bt_pk, a_scale, b_scale)
     assert a_scale.dtype == b_scale.dtype and a_scale.dim() == b_scale.dim(), \
         "a_scale and b_scale must share a format"
+    if a_scale.dim() == 2:
+        for s, rows in ((a_scale, M), (b_scale, N)):
+            if tuple(s.shape) != (rows, K // 32):
+                raise AssertionError(f"scale must be [{rows}, {K // 32}] (rows, K//32), got {list(s.shape)}")
+    C.require_device(a_pk, bt_pk, a_scale, b_scale)
     a_pk, bt_pk = _rows16(a_pk), _rows16(bt_pk)
     c = torch.empty((M, N), device=a_pk.device, dtype=out_dtype)
     if M == 0 or N == 0:
@@ -79,26 +91,45 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
     return c
 
 
+_ACT = {torch.bfloat16: C.BF16, torch.float32: C.F32, torch.float16: C.F16}
+
+
 def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
-    """Weight-only GEMM: a [M,K] bf16 activations x MXFP4 weight w_pk [N,K//2]
-    with w_scale [N,K//32] (fp32 powers of two or E8M0).  Returns
-    a @ deq(W).T [M, N] in out_dtype, fp32 accumulate."""
+    """Weight-only GEMM: activations a [M,K] x MXFP4 weight w_pk [N,K//2] with
+    w_scale [N,K//32] (fp32 powers of two or E8M0).  Returns a @ deq(W).T
+    [M, N] in out_dtype, fp32 accumulate.
+
+    bf16 activations run the bf16 MFMA kernels directly.  fp32 and fp16
+    activations are not narrowed: each is split exactly into bf16 terms
+    (lsmx_gemm_wonly_f4), so an fp32 X gives the arithmetic of an fp32
+    matmul (BASELINE cfg1's Y = X @ dequantize_mxfp4(W)^T)."""
     M, K = a.shape
     N, Kh = w_pk.shape
     assert K == 2 * Kh and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
+    if w_scale.dim() != 2 or tuple(w_scale.shape) != (N, K // 32):
+        raise AssertionError(f"scale must be [{N}, {K // 32}] (rows, K//32), got {list(w_scale.shape)}")
+    if a.dtype not in _ACT:
+        raise TypeError(f"activations must be bfloat16, float32 or float16, got {a.dtype}")
     C.require_device(a, w_pk, w_scale)
-    if a.dtype != torch.bfloat16:
-        a = a.to(torch.bfloat16)
     a = _rows16(a)
     w_pk = _rows16(w_pk)
     w_scale = _scales(w_scale, N, K // 32)
     c = torch.empty((M, N), device=a.device, dtype=out_dtype)
     if M == 0 or N == 0:
         return c
-    C.call("lsmx_gemm_bf16f4", a.data_ptr(), a.stride(0) if M > 1 else K, w_pk.data_ptr(),
+    C.call("lsmx_gemm_wonly_f4", a.data_ptr(), _ACT[a.dtype], a.stride(0) if M > 1 else K, w_pk.data_ptr(),
            w_pk.stride(0) if N > 1 else Kh, w_scale.data_ptr(), w_scale.stride(0) if N > 1 else K // 32,
            _fp4._scale_fmt(w_scale), c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
     return c
+
+
+def mxfp4_linear_w(a, w_pk, w_scale, out_dtype=None):
+    """Y = a @ deq(W)^T for an unquantized activation a [..., K] (any of
+    bf16 / fp32 / fp16) and a packed MXFP4 weight: the weight-only linear
+    forward, output in a's dtype unless out_dtype is given."""
+    K = a.shape[-1]
+    y = mxfp4_gemm_bf16(a.reshape(-1, K), w_pk, w_scale, out_dtype=out_dtype or a.dtype)
+    return y.reshape(*a.shape[:-1], w_pk.shape[0])
 
 
 def _e8m0_rows(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torch.Tensor:

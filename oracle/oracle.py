@@ -151,8 +151,10 @@ def scale_to_e8m0(scale: np.ndarray) -> np.ndarray:
 
 
 def e8m0_to_scale(e: np.ndarray) -> np.ndarray:
+    """E8M0 bytes -> fp32 2^(e-127): byte 0 is 2^-127 (a subnormal), 0xFF NaN."""
     e = np.asarray(e, dtype=np.uint8)
     out = (e.astype(np.uint32) << 23).view(np.float32).copy()
+    out[e == 0] = np.float32(2.0 ** -127)
     out[e == 0xFF] = np.nan
     return out
 

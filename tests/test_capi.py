@@ -187,3 +187,38 @@ def test_dense_python_api_asserts_then_refuses_cpu():
     f8 = torch.zeros(4, 64, dtype=torch.uint8).view(torch.float8_e4m3fn)
     with pytest.raises(AssertionError, match="K must be a multiple of 128"):
         mxfp4_gemm.mxfp4_gemm_fp8(f8, f8.t(), torch.ones(4, 2), torch.ones(2, 4))
+
+
+def test_gemm_leading_dimensions_bounded_for_32bit_offsets():
+    # 256 rows of codes or scales past a descriptor base must fit 32-bit offsets
+    big = 1 << 24
+    rc = _rc("lsmx_gemm_f4f4", FAKE, big, FAKE, 4, FAKE, 64, FAKE, 4, C.SCALE_E8M0, FAKE, C.BF16, 8, 8, 8, 128, None)
+    assert rc == C.ERR_SHAPE and "32-bit" in C.last_error()
+    rc = _rc("lsmx_gemm_f4f4", FAKE, 64, FAKE, 1 << 22, FAKE, 64, FAKE, 4, C.SCALE_F32, FAKE, C.BF16, 8, 8, 8, 128,
+             None)
+    assert rc == C.ERR_SHAPE and "32-bit" in C.last_error()
+    rc = _rc("lsmx_gemm_bf16f4", FAKE, 1 << 27, FAKE, 64, FAKE, 4, C.SCALE_E8M0, FAKE, C.BF16, 8, 8, 8, 128, None)
+    assert rc == C.ERR_SHAPE and "32-bit" in C.last_error()
+
+
+def test_weight_only_entry_point_validates_activation_type():
+    assert _rc("lsmx_gemm_wonly_f4", FAKE, 7, 128, FAKE, 64, FAKE, 4, C.SCALE_E8M0, FAKE, C.F32, 8, 8, 8, 128,
+               None) == C.ERR_DTYPE
+    # fp32 rows of 100 elements are not 16-byte multiples
+    assert _rc("lsmx_gemm_wonly_f4", FAKE, C.F32, 130, FAKE, 64, FAKE, 4, C.SCALE_E8M0, FAKE, C.F32, 8, 8, 8, 128,
+               None) == C.ERR_ALIGN
+
+
+def test_scale_shapes_are_checked_before_any_device_work():
+    from lockstep_amd import dual_gemm, mxfp4_gemm
+    pk = torch.zeros((64, 64), dtype=torch.uint8)
+    good = torch.full((64, 4), 127, dtype=torch.uint8)
+    with pytest.raises(AssertionError, match="scale must be"):
+        mxfp4_gemm.mxfp4_gemm_packed(pk, pk, good[:32], good)
+    with pytest.raises(AssertionError, match="scale must be"):
+        mxfp4_gemm.mxfp4_gemm_bf16(torch.zeros((8, 128), dtype=torch.bfloat16), pk, good[:, :3])
+    a = torch.zeros((8, 128), dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="scale must be"):
+        dual_gemm.dual_mxfp4(a, a, pk, good.t())
+    with pytest.raises(TypeError, match="activations must be"):
+        mxfp4_gemm.mxfp4_gemm_bf16(torch.zeros((8, 128), dtype=torch.float64), pk, good)

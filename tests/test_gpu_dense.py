@@ -90,8 +90,10 @@ def test_ring_kernel_walks_several_tiles_per_workgroup(dev, mods, dt):
 @pytest.mark.parametrize("dt", DTYPES, ids=str)
 @pytest.mark.parametrize("shared", [False, True], ids=["b1!=b2", "shared-W"])
 def test_dual_packed_is_concatenated_k_gemm(dev, mods, dt, shared):
-    """One accumulator: acc = A1.B1 + A2.B2, the GEMM over the K-concatenation
-    [A1 | A2] . [B1; B2] (dual_gemm.py:42-72); exact on the integer grid."""
+    """One accumulator: acc = A1.B1 + A2.B2 (dual_gemm.py:42-72), equal to the
+    GEMM over the K-concatenation [A1 | A2] . [B1; B2] on the integer grid,
+    where every order of the additions is exact (the order itself is pinned
+    by tests/test_gpu_scales.py)."""
     dg = mods[0]
     rng = np.random.default_rng(5)
     M, N, K = 160, 200, 320
