@@ -1,22 +1,34 @@
 """Benchmark of the MI355X MXFP4 hot path (one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--suite PATH]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--suite PATH]
 
-Workload (BASELINE cfg4, the config the headline metric is quoted on):
+Headline workload (BASELINE cfg4, the config the metric is quoted on):
 A, B fp32 [8192, 8192] = 0.05 * Student-t(3), resident in HBM.  One step =
-quantize A along K (fused quantize+pack, E8M0 scales) + quantize B along K +
-f4 x f4 block-scaled GEMM (v_mfma_scale_f32_32x32x64_f8f6f4), bf16 out.
+quantize A along K (fused quantize+pack, K-major E8M0 scales) + quantize B
+along K + f4 x f4 block-scaled GEMM (v_mfma_scale_f32_32x32x64_f8f6f4), bf16
+out.  `value` is 2*M*N*K / step time over the timed region.
 
-`value` is the whole step's rate, 2*M*N*K / step time.  `gemm` and `quantize`
-give per-kernel rates from HIP events recorded on the stream the kernels run
-on, and `roofline` prices the dominant kernel (the GEMM) against MI355X's
-dense FP4 MFMA peak; `roofline_quantize` prices the quantizer against HBM.
-`cpu_baseline` times the CPU oracle (a restatement of the reference's CPU
-path: fp4.py quantizer + dequantize-then-fp32-matmul, the fake-quant branch
-of fp4_linear.py:40) on this host, on rank 0 only.
+Alongside it:
+  gemm / quantize     per-kernel rates from HIP events recorded on the
+                      stream the kernels run on (median of isolated launches)
+  gemm_sustained      the GEMM back to back (events around a loop of
+                      launches): the rate under sustained load, when the
+                      clock has dropped
+  roofline            the dominant kernel (the GEMM) against MI355X's dense
+                      FP4 MFMA peak, plus the fraction at the clock rocprof
+                      measured for this kernel (GRBM_GUI_ACTIVE / duration,
+                      profiles/clock.json)
+  roofline_quantize   the quantizer against HBM
+  configs             every BASELINE config (cfg1 ... cfg5) with its rate,
+                      the roofline of its dominant kernel and its own
+                      cpu_baseline
+  cpu_baseline        the CPU oracle (a restatement of the reference's CPU
+                      path: fp4.py quantizer + dequantize-then-fp32-matmul,
+                      the fake-quant branch of fp4_linear.py:40) on this
+                      host's cores, median of 3 runs after a warm-up
 
---suite PATH also measures the other BASELINE configs (dual-batch cfg2, the
-weight-only cfg3 sweep) and writes one JSON line each to PATH.
+--suite PATH also measures the reference bench's own 4096^3 rows (its
+mxfp4 and dual GEMM throughput rows) and writes one JSON line each to PATH.
 """
 
 from __future__ import annotations
@@ -31,22 +43,22 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-PEAK_FP4_TFLOPS = 10100.0     # MI355X dense MXFP4 MFMA
+PEAK_FP4_TFLOPS = 10100.0     # MI355X dense MXFP4 MFMA (2.4 GHz)
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+NOMINAL_GHZ = 2.4
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    # ~10 ms of untimed steps: the first few milliseconds of load after idle
-    # run ~5% slower while the clocks settle
     p.add_argument("--warmup", type=int, default=30)
     p.add_argument("--size", type=int, default=8192)
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--suite", default=None, help="also bench cfg2/cfg3, one JSON line each to this file")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    p.add_argument("--no-configs", action="store_true", help="headline (cfg4) only")
+    p.add_argument("--suite", default=None, help="also bench the reference bench's rows, JSON lines to this file")
     p.add_argument("--calib", action="store_true",
                    help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
     return p.parse_args()
@@ -65,72 +77,161 @@ def t3(n, gen, dev, torch):
     return (z / torch.sqrt(chi / 3.0) * 0.05).contiguous()
 
 
+def _profile_json(name):
+    f = ROOT / "profiles" / name
+    if not f.exists():
+        return {}
+    try:
+        return json.loads(f.read_text())
+    except (ValueError, OSError):
+        return {}
+
+
 def traffic_from_profiles(kernel_prefix: str):
     """HBM bytes per launch from committed rocprofv3 --pmc summaries, if any."""
-    f = ROOT / "profiles" / "traffic.json"
-    if not f.exists():
-        return None
-    try:
-        data = json.loads(f.read_text())
-        return data.get(kernel_prefix, {}).get("bytes_per_launch")
-    except (ValueError, OSError):
-        return None
+    return _profile_json("traffic.json").get(kernel_prefix, {}).get("bytes_per_launch")
 
 
-def cpu_baseline(n: int):
-    """Time the CPU oracle on the cfg4 workload: quantize A and B (C oracle,
-    OpenMP), dequantize, fp32 A @ B^T (numpy/OpenBLAS) -- the fake-quant CPU
-    path of fp4_linear.py:40 restated.  Rate = 2*R*n*n / time for R rows of C
-    (R = n unless that would exceed ~30 s)."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def clock_from_profiles(kernel_prefix: str):
+    """Average graphics clock (GHz) rocprofv3 measured over this kernel's
+    launches (GRBM_GUI_ACTIVE cycles per XCD / duration), if committed."""
+    return _profile_json("clock.json").get(kernel_prefix, {}).get("ghz")
 
-    from oracle import oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    O.lib()
-    rng = np.random.default_rng(4001)
-    R = n
-    a = (rng.standard_t(3, (R, n)) * 0.05).astype(np.float32)
-    b = (rng.standard_t(3, (n, n)) * 0.05).astype(np.float32)
-    with threadpool_limits(limits=cores):
-        times = []
-        for _ in range(2):
-            t0 = time.perf_counter()
-            ac, as_ = O.quantize_mxfp4(a)
-            bc, bs_ = O.quantize_mxfp4(b)
-            A = O.dequantize_mxfp4(ac, as_)
-            B = O.dequantize_mxfp4(bc, bs_)
-            C = A @ B.T
-            times.append(time.perf_counter() - t0)
-            del C, A, B
-    t = min(times)
-    model = ""
+def roofline(bound, kernel, achieved, peak, unit, traffic=None, clock_ghz=None):
+    r = {"bound": bound, "kernel": kernel, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+         "frac": round(achieved / peak, 4), "traffic": traffic}
+    if clock_ghz:
+        r["measured_clock_ghz"] = clock_ghz
+        r["frac_at_measured_clock"] = round(achieved / (peak * clock_ghz / NOMINAL_GHZ), 4)
+    return r
+
+
+# ----------------------------------------------------------------- CPU legs
+def cpu_cores():
+    """Threads for the CPU legs: this process's CPUs, capped at the CPU share
+    the host gives one GPU's job when it says so (OMP_NUM_THREADS)."""
+    avail = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS")
+    return (min(avail, int(share)) if share and share.isdigit() and int(share) > 0 else avail), avail
+
+
+def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
-        pass
-    return {"value": round(2.0 * R * n * n / t / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "cpu_model": model,
-            "sample": f"full cfg4 ({R}x{n}x{n}): quantize A and B with the C oracle (OpenMP, "
-                      f"{O.num_threads()} threads), dequantize, fp32 A@B^T (numpy/OpenBLAS, {cores} threads); "
-                      f"{t:.2f} s per step, best of 2",
-            "seconds": round(t, 3)}
+        return ""
 
 
+def time_cpu(fn, runs=3):
+    """Median wall time of `runs` calls after one warm-up call."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return median(ts)
+
+
+def cpu_leg(fn, work, unit, sample):
+    """Time the CPU restatement of a config on this host (oracle C quantizer
+    with OpenMP, numpy/OpenBLAS fp32 matmul) and rate it in `unit`."""
+    from threadpoolctl import threadpool_limits
+    from oracle import oracle as O
+    cores, avail = cpu_cores()
+    O.lib()
+    with threadpool_limits(limits=cores):
+        t = time_cpu(fn)
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    return {"value": round(work / t / scale, 4), "unit": unit, "cores": cores, "host_cpus_visible": avail,
+            "kind": "port", "cpu_model": cpu_model(), "sample": sample + f"; median of 3 after a warm-up",
+            "seconds": round(t, 4)}
+
+
+def _bf16_to_f32_np(t):
+    """bf16 torch tensor -> fp32 numpy (exact)."""
+    import numpy as np
+    import torch
+    return (t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def cpu_quant_deq(O, x, dtype=None):
+    """fp4.py:57-78 on the CPU: quantize along the last axis, dequantize."""
+    c, s = O.quantize_mxfp4(x, 32, dtype)
+    return O.dequantize_mxfp4(c, s)
+
+
+# ----------------------------------------------------------------- GPU timing
+def _time_events(fn, reps=20, warm=3):
+    """Median event time of fn: a spin kernel ahead of each call keeps the GPU
+    busy while the host enqueues, so no interval includes host launch time."""
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return median(ts)
+
+
+def _time_ops(ops, reps=10, warm=2):
+    """Per-op median event times of a sequence of ops run as one step."""
+    import torch
+    for _ in range(warm):
+        for _, f in ops:
+            f()
+    torch.cuda.synchronize()
+    per = {name: [] for name, _ in ops}
+    tot = []
+    for _ in range(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(ops) + 1)]
+        torch.cuda._sleep(2_000_000)
+        ev[0].record()
+        for i, (_, f) in enumerate(ops):
+            f()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        for i, (name, _) in enumerate(ops):
+            per[name].append(ev[i].elapsed_time(ev[i + 1]))
+        tot.append(ev[0].elapsed_time(ev[-1]))
+    return {k: median(v) for k, v in per.items()}, median(tot)
+
+
+def _time_loop(fn, n=50):
+    """Average time of n back-to-back calls (events around the loop)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+# ----------------------------------------------------------------- main
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "this build has no multi-GPU path", file=sys.stderr)
+              "this build has no multi-GPU path: every GPU box here has one GPU", file=sys.stderr)
         sys.exit(2)
 
     import torch
 
-    from lockstep_amd import fp4, mxfp4_gemm
-    from lockstep_amd import _capi
+    from lockstep_amd import _capi, fp4, mxfp4_gemm
 
     _capi.load()
     dev = torch.device("cuda", 0)
@@ -167,9 +268,6 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
 
-    # per-kernel durations from HIP events on the kernels' stream; a spin
-    # kernel ahead of each step keeps the GPU busy while the host enqueues,
-    # so no event interval includes host launch time
     qa, qb, gm = [], [], []
     for _ in range(max(args.steps, 5)):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
@@ -181,12 +279,18 @@ def main():
         gm.append(ev[2].elapsed_time(ev[3]))
     gemm_ms = median(gm)
     quant_ms = median(qa + qb)
+    apk, ae8 = fp4.quantize_pack_mxfp4(A, scale_layout="kmajor")
+    bpk, be8 = fp4.quantize_pack_mxfp4(B, scale_layout="kmajor")
+    sustained_ms = _time_loop(lambda: mxfp4_gemm.mxfp4_gemm_packed(apk, bpk, ae8, be8), n=50)
+    del apk, bpk
 
     flop = 2.0 * n * n * n
     gemm_tflops = flop / (gemm_ms * 1e-3) / 1e12
+    sus_tflops = flop / (sustained_ms * 1e-3) / 1e12
     q_bytes = n * n * (4 + 0.5 + 1.0 / 32)            # fp32 in, packed nibbles + E8M0 out
     quant_gbs = q_bytes / (quant_ms * 1e-3) / 1e9
     value = flop / (ms_per_step * 1e-3) / 1e12
+    gemm_clock = clock_from_profiles("gemm_f4f4_kernel")
 
     out = {
         "metric": f"MXFP4 GEMM TFLOPS at {n}^3 (cfg4: on-the-fly quantize of A and B + f4xf4 GEMM)",
@@ -206,19 +310,16 @@ def main():
         "device": props.name,
         "gemm": {"ms": round(gemm_ms, 4), "tflops": round(gemm_tflops, 1),
                  "frac_fp4_peak": round(gemm_tflops / PEAK_FP4_TFLOPS, 4)},
+        "gemm_sustained": {"ms": round(sustained_ms, 4), "tflops": round(sus_tflops, 1),
+                           "frac_fp4_peak": round(sus_tflops / PEAK_FP4_TFLOPS, 4),
+                           "how": "50 GEMMs back to back, events around the loop"},
         "quantize": {"ms_per_operand": round(quant_ms, 4), "gbs": round(quant_gbs, 1),
-                     "frac_hbm": round(quant_gbs / PEAK_HBM_GBS, 4),
-                     "bytes_per_launch": int(q_bytes)},
-        "roofline": {"bound": "mfma", "kernel": "gemm_f4f4_kernel", "achieved": round(gemm_tflops, 1),
-                     "peak": PEAK_FP4_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_FP4_TFLOPS, 4),
-                     "traffic": traffic_from_profiles("gemm_f4f4_kernel")},
-        "roofline_quantize": {"bound": "hbm", "kernel": "quantize_rows_kernel", "achieved": round(quant_gbs, 1),
-                              "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(quant_gbs / PEAK_HBM_GBS, 4),
-                              "traffic": traffic_from_profiles("quantize_rows_kernel")},
+                     "frac_hbm": round(quant_gbs / PEAK_HBM_GBS, 4), "bytes_per_launch": int(q_bytes)},
+        "roofline": roofline("mfma", "gemm_f4f4_kernel", gemm_tflops, PEAK_FP4_TFLOPS, "TFLOP/s",
+                             traffic_from_profiles("gemm_f4f4_kernel"), gemm_clock),
+        "roofline_quantize": roofline("hbm", "quantize_rows_kernel", quant_gbs, PEAK_HBM_GBS, "GB/s",
+                                      traffic_from_profiles("quantize_rows_kernel")),
     }
-    if args.suite:
-        run_suite(args.suite, torch, dev)
     if args.calib:
         # plain copy of known size: 256 MiB read + 256 MiB written per launch
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).uniform_()
@@ -227,61 +328,217 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         out["calib_copy_bytes"] = src.numel() * 4
+        del src, dst
+    del A, B
+    torch.cuda.empty_cache()
+
+    cfg4_cpu = None
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(n)
+        cfg4_cpu = cpu_cfg4(n)
+        out["cpu_baseline"] = cfg4_cpu
+    if not args.no_configs:
+        out["configs"] = run_configs(torch, dev, cpu=not args.no_cpu)
+        out["configs"].insert(len(out["configs"]) - 1, {
+            "workload": "cfg4 fully-FP4 GEMM 8192^3, both operands quantized on the fly (the headline)",
+            "ms": round(ms_per_step, 4), "rate": round(value, 1), "unit": "TFLOP/s",
+            "roofline": out["roofline"], "roofline_quantize": out["roofline_quantize"],
+            "cpu_baseline": cfg4_cpu})
+    if args.suite:
+        lines = bench_reference_rows(torch, dev)
+        with open(args.suite, "w") as f:
+            for ln in lines:
+                f.write(json.dumps(ln) + "\n")
     print(json.dumps(out), flush=True)
 
 
-def _time_events(fn, reps=20, warm=3):
-    import torch
-    for _ in range(warm):
-        fn()
-    torch.cuda.synchronize()
-    ts = []
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(2_000_000)   # the host enqueues fn while the GPU spins
-        e0.record()
-        fn()
-        e1.record()
-        torch.cuda.synchronize()
-        ts.append(e0.elapsed_time(e1))
-    return median(ts)
+def cpu_cfg4(n):
+    """cfg4 on the CPU: quantize A and B (C oracle), dequantize, fp32 A @ B^T."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(4001)
+    a = (rng.standard_t(3, (n, n)) * 0.05).astype(np.float32)
+    b = (rng.standard_t(3, (n, n)) * 0.05).astype(np.float32)
+
+    def run():
+        cpu_quant_deq(O, a) @ cpu_quant_deq(O, b).T
+    return cpu_leg(run, 2.0 * n ** 3, "TFLOP/s",
+                   f"full cfg4 ({n}x{n}x{n}): quantize A and B (C oracle, OpenMP), dequantize, fp32 A@B^T (numpy)")
 
 
-def run_suite(path, torch, dev):
-    """cfg2 (dual-batch) and cfg3 (weight-only sweep), one JSON line each."""
+# ----------------------------------------------------------------- configs
+def run_configs(torch, dev, cpu=True):
+    """cfg1, cfg2, cfg3 (M sweep) and cfg5 at their BASELINE shapes: GPU rate,
+    roofline of the dominant kernel, CPU restatement timed beside it."""
+    import numpy as np
+
     from lockstep_amd import dual_gemm, fp4, mxfp4_gemm
-    lines = []
+    from oracle import gen
+    rows = []
+
+    # cfg1: X[256,1024] fp32, W[1024,1024] ~ N(0, 0.02); quantize W, Y = X @ deq(W)^T fp32
+    x1 = gen.normal(1001, (256, 1024))
+    w1 = gen.normal(1002, (1024, 1024), std=0.02)
+    xt, wt = torch.from_numpy(x1).to(dev), torch.from_numpy(w1).to(dev)
+    state = {}
+
+    def c1_quant():
+        state["w"] = fp4.quantize_pack_mxfp4(wt)
+
+    def c1_gemm():
+        mxfp4_gemm.mxfp4_gemm_bf16(xt, state["w"][0], state["w"][1], out_dtype=torch.float32)
+    per, tot = _time_ops([("quantize", c1_quant), ("gemm", c1_gemm)], reps=20)
+    fl1 = 2.0 * 256 * 1024 * 1024
+    qb1 = 1024 * 1024 * (4 + 0.5 + 1 / 32)
+    r = {"workload": "cfg1 fp4_linear layer: quantize W[1024,1024] + Y = X[256,1024] fp32 @ deq(W)^T, fp32 out",
+         "ms": round(tot, 4), "rate": round(fl1 / tot / 1e9, 2), "unit": "TFLOP/s",
+         "roofline": roofline("mfma", "gemm_xf4_kernel (fp32 X as 3 exact bf16 terms)", fl1 / per["gemm"] / 1e9,
+                              PEAK_BF16_TFLOPS, "TFLOP/s"),
+         "roofline_quantize": roofline("hbm", "quantize_rows_kernel", qb1 / per["quantize"] / 1e6, PEAK_HBM_GBS,
+                                       "GB/s"),
+         "note": "a correctness config: 0.5 GFLOP per step does not fill the GPU; the fp32 activations cost "
+                 "three bf16 MFMAs per product"}
+    if cpu:
+        from oracle import oracle as O
+
+        def run1():
+            x1 @ cpu_quant_deq(O, w1).T
+        r["cpu_baseline"] = cpu_leg(run1, fl1, "TFLOP/s", "full cfg1: quantize W (C oracle), dequantize, "
+                                                          "fp32 X @ W^T (numpy)")
+    rows.append(r)
+
+    # cfg2: A0, A1 bf16 [2048, 4096], W [4096, 4096] MXFP4, one dual launch
     g = torch.Generator(device=dev).manual_seed(2001)
-    # cfg2: A0, A1 bf16 [2048, 4096], W [4096, 4096] MXFP4
     a0 = torch.randn((2048, 4096), device=dev, generator=g).to(torch.bfloat16)
     a1 = torch.randn((2048, 4096), device=dev, generator=g).to(torch.bfloat16)
-    w = torch.randn((4096, 4096), device=dev, generator=g) * 0.02
-    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    w2 = torch.randn((4096, 4096), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w2)
     ms = _time_events(lambda: dual_gemm.dual_mxfp4(a0, a1, wpk, we8))
-    fl = 2.0 * 2 * 2048 * 4096 * 4096
-    lines.append({"config": "cfg2 dual-batch bf16 x mxfp4, 2x[2048,4096] . [4096,4096]^T", "ms": ms,
-                  "tflops": fl / ms / 1e9, "frac_bf16_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS})
     ms2 = _time_events(lambda: (mxfp4_gemm.mxfp4_gemm_bf16(a0, wpk, we8), mxfp4_gemm.mxfp4_gemm_bf16(a1, wpk, we8)))
-    lines[-1]["two_launch_ms"] = ms2
+    fl2 = 2.0 * 2 * 2048 * 4096 * 4096
+    r = {"workload": "cfg2 dual-batch bf16 x MXFP4: 2 x [2048,4096] . W[4096,4096]^T, one launch, bf16 out",
+         "ms": round(ms, 4), "rate": round(fl2 / ms / 1e9, 1), "unit": "TFLOP/s",
+         "roofline": roofline("mfma", "gemm_bf16f4_ring_kernel<2,...> (dual)", fl2 / ms / 1e9, PEAK_BF16_TFLOPS,
+                              "TFLOP/s", traffic_from_profiles("gemm_bf16f4_ring_kernel<2")),
+         "two_launch_ms": round(ms2, 4)}
+    if cpu:
+        from oracle import oracle as O
+        wc, ws = O.quantize_mxfp4(w2.cpu().numpy())
+        A0, A1 = _bf16_to_f32_np(a0), _bf16_to_f32_np(a1)
+
+        def run2():
+            W = O.dequantize_mxfp4(wc, ws)
+            A0 @ W.T
+            A1 @ W.T
+        r["cpu_baseline"] = cpu_leg(run2, fl2, "TFLOP/s", "full cfg2: dequantize W (C oracle), two fp32 "
+                                                          "matmuls (numpy)")
+    rows.append(r)
+    del a0, a1, w2, wpk, we8
+
     # cfg3: W [14336, 4096], M sweep
     w3 = torch.randn((14336, 4096), device=dev, generator=g) * 0.02
     w3pk, w3e8 = fp4.quantize_pack_mxfp4(w3)
+    w3c = w3s = None
+    if cpu:
+        from oracle import oracle as O
+        w3c, w3s = O.quantize_mxfp4(w3.cpu().numpy())
     for M in (1, 16, 128, 1024, 8192):
         a = torch.randn((M, 4096), device=dev, generator=g).to(torch.bfloat16)
         ms = _time_events(lambda: mxfp4_gemm.mxfp4_gemm_bf16(a, w3pk, w3e8))
         fl = 2.0 * M * 14336 * 4096
         by = 14336 * 4096 * (0.5 + 1 / 32) + 2 * M * 4096 + 2 * M * 14336
-        lines.append({"config": f"cfg3 weight-only bf16 x mxfp4, M={M}, N=14336, K=4096", "ms": ms,
-                      "tflops": fl / ms / 1e9, "gbs": by / ms / 1e6,
-                      "frac_bf16_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS, "frac_hbm": by / ms / 1e6 / PEAK_HBM_GBS})
-    lines.append(bench_cfg5(torch, dev))
-    lines += bench_reference_rows(torch, dev)
-    with open(path, "w") as f:
-        for ln in lines:
-            f.write(json.dumps(ln) + "\n")
-            print(json.dumps(ln), file=sys.stderr, flush=True)
+        kern = ("gemv_bf16f4_kernel" if M <= 2 else "gemm_bf16f4_skinny_kernel" if M <= 32 else
+                "gemm_bf16f4_ring_kernel")
+        if M <= 16:
+            rl = roofline("hbm", kern, by / ms / 1e6, PEAK_HBM_GBS, "GB/s")
+        else:
+            rl = roofline("mfma", kern, fl / ms / 1e9, PEAK_BF16_TFLOPS, "TFLOP/s")
+        r = {"workload": f"cfg3 weight-only bf16 x MXFP4, M={M}, N=14336, K=4096, bf16 out", "ms": round(ms, 4),
+             "rate": round(fl / ms / 1e9, 2), "unit": "TFLOP/s", "gbs": round(by / ms / 1e6, 1), "roofline": rl}
+        if cpu:
+            A = _bf16_to_f32_np(a)
+
+            def run3(A=A):
+                A @ O.dequantize_mxfp4(w3c, w3s).T
+            r["cpu_baseline"] = cpu_leg(run3, fl, "TFLOP/s", f"full cfg3 M={M}: dequantize W (C oracle), fp32 "
+                                                             "A @ W^T (numpy)")
+        rows.append(r)
+        del a
+    del w3, w3pk, w3e8, w3c, w3s
+    torch.cuda.empty_cache()
+
+    rows.append(bench_cfg5(torch, dev, cpu))
+    return rows
+
+
+def bench_cfg5(torch, dev, cpu, T=8192, H=2048, F=8192):
+    """cfg5: one MLP block (fc H->F, out F->H) forward + MXFP4 backward, the
+    12 quantizations and 6 f4 x f4 GEMMs of fp4_linear.mxfp4_backward and
+    _forward_hip, timed op by op inside one step."""
+    import numpy as np
+
+    from lockstep_amd import fp4, mxfp4_gemm
+    g = torch.Generator(device=dev).manual_seed(5001)
+    x = torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn((F, H), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((H, F), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    dy = torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16)
+    s = {}
+    qr = lambda t: fp4.quantize_pack_mxfp4(t, scale_layout="kmajor")   # noqa: E731
+    qc = lambda t: fp4.quantize_mxfp4_t(t, scale_layout="kmajor")      # noqa: E731
+    mm = lambda a, b: mxfp4_gemm.mxfp4_gemm_packed(a[0], b[0], a[1], b[1], out_dtype=torch.bfloat16)  # noqa: E731
+
+    def op(name, fn):
+        return (name, fn)
+    ops = [
+        op("q_rows x", lambda: s.__setitem__("qx", qr(x))), op("q_rows w1", lambda: s.__setitem__("qw1", qr(w1))),
+        op("gemm fc fwd", lambda: s.__setitem__("h", mm(s["qx"], s["qw1"]))),
+        op("q_rows h", lambda: s.__setitem__("qh", qr(s["h"]))), op("q_rows w2", lambda: s.__setitem__("qw2", qr(w2))),
+        op("gemm out fwd", lambda: s.__setitem__("y", mm(s["qh"], s["qw2"]))),
+        op("q_rows dy", lambda: s.__setitem__("qdy", qr(dy))), op("q_cols w2", lambda: s.__setitem__("qw2t", qc(w2))),
+        op("gemm out dgrad", lambda: s.__setitem__("dh", mm(s["qdy"], s["qw2t"]))),
+        op("q_cols dy", lambda: s.__setitem__("qdyt", qc(dy))), op("q_cols h", lambda: s.__setitem__("qht", qc(s["h"]))),
+        op("gemm out wgrad", lambda: s.__setitem__("dw2", mm(s["qdyt"], s["qht"]))),
+        op("q_rows dh", lambda: s.__setitem__("qdh", qr(s["dh"]))),
+        op("q_cols w1", lambda: s.__setitem__("qw1t", qc(w1))),
+        op("gemm fc dgrad", lambda: s.__setitem__("dx", mm(s["qdh"], s["qw1t"]))),
+        op("q_cols dh", lambda: s.__setitem__("qdht", qc(s["dh"]))),
+        op("q_cols x", lambda: s.__setitem__("qxt", qc(x))),
+        op("gemm fc wgrad", lambda: s.__setitem__("dw1", mm(s["qdht"], s["qxt"]))),
+    ]
+    per, tot = _time_ops(ops, reps=10)
+    gemm_ms = sum(v for k, v in per.items() if k.startswith("gemm"))
+    q_ms = sum(v for k, v in per.items() if k.startswith("q_"))
+    fl = 6 * 2.0 * T * F * H
+    # bytes per element quantized: 2 (bf16 in) + 0.5 + 1/32 out; operand sizes
+    elems = {"x": T * H, "w1": F * H, "h": T * F, "w2": H * F, "dy": T * H, "dh": T * F}
+    qbytes = sum(elems[k.split()[-1]] for k in per if k.startswith("q_")) * (2 + 0.5 + 1 / 32)
+    r = {"workload": f"cfg5 MLP block fwd + MXFP4 bwd (tokens={T}, hidden={H}, ffn={F}, bf16): 12 quantizations "
+                     "+ 6 f4 x f4 GEMMs", "ms": round(tot, 4), "rate": round(fl / tot / 1e9, 1), "unit": "TFLOP/s",
+         "gemm_ms": round(gemm_ms, 4), "quantize_ms": round(q_ms, 4),
+         "roofline": roofline("mfma", "gemm_f4f4_kernel (6 launches)", fl / gemm_ms / 1e9, PEAK_FP4_TFLOPS,
+                              "TFLOP/s"),
+         "roofline_quantize": roofline("hbm", "quantize_rows/cols_kernel (12 launches)", qbytes / q_ms / 1e6,
+                                       PEAK_HBM_GBS, "GB/s"),
+         "ops_ms": {k: round(v, 4) for k, v in per.items()}}
+    if cpu:
+        from oracle import oracle as O
+        bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)   # noqa: E731
+        X, W1, W2, DY = (bits(t) for t in (x, w1, w2, dy))
+        hf = _bf16_to_f32_np(s["h"])
+        dhf = _bf16_to_f32_np(s["dh"])
+
+        def run5():
+            qd = lambda a, d=None: cpu_quant_deq(O, a, d)   # noqa: E731
+            qd(X, "bf16") @ qd(W1, "bf16").T                              # fc fwd
+            qd(hf) @ qd(W2, "bf16").T                                     # out fwd
+            qd(DY, "bf16") @ qd(np.ascontiguousarray(W2.T), "bf16").T     # out dgrad
+            qd(np.ascontiguousarray(DY.T), "bf16") @ qd(np.ascontiguousarray(hf.T)).T   # out wgrad
+            qd(dhf) @ qd(np.ascontiguousarray(W1.T), "bf16").T            # fc dgrad
+            qd(np.ascontiguousarray(dhf.T)) @ qd(np.ascontiguousarray(X.T), "bf16").T   # fc wgrad
+        r["cpu_baseline"] = cpu_leg(run5, fl, "TFLOP/s", "full cfg5: 12 quantizations (C oracle, transposes by "
+                                                         "numpy), dequantize, 6 fp32 matmuls (numpy)")
+    del s
+    return r
 
 
 def bench_reference_rows(torch, dev, n=4096):
@@ -354,29 +611,6 @@ def bench_reference_rows(torch, dev, n=4096):
     rows.append({"config": "ref-bench fp4 -> e4m3 expansion, 64 Mi words (512 Mi codes)", "ms": ms,
                  "gbs": by / ms / 1e6, "frac_hbm": by / ms / 1e6 / PEAK_HBM_GBS})
     return rows
-
-
-def bench_cfg5(torch, dev, T=8192, H=2048, F=8192):
-    """cfg5: one MLP block (fc H->F, out F->H) forward + MXFP4 backward.
-    Per linear: quantize X and W along K + GEMM (fprop), dY along N and W
-    along its columns + GEMM (dgrad), dY and X along T + GEMM (wgrad)."""
-    from lockstep_amd import fp4_linear as fl
-    g = torch.Generator(device=dev).manual_seed(5001)
-    x = torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16)
-    w1 = (torch.randn((F, H), device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    w2 = (torch.randn((H, F), device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    dy = torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16)
-
-    def step():
-        h = fl._forward_hip(x, w1)                 # [T, F]
-        fl._forward_hip(h, w2)                     # [T, H]
-        dh, _ = fl.mxfp4_backward(dy, h, w2)       # dgrad + wgrad of out
-        fl.mxfp4_backward(dh, x, w1)               # dgrad + wgrad of fc
-    ms = _time_events(step, reps=10, warm=2)
-    fl_ = 6 * 2.0 * T * F * H
-    return {"config": f"cfg5 MLP block fwd + MXFP4 bwd, tokens={T} hidden={H} ffn={F}, bf16 in/out",
-            "ms": ms, "tflops": fl_ / ms / 1e9, "frac_fp4_peak": fl_ / ms / 1e9 / PEAK_FP4_TFLOPS,
-            "work": "12 quantizations + 6 f4xf4 GEMMs (1.649e12 FLOP)"}
 
 
 if __name__ == "__main__":
