@@ -471,9 +471,11 @@ def run_configs(torch, dev, cpu=True):
 
 
 def bench_cfg5(torch, dev, cpu, T=8192, H=2048, F=8192):
-    """cfg5: one MLP block (fc H->F, out F->H) forward + MXFP4 backward, the
-    12 quantizations and 6 f4 x f4 GEMMs of fp4_linear.mxfp4_backward and
-    _forward_hip, timed op by op inside one step."""
+    """cfg5: one MLP block (fc H->F, out F->H) forward + MXFP4 backward as
+    fp4_linear's quantized-backward autograd runs it, timed op by op inside
+    one step: each of x, w1, h, w2, dy, dh is quantized along both axes in
+    one pass (6 passes), then the 6 f4 x f4 GEMMs (fwd, dgrad, wgrad of each
+    linear, train_step.py:3-6)."""
     import numpy as np
 
     from lockstep_amd import fp4, mxfp4_gemm
@@ -483,41 +485,38 @@ def bench_cfg5(torch, dev, cpu, T=8192, H=2048, F=8192):
     w2 = (torch.randn((H, F), device=dev, generator=g) * 0.02).to(torch.bfloat16)
     dy = torch.randn((T, H), device=dev, generator=g).to(torch.bfloat16)
     s = {}
-    qr = lambda t: fp4.quantize_pack_mxfp4(t, scale_layout="kmajor")   # noqa: E731
-    qc = lambda t: fp4.quantize_mxfp4_t(t, scale_layout="kmajor")      # noqa: E731
-    mm = lambda a, b: mxfp4_gemm.mxfp4_gemm_packed(a[0], b[0], a[1], b[1], out_dtype=torch.bfloat16)  # noqa: E731
 
-    def op(name, fn):
-        return (name, fn)
+    def q2(name, t):
+        r = fp4.quantize_pack_mxfp4_2d(t, scale_layout="kmajor")
+        s[name + "_r"], s[name + "_c"] = (r[0], r[1]), (r[2], r[3])
+
+    mm = lambda a, b: mxfp4_gemm.mxfp4_gemm_packed(s[a][0], s[b][0], s[a][1], s[b][1],   # noqa: E731
+                                                   out_dtype=torch.bfloat16)
     ops = [
-        op("q_rows x", lambda: s.__setitem__("qx", qr(x))), op("q_rows w1", lambda: s.__setitem__("qw1", qr(w1))),
-        op("gemm fc fwd", lambda: s.__setitem__("h", mm(s["qx"], s["qw1"]))),
-        op("q_rows h", lambda: s.__setitem__("qh", qr(s["h"]))), op("q_rows w2", lambda: s.__setitem__("qw2", qr(w2))),
-        op("gemm out fwd", lambda: s.__setitem__("y", mm(s["qh"], s["qw2"]))),
-        op("q_rows dy", lambda: s.__setitem__("qdy", qr(dy))), op("q_cols w2", lambda: s.__setitem__("qw2t", qc(w2))),
-        op("gemm out dgrad", lambda: s.__setitem__("dh", mm(s["qdy"], s["qw2t"]))),
-        op("q_cols dy", lambda: s.__setitem__("qdyt", qc(dy))), op("q_cols h", lambda: s.__setitem__("qht", qc(s["h"]))),
-        op("gemm out wgrad", lambda: s.__setitem__("dw2", mm(s["qdyt"], s["qht"]))),
-        op("q_rows dh", lambda: s.__setitem__("qdh", qr(s["dh"]))),
-        op("q_cols w1", lambda: s.__setitem__("qw1t", qc(w1))),
-        op("gemm fc dgrad", lambda: s.__setitem__("dx", mm(s["qdh"], s["qw1t"]))),
-        op("q_cols dh", lambda: s.__setitem__("qdht", qc(s["dh"]))),
-        op("q_cols x", lambda: s.__setitem__("qxt", qc(x))),
-        op("gemm fc wgrad", lambda: s.__setitem__("dw1", mm(s["qdht"], s["qxt"]))),
+        ("q2 x", lambda: q2("x", x)), ("q2 w1", lambda: q2("w1", w1)),
+        ("gemm fc fwd", lambda: s.__setitem__("h", mm("x_r", "w1_r"))),
+        ("q2 h", lambda: q2("h", s["h"])), ("q2 w2", lambda: q2("w2", w2)),
+        ("gemm out fwd", lambda: s.__setitem__("y", mm("h_r", "w2_r"))),
+        ("q2 dy", lambda: q2("dy", dy)),
+        ("gemm out dgrad", lambda: s.__setitem__("dh", mm("dy_r", "w2_c"))),
+        ("gemm out wgrad", lambda: s.__setitem__("dw2", mm("dy_c", "h_c"))),
+        ("q2 dh", lambda: q2("dh", s["dh"])),
+        ("gemm fc dgrad", lambda: s.__setitem__("dx", mm("dh_r", "w1_c"))),
+        ("gemm fc wgrad", lambda: s.__setitem__("dw1", mm("dh_c", "x_c"))),
     ]
     per, tot = _time_ops(ops, reps=10)
     gemm_ms = sum(v for k, v in per.items() if k.startswith("gemm"))
-    q_ms = sum(v for k, v in per.items() if k.startswith("q_"))
+    q_ms = sum(v for k, v in per.items() if k.startswith("q2"))
     fl = 6 * 2.0 * T * F * H
-    # bytes per element quantized: 2 (bf16 in) + 0.5 + 1/32 out; operand sizes
+    # one pass per operand: 2 B read + 2 x (0.5 + 1/32) B written per element
     elems = {"x": T * H, "w1": F * H, "h": T * F, "w2": H * F, "dy": T * H, "dh": T * F}
-    qbytes = sum(elems[k.split()[-1]] for k in per if k.startswith("q_")) * (2 + 0.5 + 1 / 32)
-    r = {"workload": f"cfg5 MLP block fwd + MXFP4 bwd (tokens={T}, hidden={H}, ffn={F}, bf16): 12 quantizations "
-                     "+ 6 f4 x f4 GEMMs", "ms": round(tot, 4), "rate": round(fl / tot / 1e9, 1), "unit": "TFLOP/s",
-         "gemm_ms": round(gemm_ms, 4), "quantize_ms": round(q_ms, 4),
+    qbytes = sum(elems[k.split()[-1]] for k in per if k.startswith("q2")) * (2 + 2 * (0.5 + 1 / 32))
+    r = {"workload": f"cfg5 MLP block fwd + MXFP4 bwd (tokens={T}, hidden={H}, ffn={F}, bf16): 6 two-axis "
+                     "quantizations + 6 f4 x f4 GEMMs", "ms": round(tot, 4), "rate": round(fl / tot / 1e9, 1),
+         "unit": "TFLOP/s", "gemm_ms": round(gemm_ms, 4), "quantize_ms": round(q_ms, 4),
          "roofline": roofline("mfma", "gemm_f4f4_kernel (6 launches)", fl / gemm_ms / 1e9, PEAK_FP4_TFLOPS,
                               "TFLOP/s"),
-         "roofline_quantize": roofline("hbm", "quantize_rows/cols_kernel (12 launches)", qbytes / q_ms / 1e6,
+         "roofline_quantize": roofline("hbm", "quantize_2d_kernel (6 launches)", qbytes / q_ms / 1e6,
                                        PEAK_HBM_GBS, "GB/s"),
          "ops_ms": {k: round(v, 4) for k, v in per.items()}}
     if cpu:

@@ -91,6 +91,20 @@ int lsmx_quantize_mxfp4_t(const void *x, int x_dtype, int64_t K, int64_t cols, i
                           int block, void *codes, int codes_fmt, int64_t ld_codes, void *scale,
                           int scale_fmt, int64_t ld_scale, void *stream);
 
+/* Both of the above from ONE read of x: x[rows, cols] (bf16 or fp16,
+ * ldx >= cols) quantized along its rows -- codes_r [rows, ld_codes_r] packed,
+ * scale_r -- and along its columns -- codes_c [cols, ld_codes_c] packed,
+ * scale_c, laid out for x^T -- with E8M0 scales, row-major or K-major
+ * (scale_fmt; the same for both; K-major ld_scale_r >= rows, ld_scale_c >=
+ * cols).  Bit-identical to lsmx_quantize_mxfp4 and lsmx_quantize_mxfp4_t
+ * with block 32 (fp4.py:57-72 on x and on x.t().contiguous()).  A training
+ * step needs both forms of each operand it quantizes (train_step.py:3-6:
+ * X and W along K for fprop, W and dY along N for dgrad, dY and X along T
+ * for wgrad); this reads each once.  rows, cols % 128 == 0. */
+int lsmx_quantize_mxfp4_2d(const void *x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, uint8_t *codes_r,
+                           int64_t ld_codes_r, uint8_t *scale_r, int64_t ld_scale_r, uint8_t *codes_c,
+                           int64_t ld_codes_c, uint8_t *scale_c, int64_t ld_scale_c, int scale_fmt, void *stream);
+
 /* fp4.py:43-54 _round_to_e2m1: codes[i] = E2M1 code of q[i] (scale 1):
  * nearest, ties toward the smaller magnitude, clip at 6, sign copied, NaN -> 7.
  * q_dtype LSMX_F32 | LSMX_BF16 | LSMX_F16; n elements, one code byte each. */

@@ -33,6 +33,7 @@ SIGNATURES = {
     "lsmx_device_check": [],
     "lsmx_quantize_mxfp4": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
     "lsmx_quantize_mxfp4_t": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
+    "lsmx_quantize_mxfp4_2d": [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp],
     "lsmx_round_e2m1": [_vp, _int, _i64, _vp, _vp],
     "lsmx_pack_fp4": [_vp, _vp, _i64, _vp],
     "lsmx_unpack_fp4": [_vp, _vp, _i64, _vp],

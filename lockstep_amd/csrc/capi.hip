@@ -119,6 +119,33 @@ int lsmx_quantize_mxfp4_t(const void *x, int x_dtype, int64_t K, int64_t cols, i
                            ld_scale, stream, true);
 }
 
+int lsmx_quantize_mxfp4_2d(const void *x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, uint8_t *codes_r,
+                           int64_t ld_codes_r, uint8_t *scale_r, int64_t ld_scale_r, uint8_t *codes_c,
+                           int64_t ld_codes_c, uint8_t *scale_c, int64_t ld_scale_c, int scale_fmt, void *stream) {
+    const char *fn = "lsmx_quantize_mxfp4_2d";
+    if (!x || !codes_r || !scale_r || !codes_c || !scale_c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (x_dtype != LSMX_BF16 && x_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: x_dtype must be bf16 or fp16", fn);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_E8M0_KMAJOR)
+        return fail(LSMX_ERR_DTYPE, "%s: scale_fmt must be E8M0 or K-major E8M0", fn);
+    if (rows < 0 || cols < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (rows % 128 || cols % 128) return fail(LSMX_ERR_SHAPE, "%s: rows and cols must be multiples of 128", fn);
+    const bool km = scale_fmt == LSMX_SCALE_E8M0_KMAJOR;
+    if (ldx < cols || ld_codes_r < cols / 2 || ld_codes_c < rows / 2 || ld_scale_r < (km ? rows : cols / 32) ||
+        ld_scale_c < (km ? cols : rows / 32))
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (!aligned(x, 16) || (ldx * 2) % 16) return fail(LSMX_ERR_ALIGN, "%s: x rows must be 16-byte aligned", fn);
+    if (!aligned(codes_r, 4) || ld_codes_r % 4 || !aligned(codes_c, 16) || ld_codes_c % 16)
+        return fail(LSMX_ERR_ALIGN, "%s: row codes need 4-byte, column codes 16-byte aligned rows", fn);
+    if (!aligned(scale_r, 4) || !aligned(scale_c, 4) || (!km && (ld_scale_r % 4 || ld_scale_c % 4)))
+        return fail(LSMX_ERR_ALIGN, "%s: scales must be 4-byte aligned", fn);
+    if ((rows / 128) * (cols / 128) > 0x7FFFFFFF) return fail(LSMX_ERR_SHAPE, "%s: too many tiles", fn);
+    if (int r = device_guard()) return r;
+    if (rows == 0 || cols == 0) return LSMX_OK;
+    lsmx::Quant2dArgs a{x, x_dtype, rows, cols, ldx, codes_r, ld_codes_r, scale_r, ld_scale_r,
+                        codes_c, ld_codes_c, scale_c, ld_scale_c, scale_fmt};
+    return launched(lsmx::launch_quantize_2d(a, (hipStream_t)stream), fn);
+}
+
 int lsmx_round_e2m1(const void *q, int q_dtype, int64_t n, uint8_t *codes, void *stream) {
     if (!q || !codes) return fail(LSMX_ERR_ARG, "lsmx_round_e2m1: null pointer");
     if (q_dtype != LSMX_F32 && q_dtype != LSMX_BF16 && q_dtype != LSMX_F16)

@@ -73,6 +73,21 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ v16f mfma_scale_f4(v4i a, v4i b, v16f c, int cbsz, int blgp, int opsel_a, int scale_a, int opsel_b,
                               int scale_b) __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v4i32.v4i32");
 
+// The stage barrier.  A loader wave first waits until all but its newest N
+// direct-to-LDS loads have landed; the barrier then publishes every loader's
+// data.  The other waves issue no loads, so they go straight to the barrier:
+// their only vector-memory operations are the previous tile's C stores,
+// which then stay in flight across the next tile's stages instead of
+// holding the wave (vmcnt counts stores too).
+#ifndef LSMX_F4_NLW_WAIT
+#define LSMX_F4_NLW_WAIT 0
+#endif
+template <bool LOADER, int N>
+LSMX_DEV void stage_barrier() {
+    if constexpr (LOADER || LSMX_F4_NLW_WAIT) wait_vm_barrier<N>();
+    else asm volatile("s_barrier" ::: "memory");
+}
+
 // compile-time arguments of the stage code: ring slot, loader wave or not
 template <int V>
 struct SlotC {
@@ -396,7 +411,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                         // waves pass the barrier slot s is free and stage u+1
                         // has landed
                         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                        wait_vm_barrier<(S - 2) * L>();
+                        stage_barrier<LOADER, (S - 2) * L>();
                         __builtin_amdgcn_sched_barrier(0);
                     }
 #pragma unroll
@@ -447,7 +462,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                         // this wave's reads of slot s are complete; once all waves
                         // pass the barrier slot s is free and stage u+1 has landed
                         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                        wait_vm_barrier<(S - 2) * L>();
+                        stage_barrier<LOADER, (S - 2) * L>();
                         __builtin_amdgcn_sched_barrier(0);
                     }
     #pragma unroll

@@ -20,6 +20,25 @@ struct QuantArgs {
     int64_t ld_scale;
 };
 
+// Quantization of a 16-bit x[R, C] along both axes in one pass: the row
+// form (codes_r [R, ld_cr], scale_r) and the column form laid out for x^T
+// (codes_c [C, ld_cc], scale_c); packed codes, E8M0 scales (row-major or
+// K-major, the same format for both).
+struct Quant2dArgs {
+    const void *x;
+    int x_dtype;
+    int64_t R, C, ldx;
+    uint8_t *codes_r;
+    int64_t ld_cr;
+    uint8_t *scale_r;
+    int64_t ld_sr;
+    uint8_t *codes_c;
+    int64_t ld_cc;
+    uint8_t *scale_c;
+    int64_t ld_sc;
+    int scale_fmt;
+};
+
 struct DequantArgs {
     const void *codes;
     int codes_fmt;
@@ -67,6 +86,7 @@ struct DenseArgs {
 };
 
 hipError_t launch_quantize(const QuantArgs &a, bool cols, hipStream_t s);
+hipError_t launch_quantize_2d(const Quant2dArgs &a, hipStream_t s);
 hipError_t launch_round(const void *q, int q_dtype, int64_t n, uint8_t *codes, hipStream_t s);
 hipError_t launch_pack(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, hipStream_t s);
 hipError_t launch_unpack(const uint8_t *packed, uint8_t *codes, int64_t n_bytes, hipStream_t s);

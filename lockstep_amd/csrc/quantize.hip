@@ -137,6 +137,26 @@ LSMX_DEV uint32_t e2m1_pack_hw(const uint32_t (&b)[E], uint32_t e8) {
     return w - dec;  // a tie's code magnitude is 2, 4 or 6: no borrow into the next nibble
 }
 
+// The same codes for elements that come from 16-bit inputs (bf16 / fp16,
+// widened to fp32 bits).  Ties toward the smaller magnitude without any
+// comparison: the hardware rounds |x| - 1 ulp (of fp32) to nearest-even
+// instead of |x|.  A 16-bit value has at most 11 significant bits, so no
+// input lies within 1 fp32 ulp above an E2M1 midpoint (midpoint / 2^e has at
+// most 3): every midpoint rounds down, as fp4.py:50-53 does, and every other
+// value lands on the same code as before.  Zeros (either sign) and infinities
+// are left alone, and the scale is still decided from the unmodified amax.
+LSMX_DEV uint32_t below_ulp(uint32_t b) {
+    const uint32_t ax = b & 0x7FFFFFFFu;
+    return (ax - 1u) < 0x7F7FFFFFu ? b - 1u : b;  // 0 < |x| < inf: one ulp toward zero
+}
+template <int E>
+LSMX_DEV uint32_t e2m1_pack_hw16(const uint32_t (&b)[E], uint32_t e8) {
+    uint32_t bd[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) bd[i] = below_ulp(b[i]);
+    return cvt_fp4_pairs<0, E>(0u, bd, u2f(e8 << 23));
+}
+
 // The same codes from the element-by-element rule (lsmx::e2m1_code), which
 // also covers a NaN block (e8 == 255).
 template <int E>
@@ -209,7 +229,10 @@ __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
             if (v >= vpr) continue;  // whole blocks are in or out of range
             // NaN blocks are rare: any lane with one takes the whole wave
             // through the exact per-element rule
-            const uint32_t w = __any(e8 == 255u) ? e2m1_pack_exact<E>(b, e8) : e2m1_pack_hw<E>(b, e8);
+            uint32_t w;
+            if (__any(e8 == 255u)) w = e2m1_pack_exact<E>(b, e8);
+            else if constexpr (sizeof(T) == 2) w = e2m1_pack_hw16<E>(b, e8);
+            else w = e2m1_pack_hw<E>(b, e8);
             const int64_t col = v * E;
             if constexpr (PACKED) {
                 if constexpr (E == 4) *reinterpret_cast<uint16_t *>(codes + r * ld_codes + col / 2) = (uint16_t)w;
@@ -230,6 +253,179 @@ __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
             }
         }
     }
+}
+
+// ------------------------------------------ both axes in one pass
+// x[R, C] of 16-bit elements quantized along its rows (blocks of 32
+// consecutive columns, the quantize_rows_kernel result) AND along its columns
+// (blocks of 32 consecutive rows, the quantize_cols_kernel result, laid out
+// for x^T), reading x once.  A training step needs both forms of every
+// operand it quantizes: X and W along K for the forward, W and dY along N
+// for dgrad, dY and X along T for wgrad (train_step.py:3-6).
+//
+// One workgroup of 4 waves per 128 x 128 tile; wave w holds the tile's rows
+// 32w .. 32w+31, i.e. exactly one 32-row column block, so every reduction
+// stays inside the wave.  Lane l holds the 8 columns 8(l%16) .. +8 of the 8
+// rows 32w + 8(l/16) + i, i = 0..7 (eight 16-byte loads; each instruction
+// reads four 256-byte row segments).
+//   rows:    for each of its rows a lane and the 3 other lanes of its quad
+//            hold one 32-column block: DPP max, hardware FP4 conversion
+//            (e2m1_pack_hw16), 4 bytes of codes per lane and row
+//            (64 contiguous bytes per row and instruction).
+//   columns: a lane's 8 rows of a column are a quarter of its block: max
+//            over them, then over the 4 lanes l, l^16, l^32, l^48 of the
+//            wave; each lane then converts its 4 row pairs of every column
+//            with the column's scale (one dword per column), the dwords go
+//            to LDS, and after one barrier each column's 64 bytes of codes
+//            (the tile's 128 rows) are written by 4 lanes.
+// Scales are E8M0, row-major or K-major; R and C are multiples of 128.
+namespace q2 {
+constexpr int T = 128;      // tile edge
+constexpr int NT = 256;     // threads (4 waves)
+}  // namespace q2
+
+template <typename T>
+LSMX_DEV void bits16(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    if constexpr (__is_same(T, f16_t)) {
+        lo = f2u((float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu)));
+        hi = f2u((float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)));
+    } else {
+        lo = w << 16;
+        hi = w & 0xFFFF0000u;
+    }
+}
+
+template <typename T, int SFMT>
+__global__ __launch_bounds__(q2::NT) void quantize_2d_kernel(
+    const T *__restrict__ x, int64_t R, int64_t C, int64_t ldx, uint8_t *__restrict__ codes_r, int64_t ld_cr,
+    uint8_t *__restrict__ scale_r, int64_t ld_sr, uint8_t *__restrict__ codes_c, int64_t ld_cc,
+    uint8_t *__restrict__ scale_c, int64_t ld_sc) {
+    static_assert(sizeof(T) == 2, "16-bit inputs");
+    // [column][dword]: dword 4w + g holds the codes of tile rows 32w + 8g .. +8
+    __shared__ __attribute__((aligned(16))) uint32_t ccode[q2::T][17];
+    __shared__ uint32_t cscale[q2::T];
+
+    const int tiles_c = (int)(C / q2::T);
+    const int64_t r0 = (int64_t)(blockIdx.x / tiles_c) * q2::T, c0 = (int64_t)(blockIdx.x % tiles_c) * q2::T;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int v = lane & 15, g = lane >> 4;
+    const int rl = 32 * w + 8 * g;                       // first tile row of this lane
+
+    u32x4 raw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        raw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (r0 + rl + i) * ldx + c0 + 8 * v));
+
+    // ---- rows: blocks of 32 columns = the 4 lanes of a quad; the column
+    // maxima are gathered on the way
+    uint32_t cm[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cm[e] = 0;
+    const int64_t slice = c0 / 128;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t b[8];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) bits16<T>(raw[i][p], b[2 * p], b[2 * p + 1]);
+        uint32_t am = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            am = max(am, b[e] & 0x7FFFFFFFu);
+            cm[e] = max(cm[e], b[e] & 0x7FFFFFFFu);
+        }
+        am = group_max<4>(am);
+        const uint32_t e8 = block_e8m0(am);
+        const uint32_t wd = __any(e8 == 255u) ? e2m1_pack_exact<8>(b, e8) : e2m1_pack_hw16<8>(b, e8);
+        const int64_t r = r0 + rl + i;
+        *reinterpret_cast<uint32_t *>(codes_r + r * ld_cr + (c0 + 8 * v) / 2) = wd;
+        // the 4 block bytes of this row's 128 columns, gathered by lane v == 0
+        const uint32_t e4 = e8 | ((uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 4) & 63) << 2, (int)e8) << 8) |
+                            ((uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 8) & 63) << 2, (int)e8) << 16) |
+                            ((uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 12) & 63) << 2, (int)e8) << 24);
+        if (v == 0) {
+            if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR)
+                reinterpret_cast<uint32_t *>(scale_r)[slice * ld_sr + r] = e4;
+            else
+                *reinterpret_cast<uint32_t *>(scale_r + r * ld_sr + c0 / 32) = e4;
+        }
+    }
+
+    // ---- columns: |x| max over the wave's 32 rows (lanes l, l^16, l^32, l^48)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        cm[e] = max(cm[e], (uint32_t)__shfl_xor((int)cm[e], 16, 64));
+        cm[e] = max(cm[e], (uint32_t)__shfl_xor((int)cm[e], 32, 64));
+    }
+    uint32_t e8c[8];
+    bool nan_blk = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        e8c[e] = block_e8m0(cm[e]);
+        nan_blk |= e8c[e] == 255u;
+    }
+    // the column pass re-expands the raw words instead of keeping 64
+    // widened elements live across the row pass
+#pragma unroll
+    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(raw[i]));
+    const bool exact = __any(nan_blk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        uint32_t col[8];  // this lane's 8 rows of column 8v + e
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t lo, hi;
+            bits16<T>(raw[i][e >> 1], lo, hi);
+            col[i] = (e & 1) ? hi : lo;
+        }
+        uint32_t dw;  // codes of rows rl .. rl+7, first row in the low nibble
+        if (exact) {
+            dw = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dw |= e2m1_code(col[i], e8c[e]) << (4 * i);
+        } else {
+            dw = e2m1_pack_hw16<8>(col, e8c[e]);
+        }
+        ccode[8 * v + e][4 * w + g] = dw;
+    }
+    // this wave's column scales: byte w of each column's K-major dword
+    if (g == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            reinterpret_cast<uint8_t *>(cscale)[4 * (8 * v + e) + w] = (uint8_t)e8c[e];
+    }
+    __syncthreads();
+    {
+        // column t / 2, half t % 2: 32 bytes of its 64 = dwords 8h .. 8h+7
+        const int col = t >> 1, h = t & 1;
+        const uint32_t *src = &ccode[col][8 * h];
+        const u32x4 q0 = u32x4{src[0], src[1], src[2], src[3]}, q1 = u32x4{src[4], src[5], src[6], src[7]};
+        uint8_t *dst = codes_c + (c0 + col) * ld_cc + r0 / 2 + 32 * h;
+        *reinterpret_cast<u32x4 *>(dst) = q0;
+        *reinterpret_cast<u32x4 *>(dst + 16) = q1;
+        if (t < q2::T) {
+            const uint32_t e4 = cscale[t];
+            if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR)
+                reinterpret_cast<uint32_t *>(scale_c)[(r0 / 128) * ld_sc + c0 + t] = e4;
+            else
+                *reinterpret_cast<uint32_t *>(scale_c + (c0 + t) * ld_sc + r0 / 32) = e4;
+        }
+    }
+}
+
+template <typename T>
+static hipError_t launch_2d(const Quant2dArgs &a, hipStream_t s) {
+    const dim3 grid((unsigned)((a.R / q2::T) * (a.C / q2::T))), blk(q2::NT);
+#define LSMX_Q2(F)                                                                                                \
+    hipLaunchKernelGGL((quantize_2d_kernel<T, F>), grid, blk, 0, s, reinterpret_cast<const T *>(a.x), a.R, a.C,  \
+                       a.ldx, a.codes_r, a.ld_cr, a.scale_r, a.ld_sr, a.codes_c, a.ld_cc, a.scale_c, a.ld_sc)
+    if (a.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) LSMX_Q2(LSMX_SCALE_E8M0_KMAJOR);
+    else LSMX_Q2(LSMX_SCALE_E8M0);
+#undef LSMX_Q2
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_2d(const Quant2dArgs &a, hipStream_t s) {
+    return a.x_dtype == LSMX_BF16 ? launch_2d<bf16_t>(a, s) : launch_2d<f16_t>(a, s);
 }
 
 // ------------------------------------------------- column-mode quantize

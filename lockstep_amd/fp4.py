@@ -173,6 +173,44 @@ def quantize_mxfp4_t(x: torch.Tensor, block: int = 32, packed: bool = True, e8m0
     return codes, scale
 
 
+def quantize_pack_mxfp4_2d(x: torch.Tensor, scale_layout: str = "kmajor"):
+    """Both MXFP4 forms of a 2-D x [R, C] from one read of x:
+
+        (row_packed, row_scale) == quantize_pack_mxfp4(x, scale_layout=...)
+        (col_packed, col_scale) == quantize_mxfp4_t(x, scale_layout=...)
+
+    i.e. x quantized along its rows (blocks of 32 columns) and along its
+    columns (blocks of 32 rows, laid out for x^T), E8M0 scales.  bf16 / fp16
+    x with R and C multiples of 128 run the fused one-pass kernel
+    (lsmx_quantize_mxfp4_2d); other inputs run the two quantizers."""
+    C.require_device(x)
+    assert x.dim() == 2, "quantize_pack_mxfp4_2d takes a 2-D tensor"
+    R, Cn = x.shape
+    if scale_layout not in ("rows", "kmajor"):
+        raise ValueError(f"scale_layout must be 'rows' or 'kmajor', got {scale_layout!r}")
+    if x.dtype not in (torch.bfloat16, torch.float16) or R % 128 or Cn % 128:
+        rp, rs = quantize_pack_mxfp4(x, scale_layout=scale_layout)
+        cp, cs = quantize_mxfp4_t(x, scale_layout=scale_layout)
+        return rp, rs, cp, cs
+    if x.stride(1) != 1 or (R > 1 and x.stride(0) < Cn) or x.data_ptr() % 16 or (x.stride(0) * 2) % 16:
+        x = x.contiguous()
+    rp = torch.empty((R, Cn // 2), dtype=torch.uint8, device=x.device)
+    cp = torch.empty((Cn, R // 2), dtype=torch.uint8, device=x.device)
+    if scale_layout == "kmajor":
+        rs = torch.empty((Cn // 128, R, 4), dtype=torch.uint8, device=x.device)
+        cs = torch.empty((R // 128, Cn, 4), dtype=torch.uint8, device=x.device)
+        fmt, lsr, lsc = C.SCALE_E8M0_KMAJOR, R, Cn
+    else:
+        rs = torch.empty((R, Cn // 32), dtype=torch.uint8, device=x.device)
+        cs = torch.empty((Cn, R // 32), dtype=torch.uint8, device=x.device)
+        fmt, lsr, lsc = C.SCALE_E8M0, Cn // 32, R // 32
+    if R and Cn:
+        C.call("lsmx_quantize_mxfp4_2d", x.data_ptr(), C.dtype_code(x.dtype), R, Cn, x.stride(0) if R > 1 else Cn,
+               rp.data_ptr(), Cn // 2, rs.data_ptr(), lsr, cp.data_ptr(), R // 2, cs.data_ptr(), lsc, fmt,
+               C.stream_of(x))
+    return rp, rs, cp, cs
+
+
 def e8m0_to_scale(e8m0: torch.Tensor) -> torch.Tensor:
     """E8M0 bytes -> fp32 powers of two 2^(e - 127) (0xFF -> NaN; byte 0 ->
     2^-127, the fp32 subnormal 0x00400000).  Exact."""

@@ -17,9 +17,11 @@ and W [N, K],
                            W along its columns (quantize_mxfp4_t),
     wgrad  dW = dY^T X     contracts over T: dY and X quantized along their
                            columns,
-each followed by the block-scaled f4 x f4 GEMM with fp32 accumulation: six
-quantizations and three GEMMs per linear, the scheme of train_step.py:3-6
-with every GEMM in MXFP4.  T, N and K must be multiples of 128.
+each followed by the block-scaled f4 x f4 GEMM with fp32 accumulation: the
+scheme of train_step.py:3-6 with every GEMM in MXFP4.  Each of X, W and dY is
+needed along two axes; fp4.quantize_pack_mxfp4_2d produces both forms from
+one read, so a linear costs three quantization passes and three GEMMs.
+T, N and K must be multiples of 128.
 """
 
 from __future__ import annotations
@@ -60,20 +62,6 @@ def _forward_hip(x2: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return mxfp4_gemm_packed(xp, wp, xs, ws, out_dtype=x2.dtype)
 
 
-def _mm_rows_cols(a: torch.Tensor, b: torch.Tensor, out_dtype) -> torch.Tensor:
-    """a [M, R] @ b [R, N] in MXFP4: a quantized along its rows, b along its columns."""
-    ap, as_ = fp4.quantize_pack_mxfp4(a, scale_layout="kmajor")
-    bp, bs = fp4.quantize_mxfp4_t(b, scale_layout="kmajor")
-    return mxfp4_gemm_packed(ap, bp, as_, bs, out_dtype=out_dtype)
-
-
-def _mm_cols_cols(a: torch.Tensor, b: torch.Tensor, out_dtype) -> torch.Tensor:
-    """a[R, M]^T @ b [R, N] in MXFP4: both quantized along their columns (axis R)."""
-    ap, as_ = fp4.quantize_mxfp4_t(a, scale_layout="kmajor")
-    bp, bs = fp4.quantize_mxfp4_t(b, scale_layout="kmajor")
-    return mxfp4_gemm_packed(ap, bp, as_, bs, out_dtype=out_dtype)
-
-
 def mxfp4_backward(gy: torch.Tensor, x: torch.Tensor, w: torch.Tensor):
     """(dX, dW) of Y = X W^T with both backward GEMMs in MXFP4.
 
@@ -84,8 +72,12 @@ def mxfp4_backward(gy: torch.Tensor, x: torch.Tensor, w: torch.Tensor):
     assert T % 128 == 0 and N % 128 == 0 and K % 128 == 0, \
         "the MXFP4 backward needs T, N and K to be multiples of 128"
     gy = gy.contiguous()
-    dx = _mm_rows_cols(gy, w, x.dtype)          # dY [T,N] @ W [N,K]
-    dw = _mm_cols_cols(gy, x, w.dtype)          # dY^T [N,T] @ X [T,K]
+    # dY along N (dgrad) and along T (wgrad) from one read of dY
+    gr, grs, gc, gcs = fp4.quantize_pack_mxfp4_2d(gy, scale_layout="kmajor")
+    wc, wcs = fp4.quantize_mxfp4_t(w, scale_layout="kmajor")
+    xc, xcs = fp4.quantize_mxfp4_t(x, scale_layout="kmajor")
+    dx = mxfp4_gemm_packed(gr, wc, grs, wcs, out_dtype=x.dtype)     # dY [T,N] @ W [N,K]
+    dw = mxfp4_gemm_packed(gc, xc, gcs, xcs, out_dtype=w.dtype)     # dY^T [N,T] @ X [T,K]
     return dx, dw
 
 
@@ -106,21 +98,44 @@ class _MXFP4Matmul(torch.autograd.Function):
 
 
 class _MXFP4MatmulQ(torch.autograd.Function):
-    """_MXFP4Matmul with the backward GEMMs in MXFP4 too (see mxfp4_backward)."""
+    """_MXFP4Matmul with the backward GEMMs in MXFP4 too (see mxfp4_backward).
+
+    When T, N and K are multiples of 128 the forward quantizes X and W along
+    both axes in one pass each (fp4.quantize_pack_mxfp4_2d): the row forms
+    feed the forward GEMM and the column forms -- exactly what the backward
+    GEMMs need of X and W -- are saved instead of X and W, so the backward
+    only quantizes dY (again both axes in one pass).  The gradients are bit
+    for bit those of mxfp4_backward."""
 
     @staticmethod
     def forward(ctx, x, w):
-        ctx.save_for_backward(x, w)
         k = kernel()
         if k is None:
             raise RuntimeError("MXFP4Linear needs a gfx950 GPU and liblsmx.so (path() == "
                                f"{path()!r}); there is no CPU fallback")
-        return k(x, w)
+        T, K = x.shape
+        N = w.shape[0]
+        ctx.dtypes = (x.dtype, w.dtype)
+        if T % 128 or N % 128 or K % 128:
+            ctx.fused = False
+            ctx.save_for_backward(x, w)
+            return k(x, w)
+        ctx.fused = True
+        xr, xrs, xc, xcs = fp4.quantize_pack_mxfp4_2d(x, scale_layout="kmajor")
+        wr, wrs, wc, wcs = fp4.quantize_pack_mxfp4_2d(w, scale_layout="kmajor")
+        ctx.save_for_backward(xc, xcs, wc, wcs)
+        return mxfp4_gemm_packed(xr, wr, xrs, wrs, out_dtype=x.dtype)
 
     @staticmethod
     def backward(ctx, gy):
-        x, w = ctx.saved_tensors
-        return mxfp4_backward(gy, x, w)
+        if not ctx.fused:
+            x, w = ctx.saved_tensors
+            return mxfp4_backward(gy, x, w)
+        xc, xcs, wc, wcs = ctx.saved_tensors
+        gr, grs, gc, gcs = fp4.quantize_pack_mxfp4_2d(gy.contiguous(), scale_layout="kmajor")
+        dx = mxfp4_gemm_packed(gr, wc, grs, wcs, out_dtype=ctx.dtypes[0])
+        dw = mxfp4_gemm_packed(gc, xc, gcs, xcs, out_dtype=ctx.dtypes[1])
+        return dx, dw
 
 
 def mxfp4_matmul(x2: torch.Tensor, w: torch.Tensor, quantized_backward: bool = False):

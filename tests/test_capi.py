@@ -222,3 +222,12 @@ def test_scale_shapes_are_checked_before_any_device_work():
         dual_gemm.dual_mxfp4(a, a, pk, good.t())
     with pytest.raises(TypeError, match="activations must be"):
         mxfp4_gemm.mxfp4_gemm_bf16(torch.zeros((8, 128), dtype=torch.float64), pk, good)
+
+
+def test_two_axis_quantizer_validates_before_launch():
+    def args(dt, R, cols, fmt):
+        return (FAKE, dt, R, cols, cols, FAKE, cols // 2, FAKE, R, FAKE, R // 2, FAKE, cols, fmt, None)
+    assert _rc("lsmx_quantize_mxfp4_2d", *args(C.F32, 256, 256, C.SCALE_E8M0_KMAJOR)) == C.ERR_DTYPE
+    assert _rc("lsmx_quantize_mxfp4_2d", *args(C.BF16, 256, 256, C.SCALE_F32)) == C.ERR_DTYPE
+    rc = _rc("lsmx_quantize_mxfp4_2d", *args(C.BF16, 200, 256, C.SCALE_E8M0_KMAJOR))
+    assert rc == C.ERR_SHAPE and "multiples of 128" in C.last_error()

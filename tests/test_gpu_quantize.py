@@ -301,3 +301,70 @@ def test_exact_ties_round_toward_smaller_magnitude(dev, fp4mod, oracle, dtype):
     assert np.array_equal(pk.cpu().numpy(), oracle.pack_fp4(ref_codes))
     want = oracle.scale_to_e8m0(ref_scale).reshape(rows, K // 128, 4).transpose(1, 0, 2)
     assert np.array_equal(e8k.cpu().numpy(), want)
+
+
+def _both_forms_ref(oracle, xh, dtype):
+    """The oracle's row form of x and row form of x^T (the column form)."""
+    rc, rs = oracle.quantize_mxfp4(xh, 32, dtype)
+    cc, cs = oracle.quantize_mxfp4(np.ascontiguousarray(xh.T), 32, dtype)
+    return oracle.pack_fp4(rc), oracle.scale_to_e8m0(rs), oracle.pack_fp4(cc), oracle.scale_to_e8m0(cs)
+
+
+def _kmajor(e8):
+    rows, nb = e8.shape
+    return e8.reshape(rows, nb // 4, 4).transpose(1, 0, 2)
+
+
+def _check_2d(fp4mod, oracle, xh, dtype, dev, layouts=("kmajor", "rows")):
+    rp, rs, cp, cs = _both_forms_ref(oracle, xh, dtype)
+    xt = to_dev(xh, dtype, dev)
+    for lay in layouts:
+        grp, grs, gcp, gcs = fp4mod.quantize_pack_mxfp4_2d(xt, scale_layout=lay)
+        assert np.array_equal(grp.cpu().numpy(), rp) and np.array_equal(gcp.cpu().numpy(), cp), lay
+        want_r, want_c = (_kmajor(rs), _kmajor(cs)) if lay == "kmajor" else (rs, cs)
+        assert np.array_equal(grs.cpu().numpy(), want_r) and np.array_equal(gcs.cpu().numpy(), want_c), lay
+        # the same bytes as the two one-axis quantizers
+        a = fp4mod.quantize_pack_mxfp4(xt, scale_layout=lay)
+        b = fp4mod.quantize_mxfp4_t(xt, scale_layout=lay)
+        assert torch.equal(a[0], grp) and torch.equal(a[1], grs) and torch.equal(b[0], gcp) and torch.equal(b[1], gcs)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("R,C", [(128, 128), (256, 384), (384, 1024), (2048, 8192)])
+def test_quantize_both_axes_in_one_pass(dev, fp4mod, oracle, dtype, R, C):
+    """quantize_pack_mxfp4_2d: row form == fp4.py:57-72 on x, column form ==
+    fp4.py:57-72 on x.t().contiguous(), both layouts of E8M0 scales."""
+    x = gen.student_t3(R + 3 * C, (R, C), scale=0.05)
+    xh = gen.to_bf16_bits(x) if dtype == "bf16" else x.astype(np.float16).view(np.uint16)
+    _check_2d(fp4mod, oracle, xh, dtype, dev)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_quantize_both_axes_ties_and_specials(dev, fp4mod, oracle, dtype):
+    """Values on the quarter grid of 2^-3 with most 32-blocks (along either
+    axis) reaching 5 or 6 units: their scale is 2^-3, and the many elements at
+    0.75, 1.75 and 3.5 units are ties that fp4.py rounds toward the smaller
+    magnitude along both axes.  Plus NaN, +-Inf and -0 blocks."""
+    R, C = 256, 256
+    rng = np.random.default_rng(11)
+    grid = np.array([0, 0.25, 0.5, 0.75, 1, 1.25, 1.5, 1.75, 2, 2.5, 3, 3.5, 4, 5, 6], dtype=np.float64)
+    x = rng.choice(grid, (R, C)) * rng.choice([-1.0, 1.0], (R, C)) * 0.125
+    x = x.astype(np.float32)
+    x[5, 40] = np.nan
+    x[130, 7] = np.inf
+    x[131, 9] = -np.inf
+    x[64:96, 160:192] = -0.0
+    x[200, 200:232] = 0.0
+    xh = gen.to_bf16_bits(x) if dtype == "bf16" else x.astype(np.float16).view(np.uint16)
+    rc, _ = oracle.quantize_mxfp4(xh, 32, dtype)
+    assert np.isin(rc & 7, [1, 3, 5]).mean() > 0.2       # plenty of rounded-down ties
+    _check_2d(fp4mod, oracle, xh, dtype, dev)
+
+
+def test_quantize_both_axes_falls_back_for_other_inputs(dev, fp4mod, oracle):
+    """fp32 input, or sizes that are not multiples of 128, run the two
+    one-axis kernels and give the same bytes."""
+    for (R, C, dtype) in [(256, 256, "f32"), (96, 128, "bf16")]:
+        x = gen.normal(R * C, (R, C))
+        xh = x if dtype == "f32" else gen.to_bf16_bits(x)
+        _check_2d(fp4mod, oracle, xh, None if dtype == "f32" else dtype, dev, layouts=("rows",))
