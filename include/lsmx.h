@@ -157,8 +157,31 @@ int lsmx_gemm_bf16f4(const void *a, int64_t lda, const uint8_t *w_pk, int64_t ld
                      const void *w_scale, int64_t ld_sw, int scale_fmt, void *c, int c_dtype,
                      int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
 
+/* Workspace bytes the split-K form of the bf16 x MXFP4 GEMM below needs at
+ * this shape (single form: dual = 0, dual-batch form: dual = 1), or 0 when
+ * the library does not split this shape.  It splits K in 2 or 4 slices when
+ * the whole-K 128 x 256 output tiles would fill less than half of the CUs
+ * (a few hundred activation rows against a wide weight, e.g. M = 128
+ * against N = 14336); the decision depends on M, N and K only. */
+int64_t lsmx_gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, int dual);
+
+/* lsmx_gemm_bf16f4 (a1 = c1 = NULL) or lsmx_gemm_dual_bf16f4 (both set)
+ * with a caller-provided device workspace, which lets the library split K
+ * (lsmx_gemm_bf16f4_workspace): each K slice of a 128 x 256 output tile is
+ * one workgroup that writes an fp32 partial tile to the workspace, and a
+ * second kernel on the same stream adds the slices in slice order (a fixed
+ * order: repeated calls, and the single and dual forms, give identical
+ * bits).  The same sums as the reference's split-K GEMM (dual_gemm.py:
+ * 117-179) without its atomics.  Workspace: 16-byte aligned, at least the
+ * bytes lsmx_gemm_bf16f4_workspace returns, no initial contents required;
+ * calls that share a workspace must be stream-ordered.  A NULL workspace,
+ * or a shape the library does not split, runs the whole-K kernels. */
+int lsmx_gemm_bf16f4_ws(const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                        const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype, int64_t ldc,
+                        int64_t M, int64_t N, int64_t K, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Weight-only GEMM for any activation type: C[M, N] = A[M, K] . deq(W)^T.
- * Replaces the fp32 product of BASELINE cfg1, Y = X @ dequantize_mxfp4(W)^T
+ * Replaces the reference's fp32 fake-quant product, Y = X @ dequantize_mxfp4(W)^T
  * (fp4.py:75-78 inside fp4_linear.py:40's fake-quant F.linear, with X left
  * unquantized), which the reference computes in fp32 on the CPU.
  *   a_dtype LSMX_BF16: the same kernels as lsmx_gemm_bf16f4.

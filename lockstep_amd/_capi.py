@@ -41,6 +41,9 @@ SIGNATURES = {
     "lsmx_fp4_to_e4m3": [_vp, _vp, _i64, _vp],
     "lsmx_gemm_f4f4": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_bf16f4": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
+    "lsmx_gemm_bf16f4_workspace": [_i64, _i64, _i64, _int],
+    "lsmx_gemm_bf16f4_ws": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp,
+                            _i64, _vp],
     "lsmx_gemm_wonly_f4": [_vp, _int, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_dual_bf16f4": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64,
                               _i64, _vp],
@@ -49,6 +52,8 @@ SIGNATURES = {
     "lsmx_transpose": [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp],
     "lsmx_scale_to_e8m0": [_vp, _i64, _i64, _i64, _int, _vp, _i64, _vp],
 }
+
+RET_I64 = ("lsmx_gemm_bf16f4_workspace",)
 
 _lib = None
 _lock = threading.Lock()
@@ -77,7 +82,8 @@ def load() -> ctypes.CDLL:
             for name, argtypes in SIGNATURES.items():
                 fn = getattr(L, name)
                 fn.argtypes = argtypes
-                fn.restype = ctypes.c_char_p if name in ("lsmx_version", "lsmx_last_error") else ctypes.c_int
+                fn.restype = (ctypes.c_char_p if name in ("lsmx_version", "lsmx_last_error") else
+                              ctypes.c_int64 if name in RET_I64 else ctypes.c_int)
             _lib = L
     return _lib
 
@@ -119,3 +125,19 @@ def require_device(*tensors: torch.Tensor) -> None:
             raise RuntimeError(
                 "lockstep_amd runs its MXFP4 ops on a gfx950 GPU only; got a tensor on "
                 f"{t.device} (there is no CPU fallback)")
+
+
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A device workspace of at least nbytes for the split-K GEMMs, one per
+    (device, stream): calls on one stream are ordered, so they may share it.
+    Kept for later calls; grown by replacing it with a larger one (the old
+    one returns to torch's caching allocator, stream-ordered)."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws

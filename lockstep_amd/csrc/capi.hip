@@ -347,7 +347,8 @@ int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, 
 
 static int w4_common(const char *fn, const void *a0, const void *a1, int a_dtype, int64_t lda, const uint8_t *w_pk,
                      int64_t ldw, const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype,
-                     int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
+                     int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream, void *ws = nullptr,
+                     int64_t ws_bytes = 0) {
     if (!a0 || !w_pk || !w_scale || !c0) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
     if (a_dtype != LSMX_BF16 && a_dtype != LSMX_F32 && a_dtype != LSMX_F16)
         return fail(LSMX_ERR_DTYPE, "%s: a_dtype %d unsupported", fn, a_dtype);
@@ -370,11 +371,19 @@ static int w4_common(const char *fn, const void *a0, const void *a1, int a_dtype
         return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
     const int cb = c_dtype == LSMX_F32 ? 4 : 2;
     if (!aligned(c0, cb) || (c1 && !aligned(c1, cb))) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (ws) {
+        const int64_t need = lsmx::gemm_bf16f4_workspace(M, N, K, a1 != nullptr);
+        if (ws_bytes < need)
+            return fail(LSMX_ERR_ARG, "%s: workspace of %lld bytes, this shape needs %lld", fn, (long long)ws_bytes,
+                        (long long)need);
+        if (!aligned(ws, 16)) return fail(LSMX_ERR_ALIGN, "%s: workspace must be 16-byte aligned", fn);
+    }
     if (int r = device_guard()) return r;
     if (M == 0 || N == 0) return LSMX_OK;
     if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
     lsmx::GemmArgs g{reinterpret_cast<const uint8_t *>(a0), reinterpret_cast<const uint8_t *>(a1), lda, nullptr, 0,
                      w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype, ldc, M, N, K};
+    g.ws = reinterpret_cast<float *>(ws);
     if (a_dtype != LSMX_BF16) return launched(lsmx::launch_gemm_xf4(g, a_dtype, (hipStream_t)stream), fn);
     return launched(lsmx::launch_gemm_bf16f4(g, (hipStream_t)stream), fn);
 }
@@ -391,6 +400,19 @@ int lsmx_gemm_dual_bf16f4(const void *a0, const void *a1, int64_t lda, const uin
     if (!a1 || !c1) return fail(LSMX_ERR_ARG, "lsmx_gemm_dual_bf16f4: null pointer");
     return w4_common("lsmx_gemm_dual_bf16f4", a0, a1, LSMX_BF16, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype,
                      ldc, M, N, K, stream);
+}
+
+int64_t lsmx_gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, int dual) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
+    return lsmx::gemm_bf16f4_workspace(M, N, K, dual != 0);
+}
+
+int lsmx_gemm_bf16f4_ws(const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                        const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype, int64_t ldc,
+                        int64_t M, int64_t N, int64_t K, void *workspace, int64_t workspace_bytes, void *stream) {
+    if ((a1 == nullptr) != (c1 == nullptr)) return fail(LSMX_ERR_ARG, "lsmx_gemm_bf16f4_ws: a1 and c1 go together");
+    return w4_common("lsmx_gemm_bf16f4_ws", a0, a1, LSMX_BF16, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1,
+                     c_dtype, ldc, M, N, K, stream, workspace, workspace_bytes);
 }
 
 int lsmx_gemm_wonly_f4(const void *a, int a_dtype, int64_t lda, const uint8_t *w_pk, int64_t ldw,

@@ -240,8 +240,8 @@ __global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(
 
 // ------------------------------------------------------------------ fp32 / fp16 activations
 // Weight-only GEMM with wider activations: Y = X . deq(W)^T for X in fp32
-// (BASELINE cfg1: the fake-quant forward of fp4_linear.py:40 with an
-// unquantized fp32 X, deq(W) of fp4.py:75-78) or fp16.  Each activation is
+// (the fake-quant forward of fp4_linear.py:40 with an unquantized fp32
+// X, deq(W) of fp4.py:75-78) or fp16.  Each activation is
 // split exactly into NTERM bf16 terms, each the bf16 truncation of what the
 // terms before it leave,
 //     hi = tr(x),  mid = tr(x - hi),  lo = x - hi - mid     (fp32: NTERM = 3)
@@ -473,11 +473,21 @@ LSMX_DEV int swz(int row) { return (row >> 1) & 7; }
 // BR x BN tile (256 x 256 for large M; 128 x 64 and 128 x 128 for M of a few
 // hundred rows, where a 256-row tile would leave most CUs idle and every CU
 // streams all of A), S-slot ring.
-template <int NB, int CT, int BR, int BN, int S>
+// SPLITK: the workgroup takes K slice blockIdx % splits of its tile (g.k_split
+// deep) and writes its fp32 partial tile to the workspace g.ws;
+// splitk_reduce_kernel then adds the slices in slice order and stores C.
+// WGM x (8 / WGM) waves: 4 x 2 (each wave a quarter of the rows and half of
+// the columns) or, for 128-row tiles, 1 x 8 (each wave all rows and a 32-
+// column strip, so every weight fragment is dequantized by one wave instead
+// of four: the dequantization is VALU work that does not shrink with the
+// tile's row count).
+template <int NB, int CT, int BR, int BN, int S, bool SPLITK = false, int WGM = 4>
 __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g) {
     using namespace wr;
     constexpr int RPB = BR / NB;        // A rows per batch per workgroup
-    constexpr int TM = BR / 128, TN = BN / 64;   // 32 x 32 tiles per wave (4 x 2 waves)
+    constexpr int WGN = NW / WGM;
+    constexpr int TM = BR / 32 / WGM, TN = BN / 32 / WGN;   // 32 x 32 tiles per wave
+    static_assert(NB == 1 || TM * 32 <= RPB, "a wave's rows lie in one batch");
     constexpr int A_SLOT = BR * A_ROW_B, W_SLOT = BN * W_ROW_B;
     constexpr int XA = A_SLOT / 1024 / NW;       // A load instructions per wave per stage
     constexpr int L = XA + 1;                    // + one W load (scales: one more every 8 stages)
@@ -493,14 +503,18 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     __shared__ __attribute__((aligned(16))) uint8_t sNull[WW < NW ? 1024 : 16];
 
     const int tiles_m = (int)((g.M + RPB - 1) / RPB), tiles_n = (int)((g.N + BN - 1) / BN);
+    const int tile = SPLITK ? (int)blockIdx.x / g.splits : (int)blockIdx.x;
+    const int split = SPLITK ? (int)blockIdx.x - tile * g.splits : 0;
     int tm, tn;
-    tile_coords((int)blockIdx.x, tiles_m, tiles_n, GROUP_M, tm, tn);
+    tile_coords(tile, tiles_m, tiles_n, GROUP_M, tm, tn);
     const int64_t m0 = (int64_t)tm * RPB, n0 = (int64_t)tn * BN;
-    const int nk = (int)(g.K / BK);
+    // this workgroup's K range: [kb0, kb0 + kdepth)
+    const int64_t kb0 = SPLITK ? (int64_t)split * g.k_split : 0, kdepth = SPLITK ? g.k_split : g.K;
+    const int nk = (int)(kdepth / BK);
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int frow = lane & 31, half = lane >> 5;
 
     // ---- DMA addressing.  A load i of wave w covers slot rows
@@ -521,30 +535,30 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         const int rb = r0 - b * RPB;                    // row inside the batch tile
         const int row = r0 + arow_l;
         a_off[i] = (uint32_t)(arow_l * lda_b + (((lane & 7) ^ swz(row)) << 4));
-        a_base[i] = (b ? g.a1 : g.a) + (m0 + rb) * lda_b;
+        a_base[i] = (b ? g.a1 : g.a) + (m0 + rb) * lda_b + kb0 * 2;
         // rows left in the operand from this instruction's first row, at most 8
         const int64_t left = g.M - (m0 + rb), rows = left < 8 ? (left > 0 ? left : 0) : 8;
-        a_bytes[i] = rows > 0 ? (uint64_t)((rows - 1) * lda_b + g.K * 2) : 0;
+        a_bytes[i] = rows > 0 ? (uint64_t)((rows - 1) * lda_b + (g.K - kb0) * 2) : 0;
     }
     // W: wave w < WW loads slot rows w*32 .. +31, lane -> row lane%32,
     // 16-byte half lane/32
     const bool w_real = wave < WW;
     const uint32_t w_off = (uint32_t)((lane & 31) * g.ldb + (lane >> 5) * 16);
-    const uint8_t *w_base = g.b + (n0 + (w_real ? wave : 0) * 32) * g.ldb;
+    const uint8_t *w_base = g.b + (n0 + (w_real ? wave : 0) * 32) * g.ldb + kb0 / 2;
     const int64_t w_left = w_real ? g.N - (n0 + wave * 32) : 0, w_rows = w_left < 32 ? (w_left > 0 ? w_left : 0) : 32;
-    const uint64_t w_bytes = w_rows > 0 ? (uint64_t)((w_rows - 1) * g.ldb + g.K / 2) : 0;
+    const uint64_t w_bytes = w_rows > 0 ? (uint64_t)((w_rows - 1) * g.ldb + (g.K - kb0) / 2) : 0;
     const uint32_t w_lds = w_real ? lds_u32(&sW[0][0]) + wave * 1024 : lds_u32(&sNull[0]);
     const uint32_t w_slot = w_real ? W_SLOT : 0;
     // scales: wave w loads 16 bytes of weight rows (w % SWV)*64 + lane (waves
     // w and w + SWV write the same bytes, so every wave counts the same loads)
     const int s_w = wave % SWV;
     const int64_t s_rows = g.N - n0;
-    const uint8_t *s_base = reinterpret_cast<const uint8_t *>(g.sb) + n0 * g.ld_sb;
+    const uint8_t *s_base = reinterpret_cast<const uint8_t *>(g.sb) + n0 * g.ld_sb + kb0 / 32;
     const uint32_t s_off = (uint32_t)(((s_w * 64) + lane) * g.ld_sb);
     auto issue_scales = [&](int grp) __attribute__((always_inline)) {
         const int64_t ks = (int64_t)grp * 16;
         const int64_t rows = s_rows < BN ? s_rows : BN;
-        const uint64_t bytes = (uint64_t)((rows - 1) * g.ld_sb + g.K / 32 - ks);
+        const uint64_t bytes = (uint64_t)((rows - 1) * g.ld_sb + (g.K - kb0) / 32 - ks);
         dma_x4(s_off, buf_rsrc(s_base + ks, bytes), lds_u32(&sS[grp & 1][0]) + s_w * 1024);
     };
 
@@ -639,6 +653,33 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     }
     // no load may still be writing this workgroup's LDS when it exits
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    if constexpr (SPLITK) {
+        // The K slice's partial tile goes to partial array `split` of the
+        // workspace, [splits][NB][Mp][Np] fp32 with Mp, Np the tile-padded
+        // sizes, so every store is in bounds; 16-byte stores of 4
+        // consecutive columns after the in-quad transpose.  The reduction
+        // kernel launched next on the stream adds the slices.
+        const int64_t Mp = (int64_t)tiles_m * RPB, Np = (int64_t)tiles_n * BN;
+        const int bq = NB == 2 ? (wm * TM * 32) / RPB : 0;
+        float *pbase = g.ws + ((int64_t)split * NB + bq) * Mp * Np;
+        const int64_t prow0 = m0 + wm * (TM * 32) - bq * RPB, pcol0 = n0 + wn * (TN * 32);
+        const int q = frow & 3;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                  acc[i][j][4 * gq + 3]};
+                    quad_transpose(x, q);
+                    const int64_t row = prow0 + i * 32 + 8 * gq + 4 * half + q;
+                    *reinterpret_cast<u32x4 *>(pbase + row * Np + pcol0 + j * 32 + (frow & ~3)) =
+                        u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
+                }
+        return;
+    }
 
     // epilogue: acc element e of tile (i, j) is row i*32 + 8*(e/4) + 4*half + e%4, column j*32 + frow
     const int b = NB == 2 ? (wm * TM * 32) / RPB : 0;
@@ -1023,7 +1064,7 @@ static hipError_t launch_gemv(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
-// up to 32 rows per batch (cfg3 M = 16: 20 us against 34 us for the 128-row
+// up to 32 rows per batch (M = 16 against a 14336 x 4096 weight: 20 us against 34 us for the 128-row
 // ring tile, whose MFMAs would be 7/8 padding; from M = 64 the ring is faster)
 #ifndef LSMX_SKINNY_MAX_M
 #define LSMX_SKINNY_MAX_M 32
@@ -1097,14 +1138,102 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 #ifndef LSMX_W4_RING
 #define LSMX_W4_RING 1
 #endif
-    // the ring kernel is worth it from half a wave of 256 x 256 tiles on (cfg3 M = 1024: 224 tiles)
+    // the ring kernel is worth it from half a wave of 256 x 256 tiles on (M = 1024, N = 14336: 224 tiles)
     if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3>(g, s);
     if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
     if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
-    // a few hundred rows: 128 x 64 tiles through a 4-slot DMA ring (cfg3
-    // M = 128: 48 -> 38 us; M = 64: 44 -> 35 us against the skinny kernel)
+    // a few hundred rows: 128 x 64 tiles through a 4-slot DMA ring (N =
+    // 14336, K = 4096, M = 128: 48 -> 38 us; M = 64: 44 -> 35 us against the skinny kernel)
     if (LSMX_W4_RING && ring_ok(g)) return launch_ring<NB, 128, 64, 4>(g, s);
     return launch_w4<NB, 128, 64>(g, s);
+}
+
+// ------------------------------------------------------------------ split-K
+// A few hundred activation rows against a wide weight (M = 128, N = 14336:
+// 56 output tiles of 128 x 256 for 256 CUs) leave most CUs idle with whole-K
+// tiles, and narrower tiles make every CU re-read the whole activation
+// panel.  Instead each 128 x 256 tile is cut into 2 or 4 K slices (>= 512
+// deep, a whole group of E8M0 scale loads), one workgroup each; the fp32
+// partial tiles meet in a caller-provided workspace.  The decision depends
+// on M, N and K only (128-row tiles per batch in both forms), so the single
+// and the dual launch of one M give identical bits.
+int gemm_bf16f4_splits(int64_t M, int64_t N, int64_t K, bool /*dual*/) {
+    if (M <= LSMX_SKINNY_MAX_M) return 1;  // the GEMV and skinny kernels own these
+    const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256), cus = num_cus_w();
+    if (2 * tiles > cus) return 1;
+    for (int sp = 4; sp >= 2; sp /= 2)
+        if (tiles * sp <= cus && K % (512 * sp) == 0) return sp;
+    return 1;
+}
+
+// Workspace: the fp32 partial tiles [splits][NB][Mp][Np] (Mp = M rounded up
+// to 128 rows, Np = N rounded up to 256 columns).
+int64_t gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, bool dual) {
+    const int sp = gemm_bf16f4_splits(M, N, K, dual);
+    if (sp < 2) return 0;
+    return (int64_t)sp * (dual ? 2 : 1) * ((M + 127) / 128 * 128) * ((N + 255) / 256 * 256) * 4;
+}
+
+// C[b][m][n] = sum over slices s = 0, 1, ... of partial[s][b][m][n], in that
+// order: 4 consecutive columns per thread, one 16-byte load per slice.
+template <int CT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws, int splits, int nb,
+                                                            int64_t Mp, int64_t Np, void *c0, void *c1, int64_t ldc,
+                                                            int64_t M, int64_t N) {
+    const int64_t q4 = Np / 4;  // column quads per row
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t b = i / (M * q4), rem = i - b * (M * q4);
+    if (b >= nb) return;
+    const int64_t m = rem / q4, n = (rem - m * q4) * 4;
+    if (n >= N) return;
+    const float *p = ws + (b * Mp + m) * Np + n;
+    const int64_t slice = (int64_t)nb * Mp * Np;
+    u32x4 v = *reinterpret_cast<const u32x4 *>(p);
+    float x[4] = {u2f(v.x), u2f(v.y), u2f(v.z), u2f(v.w)};
+    for (int s = 1; s < splits; ++s) {
+        v = *reinterpret_cast<const u32x4 *>(p + s * slice);
+        x[0] += u2f(v.x);
+        x[1] += u2f(v.y);
+        x[2] += u2f(v.z);
+        x[3] += u2f(v.w);
+    }
+    void *c = b ? c1 : c0;
+    const int64_t idx = m * ldc + n;
+    if (n + 4 <= N && (((uintptr_t)c + idx * (CT == LSMX_F32 ? 4 : 2)) & (CT == LSMX_F32 ? 15 : 7)) == 0) {
+        store_c4<CT>(c, idx, x[0], x[1], x[2], x[3]);
+    } else {
+        for (int k = 0; k < 4 && n + k < N; ++k) store_c<CT>(c, idx + k, x[k]);
+    }
+}
+
+// Ring depth of the single form's split-K kernel (24 KiB per slot): 3, 4 and
+// 6 slots time within 3% of each other for M = 64 .. 256 against a 14336 x
+// 4096 weight, 4 the fastest, so the loads in flight do not set its pace.
+// The dual form's 40 KiB slots fit 3.
+#ifndef LSMX_SK_SLOTS
+#define LSMX_SK_SLOTS 4
+#endif
+template <int NB>
+static hipError_t launch_ring_splitk(GemmArgs g, int splits, hipStream_t s) {
+    constexpr int BR = 128 * NB, BN = 256;
+    const int64_t tiles = ((g.M + 127) / 128) * ((g.N + BN - 1) / BN);
+    g.splits = splits;
+    g.k_split = g.K / splits;
+    const dim3 grid((unsigned)(tiles * splits)), blk(wr::NT);
+    const int64_t Mp = (g.M + 127) / 128 * 128, Np = (g.N + BN - 1) / BN * BN;
+    const int64_t threads = NB * g.M * (Np / 4);
+    const dim3 rgrid((unsigned)((threads + 255) / 256)), rblk(256);
+#define LSMX_RS(CT)                                                                                              \
+    do {                                                                                                         \
+        hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT, BR, BN, NB == 1 ? LSMX_SK_SLOTS : 3, true, NB == 1 ? 1 : 4>), grid, blk, 0, s, g); \
+        hipLaunchKernelGGL((splitk_reduce_kernel<CT>), rgrid, rblk, 0, s, g.ws, splits, NB, Mp, Np, g.c, g.c1, \
+                           g.ldc, g.M, g.N);                                                                     \
+    } while (0)
+    if (g.c_dtype == LSMX_F32) LSMX_RS(LSMX_F32);
+    else if (g.c_dtype == LSMX_BF16) LSMX_RS(LSMX_BF16);
+    else LSMX_RS(LSMX_F16);
+#undef LSMX_RS
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
@@ -1113,6 +1242,10 @@ hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
     // test depends on M and K only, so single and dual launches agree)
     if (g.M <= LSMX_GEMV_MAX_M && 2 * g.M * g.K * 2 <= kGemvMaxLds) return launch_gemv(g, s);
     if (g.M <= LSMX_SKINNY_MAX_M && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
+    if (g.ws && ring_ok(g)) {
+        const int sp = gemm_bf16f4_splits(g.M, g.N, g.K, g.a1 != nullptr);
+        if (sp > 1) return g.a1 ? launch_ring_splitk<2>(g, sp, s) : launch_ring_splitk<1>(g, sp, s);
+    }
     return g.a1 ? launch_w4_any<2>(g, s) : launch_w4_any<1>(g, s);
 }
 

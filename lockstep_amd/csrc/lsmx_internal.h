@@ -69,6 +69,11 @@ struct GemmArgs {
     int c_dtype;
     int64_t ldc;
     int64_t M, N, K;
+    // split-K (weight-only ring kernel): K slices of k_split, fp32 partial
+    // tiles in the workspace ws
+    int splits = 1;
+    int64_t k_split = 0;
+    float *ws = nullptr;
 };
 
 struct DenseArgs {
@@ -95,6 +100,10 @@ hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
 hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_xf4(const GemmArgs &g, int a_dtype, hipStream_t s);
+// split count the weight-only GEMM uses at this shape when given a workspace
+// (1: no split), and the workspace bytes that needs (partials + counters)
+int gemm_bf16f4_splits(int64_t M, int64_t N, int64_t K, bool dual);
+int64_t gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, bool dual);
 hipError_t launch_gemm_dense(const DenseArgs &g, int dtype, int mode, hipStream_t s);
 bool dense_ring_ok(const DenseArgs &g, int dtype);
 hipError_t launch_gemm_dense_ring(const DenseArgs &g, int dtype, int mode, hipStream_t s);

@@ -295,7 +295,8 @@ LSMX_DEV void bits16(uint32_t w, uint32_t &lo, uint32_t &hi) {
     }
 }
 
-template <typename T, int SFMT>
+// ROWS = false: the column form only (lsmx_quantize_mxfp4_t of a 16-bit x).
+template <typename T, int SFMT, bool ROWS = true>
 __global__ __launch_bounds__(q2::NT) void quantize_2d_kernel(
     const T *__restrict__ x, int64_t R, int64_t C, int64_t ldx, uint8_t *__restrict__ codes_r, int64_t ld_cr,
     uint8_t *__restrict__ scale_r, int64_t ld_sr, uint8_t *__restrict__ codes_c, int64_t ld_cc,
@@ -333,6 +334,7 @@ __global__ __launch_bounds__(q2::NT) void quantize_2d_kernel(
             am = max(am, b[e] & 0x7FFFFFFFu);
             cm[e] = max(cm[e], b[e] & 0x7FFFFFFFu);
         }
+        if constexpr (!ROWS) continue;
         am = group_max<4>(am);
         const uint32_t e8 = block_e8m0(am);
         const uint32_t wd = __any(e8 == 255u) ? e2m1_pack_exact<8>(b, e8) : e2m1_pack_hw16<8>(b, e8);
@@ -651,6 +653,22 @@ static hipError_t launch_rows(const QuantArgs &a, hipStream_t s) {
 
 template <typename T, int BLOCK, bool PACKED, int SF32>
 static hipError_t launch_cols(const QuantArgs &a, hipStream_t s) {
+    // 16-bit x, 32-blocks, packed codes and E8M0 scales on whole 128 x 128
+    // tiles: the column half of the two-axis kernel (one 32-row block per
+    // wave, 64-byte code runs per column)
+    if constexpr (sizeof(T) == 2 && BLOCK == 32 && PACKED && SF32 != LSMX_SCALE_F32) {
+        const uintptr_t cp = reinterpret_cast<uintptr_t>(a.codes), sp = reinterpret_cast<uintptr_t>(a.scale);
+        if (a.K % q2::T == 0 && a.rows % q2::T == 0 && a.ldx * 2 % 16 == 0 &&
+            (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (cp & 15) == 0 && a.ld_codes % 16 == 0 &&
+            (sp & 3) == 0 && (SF32 == LSMX_SCALE_E8M0_KMAJOR || a.ld_scale % 4 == 0)) {
+            const dim3 grid((unsigned)((a.K / q2::T) * (a.rows / q2::T))), blk(q2::NT);
+            hipLaunchKernelGGL((quantize_2d_kernel<T, SF32, false>), grid, blk, 0, s, reinterpret_cast<const T *>(a.x),
+                               a.K, a.rows, a.ldx, nullptr, (int64_t)0, nullptr, (int64_t)0,
+                               reinterpret_cast<uint8_t *>(a.codes), a.ld_codes, reinterpret_cast<uint8_t *>(a.scale),
+                               a.ld_scale);
+            return hipGetLastError();
+        }
+    }
     // a.rows = cols, a.K = K for the column mode
     const int64_t gx = (a.rows + kTThreads - 1) / kTThreads;
     const int64_t nkb = a.K / BLOCK;

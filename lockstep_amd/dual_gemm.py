@@ -75,10 +75,13 @@ def dual_mxfp4(a0, a1, w_pk, w_scale, out_dtype=torch.bfloat16):
     c1 = torch.empty_like(c0)
     if M == 0 or N == 0:
         return c0, c1
-    C.call("lsmx_gemm_dual_bf16f4", a0.data_ptr(), a1.data_ptr(), a0.stride(0) if M > 1 else K,
+    nws = C.load().lsmx_gemm_bf16f4_workspace(M, N, K, 1)
+    ws = C.workspace(a0.device, nws) if nws > 0 else None
+    C.call("lsmx_gemm_bf16f4_ws", a0.data_ptr(), a1.data_ptr(), a0.stride(0) if M > 1 else K,
            w_pk.data_ptr(), w_pk.stride(0) if N > 1 else Kh, w_scale.data_ptr(),
            w_scale.stride(0) if N > 1 else K // 32, _fp4._scale_fmt(w_scale), c0.data_ptr(),
-           c1.data_ptr(), C.dtype_code(out_dtype), N, M, N, K, C.stream_of(c0))
+           c1.data_ptr(), C.dtype_code(out_dtype), N, M, N, K, ws.data_ptr() if ws is not None else None, nws,
+           C.stream_of(c0))
     return c0, c1
 
 

@@ -102,7 +102,7 @@ def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
     bf16 activations run the bf16 MFMA kernels directly.  fp32 and fp16
     activations are not narrowed: each is split exactly into bf16 terms
     (lsmx_gemm_wonly_f4), so an fp32 X gives the arithmetic of an fp32
-    matmul (BASELINE cfg1's Y = X @ dequantize_mxfp4(W)^T)."""
+    matmul (the reference's fake-quant Y = X @ dequantize_mxfp4(W)^T)."""
     M, K = a.shape
     N, Kh = w_pk.shape
     assert K == 2 * Kh and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
@@ -116,6 +116,15 @@ def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
     w_scale = _scales(w_scale, N, K // 32)
     c = torch.empty((M, N), device=a.device, dtype=out_dtype)
     if M == 0 or N == 0:
+        return c
+    if a.dtype == torch.bfloat16:
+        # with a workspace the library may split K (mid-size M against a wide W)
+        nws = C.load().lsmx_gemm_bf16f4_workspace(M, N, K, 0)
+        ws = C.workspace(a.device, nws) if nws > 0 else None
+        C.call("lsmx_gemm_bf16f4_ws", a.data_ptr(), None, a.stride(0) if M > 1 else K, w_pk.data_ptr(),
+               w_pk.stride(0) if N > 1 else Kh, w_scale.data_ptr(), w_scale.stride(0) if N > 1 else K // 32,
+               _fp4._scale_fmt(w_scale), c.data_ptr(), None, _out_code(out_dtype), N, M, N, K,
+               ws.data_ptr() if ws is not None else None, nws, C.stream_of(c))
         return c
     C.call("lsmx_gemm_wonly_f4", a.data_ptr(), _ACT[a.dtype], a.stride(0) if M > 1 else K, w_pk.data_ptr(),
            w_pk.stride(0) if N > 1 else Kh, w_scale.data_ptr(), w_scale.stride(0) if N > 1 else K // 32,

@@ -228,3 +228,35 @@ def test_kmajor_scales_give_identical_gemm(dev, mods, oracle, M, N, K):
     assert torch.equal(c_rows, c_km)
     ref = oracle.reference_gemm_packed(*[t.cpu().numpy() for t in (apk, ae8, bpk, be8)])
     assert oracle.max_rel(c_km.cpu().numpy(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 14336, 4096), (200, 1000, 2048), (256, 4096, 1024), (64, 2304, 4096)])
+def test_weight_only_split_k(dev, mods, oracle, M, N, K):
+    """Mid-size M against a wide weight splits K (lsmx_gemm_bf16f4_ws): each
+    slice's fp32 partial tile meets the others in a workspace and the last
+    workgroup of a tile adds them in slice order.  vs fp64; repeated calls
+    (the arrival counters reset themselves) and the dual form give the same
+    bits; a call at another shape in between does not disturb them."""
+    fp4, mg, dg, _ = mods
+    from lockstep_amd import _capi
+    assert _capi.load().lsmx_gemm_bf16f4_workspace(M, N, K, 0) > 0, "this shape must take the split-K path"
+    g = torch.Generator(device=dev).manual_seed(M * 7 + K)
+    a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    a1 = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    c = mg.mxfp4_gemm_bf16(a, wpk, we8, out_dtype=torch.float32)
+    rows = np.unique(np.linspace(0, M - 1, 40).astype(np.int64))
+    cols = np.arange(0, N, 3)
+    ref = oracle.reference_gemm_wonly(a.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy(),
+                                      rows=rows, cols=cols)
+    assert oracle.max_rel(c.cpu().numpy()[np.ix_(rows, cols)], ref) <= 1e-5
+    other = mg.mxfp4_gemm_bf16(a[:, :K // 2].contiguous(), wpk[:N // 2, :K // 4].contiguous(),
+                               we8[:N // 2, :K // 64].contiguous(), out_dtype=torch.float32)
+    assert other.shape == (M, N // 2)
+    assert torch.equal(mg.mxfp4_gemm_bf16(a, wpk, we8, out_dtype=torch.float32), c)
+    c0, c1 = dg.dual_mxfp4(a, a1, wpk, we8, out_dtype=torch.float32)
+    assert torch.equal(c0, c)
+    assert torch.equal(c1, mg.mxfp4_gemm_bf16(a1, wpk, we8, out_dtype=torch.float32))
+    b16 = mg.mxfp4_gemm_bf16(a, wpk, we8)
+    assert torch.equal(b16, c.to(torch.bfloat16))

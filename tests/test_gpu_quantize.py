@@ -107,7 +107,7 @@ def test_quantize_strided_rows_and_leading_dims(dev, fp4mod, oracle):
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("block", [32, 16])
 def test_quantize_transposed_axis_matches_oracle(dev, fp4mod, oracle, dtype, block):
-    for (K, N) in [(32, 1), (64, 300), (1024, 96), (4096, 257)]:
+    for (K, N) in [(32, 1), (64, 300), (1024, 96), (4096, 257), (512, 384)]:   # the last on whole 128 x 128 tiles
         if K % block:
             continue
         x = gen.normal(41 + K, (K, N), std=0.02)
