@@ -233,10 +233,10 @@ def test_kmajor_scales_give_identical_gemm(dev, mods, oracle, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(128, 14336, 4096), (200, 1000, 2048), (256, 4096, 1024), (64, 2304, 4096)])
 def test_weight_only_split_k(dev, mods, oracle, M, N, K):
     """Mid-size M against a wide weight splits K (lsmx_gemm_bf16f4_ws): each
-    slice's fp32 partial tile meets the others in a workspace and the last
-    workgroup of a tile adds them in slice order.  vs fp64; repeated calls
-    (the arrival counters reset themselves) and the dual form give the same
-    bits; a call at another shape in between does not disturb them."""
+    slice's fp32 partial tile goes to a workspace and a second kernel adds
+    the slices in slice order.  vs fp64; repeated calls and the dual form
+    give the same bits; a call at another shape in between (sharing the
+    cached workspace) does not disturb them."""
     fp4, mg, dg, _ = mods
     from lockstep_amd import _capi
     assert _capi.load().lsmx_gemm_bf16f4_workspace(M, N, K, 0) > 0, "this shape must take the split-K path"
