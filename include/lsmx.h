@@ -180,6 +180,21 @@ int lsmx_gemm_bf16f4_ws(const void *a0, const void *a1, int64_t lda, const uint8
                         const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype, int64_t ldc,
                         int64_t M, int64_t N, int64_t K, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* lsmx_gemm_bf16f4_ws without the workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same kernels and the same bits as lsmx_gemm_bf16f4_ws with a workspace;
+ * the split-K partial tiles go to a fixed 64 MiB device array of the library
+ * instead (one per GPU, held from the first call on that GPU until the process
+ * ends; its device address is looked up once per GPU on that first call).
+ * A shape whose split-K partials need more is rejected with LSMX_ERR_SHAPE
+ * (on a 256-CU gfx950 none does).  The call allocates nothing.  Every call
+ * on one GPU shares the array: calls that overlap on one GPU (different
+ * streams, or host threads without stream ordering) race. */
+int lsmx_gemm_bf16f4_noalloc(const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                             const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
+
 /* Weight-only GEMM for any activation type: C[M, N] = A[M, K] . deq(W)^T.
  * Replaces the reference's fp32 fake-quant product, Y = X @ dequantize_mxfp4(W)^T
  * (fp4.py:75-78 inside fp4_linear.py:40's fake-quant F.linear, with X left

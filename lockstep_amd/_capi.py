@@ -44,6 +44,8 @@ SIGNATURES = {
     "lsmx_gemm_bf16f4_workspace": [_i64, _i64, _i64, _int],
     "lsmx_gemm_bf16f4_ws": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp,
                             _i64, _vp],
+    "lsmx_gemm_bf16f4_noalloc": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64, _i64,
+                                 _vp],
     "lsmx_gemm_wonly_f4": [_vp, _int, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_dual_bf16f4": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64,
                               _i64, _vp],

@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 
 #include "lsmx_internal.h"
@@ -52,6 +53,53 @@ int launched(hipError_t e, const char *what) {
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int elem_size(int dt) { return dt == LSMX_F32 ? 4 : 2; }
+
+// Split-K scratch of lsmx_gemm_bf16f4_noalloc: the largest partial-tile
+// workspace the library asks for on a 256-CU gfx950 (4 K slices x 2 batches
+// x 256 tiles' worth of 128 x 256 fp32 partials = 64 MiB; the single form
+// needs at most half).
+constexpr int64_t kScratchBytes = (int64_t)64 << 20;
+
+}  // namespace
+
+// One copy per device, loaded with this file's code object and held until
+// the process ends.  Host code never passes `scratch` itself to a kernel
+// (on the host it names a stand-in, not device memory): it uses the device
+// address that scratch_of looks up.
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+std::atomic<void *> g_scratch[kMaxDev];
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the device `stream` runs on: looked up
+// with hipGetSymbolAddress once per device, with that device current.
+int scratch_of(void *stream, void **out) {
+    int dev = -1;
+    hipError_t e = stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0) return fail(LSMX_ERR_DEVICE, "scratch: no device for the stream: %s", hipGetErrorString(e));
+    if (dev >= kMaxDev) return fail(LSMX_ERR_DEVICE, "scratch: device index %d out of range", dev);
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            int cur = -1;
+            if ((e = hipGetDevice(&cur)) != hipSuccess) return fail(LSMX_ERR_DEVICE, "scratch: %s", hipGetErrorString(e));
+            if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+                return fail(LSMX_ERR_DEVICE, "scratch: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            const hipError_t e2 = cur != dev ? hipSetDevice(cur) : hipSuccess;
+            if (e != hipSuccess || !p)
+                return fail(LSMX_ERR_DEVICE, "scratch: hipGetSymbolAddress on device %d: %s", dev, hipGetErrorString(e));
+            if (e2 != hipSuccess) return fail(LSMX_ERR_DEVICE, "scratch: hipSetDevice(%d): %s", cur, hipGetErrorString(e2));
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return LSMX_OK;
+}
 
 }  // namespace
 
@@ -413,6 +461,28 @@ int lsmx_gemm_bf16f4_ws(const void *a0, const void *a1, int64_t lda, const uint8
     if ((a1 == nullptr) != (c1 == nullptr)) return fail(LSMX_ERR_ARG, "lsmx_gemm_bf16f4_ws: a1 and c1 go together");
     return w4_common("lsmx_gemm_bf16f4_ws", a0, a1, LSMX_BF16, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1,
                      c_dtype, ldc, M, N, K, stream, workspace, workspace_bytes);
+}
+
+int lsmx_gemm_bf16f4_noalloc(const void *a0, const void *a1, int64_t lda, const uint8_t *w_pk, int64_t ldw,
+                             const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {
+    const char *fn = "lsmx_gemm_bf16f4_noalloc";
+    if ((a1 == nullptr) != (c1 == nullptr)) return fail(LSMX_ERR_ARG, "%s: a1 and c1 go together", fn);
+    // the split-K partial tiles this shape needs (0: whole-K kernels, no
+    // scratch); w4_common validates everything else before any launch
+    int64_t need = 0;
+    if (M > 0 && N > 0 && K > 0 && K % 128 == 0 && M <= ((int64_t)1 << 30) && N <= ((int64_t)1 << 30))
+        need = lsmx::gemm_bf16f4_workspace(M, N, K, a1 != nullptr);
+    if (need > kScratchBytes)
+        return fail(LSMX_ERR_SHAPE, "%s: this shape needs %lld bytes of split-K scratch; the fixed scratch holds %lld",
+                    fn, (long long)need, (long long)kScratchBytes);
+    void *ws = nullptr;
+    if (need > 0) {
+        if (int r = device_guard()) return r;
+        if (int r = scratch_of(stream, &ws)) return r;
+    }
+    return w4_common(fn, a0, a1, LSMX_BF16, lda, w_pk, ldw, w_scale, ld_sw, scale_fmt, c0, c1, c_dtype, ldc, M, N, K,
+                     stream, ws, ws ? kScratchBytes : 0);
 }
 
 int lsmx_gemm_wonly_f4(const void *a, int a_dtype, int64_t lda, const uint8_t *w_pk, int64_t ldw,
