@@ -675,8 +675,12 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
                                   acc[i][j][4 * gq + 3]};
                     quad_transpose(x, q);
                     const int64_t row = prow0 + i * 32 + 8 * gq + 4 * half + q;
-                    *reinterpret_cast<u32x4 *>(pbase + row * Np + pcol0 + j * 32 + (frow & ~3)) =
-                        u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
+                    // rows past M are never read by the reduction; streaming
+                    // stores (the reduction kernel reads each value once)
+                    if (row < g.M)
+                        __builtin_nontemporal_store(u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])},
+                                                    reinterpret_cast<u32x4 *>(pbase + row * Np + pcol0 + j * 32 +
+                                                                              (frow & ~3)));
                 }
         return;
     }
@@ -899,6 +903,295 @@ __global__ __launch_bounds__(64 * sk::WK, MT <= 2 ? 4 : 2) void gemm_bf16f4_skin
     }
 }
 
+// ------------------------------------------------------------------ decode M
+static int num_cus_w();
+// Up to 16 activation rows per batch (dual: 32 virtual rows): the weight is
+// read once, in whole 256-byte row pieces, with all of a workgroup's bytes in
+// flight at once.
+//   - a workgroup owns up to R weight rows (as many as spread the weight
+//     evenly over the CUs, one workgroup each); its 8 waves split each
+//     4096-deep K pass
+//     into 512-deep slices (wave w: K = 512w .. 512w + 511, 256 bytes of
+//     every row);
+//   - at the start of a pass every wave issues its whole share: R/4 direct-
+//     to-LDS loads of 4 rows x 256 contiguous bytes, the pass's E8M0 scales
+//     (R rows x 128 E8M0 bytes, or 128 fp32 powers of two), and its
+//     activation fragments into registers;
+//     nothing is computed before they land, so a workgroup's latency is paid
+//     once per pass while the other workgroups' loads keep HBM busy;
+//   - lane (n, q) of MFMA step s (v_mfma_f32_16x16x32_bf16) reads 4 bytes
+//     (8 codes) of weight row n: LDS chunk s of a row sits at 16 * (s ^ n),
+//     which puts the 64 lanes of a ds_read_b32 on 64 distinct banks (the DMA
+//     writes lanes in order, so the swizzle is applied by choosing each
+//     lane's source chunk);
+//   - v_cvt_scalef32_pk_bf16_fp4 expands the codes to bf16 with the block
+//     scale (exact); the activation fragment of step s holds the same 8 K
+//     positions (K = 32s + 8q .. +8 of the slice);
+//   - the 8 waves' partial sums meet in LDS and are added in wave order.
+// The summation order of an output element depends on K only, so single and
+// dual launches of the same M give identical bits.
+namespace dk {
+constexpr int NW = 8, NT = 64 * NW;
+constexpr int SLICE_K = 512;          // K per wave per pass
+constexpr int PASS_K = NW * SLICE_K;  // 4096
+constexpr int ROW_B = SLICE_K / 2;    // code bytes of one row per slice
+constexpr int SC_ROW = PASS_K / 32;   // scale bytes of one row per pass
+}  // namespace dk
+
+// 16-byte global load from inline asm: its completion is waited for with an
+// explicit s_waitcnt, which counts it together with the direct-to-LDS loads.
+LSMX_DEV u32x4 gload_x4(const void *p) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+    return v;
+}
+
+// E8M0 byte -> fp32 scale without branches: 2^(e - 127), with byte 0 ->
+// 2^-127 (0x00400000) and byte 255 -> NaN (0x7FC00000), both of which are
+// (e << 23) | 2^22.
+LSMX_DEV float e8m0_scale_nb(uint32_t e) {
+    const uint32_t special = ((((e + 1u) & 0xFEu) - 1u) >> 9) & 0x00400000u;
+    return u2f((e << 23) | special);
+}
+// fp32 scale -> itself when it has an E8M0 form (a power of two in
+// [2^-127, 2^127]), else NaN, without branches.
+LSMX_DEV float f32_scale_nb(uint32_t b) {
+    const bool ok = ((b & 0x807FFFFFu) == 0u && b - 0x00800000u <= 0x7E800000u) || b == 0x00400000u;
+    return u2f(ok ? b : 0x7FC00000u);
+}
+
+// MT = 1 with R <= 32: at most 128 VGPRs, two workgroups per CU
+template <int MT, int R, int CT, bool SF32>
+__global__ __launch_bounds__(dk::NT, (R <= 32 && MT == 1) ? 2 : 1) void gemm_bf16f4_decode_kernel(GemmArgs g) {
+    using namespace dk;
+    constexpr int TN = R / 16;                   // 16-column MFMA tiles
+    constexpr int XW = R / 4;                    // weight loads per wave per pass
+    constexpr int SV = SF32 ? 4 : 1;             // 16-byte scale vectors per row per slice
+    static_assert(R % 16 == 0, "tile");
+    __shared__ __attribute__((aligned(16))) uint8_t sW[NW][R * ROW_B];
+    static_assert(sizeof(sW) >= (size_t)NW * MT * TN * 256 * 4, "reduction buffer");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n16 = lane & 15, q = lane >> 4;
+    const bool dual = g.a1 != nullptr;
+    const int64_t VM = dual ? 2 * g.M : g.M;
+    const int64_t n0 = (int64_t)blockIdx.x * g.rows_wg;
+    const int64_t nend = min(n0 + g.rows_wg, g.N);   // rows past nend read zeros
+
+    // activation rows of this lane (rows past VM repeat the last one; their
+    // outputs are not stored)
+    const uint8_t *arow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int64_t v = min((int64_t)(16 * mt + n16), VM - 1);
+        const bool second = dual && v >= g.M;
+        arow[mt] = (second ? g.a1 : g.a) + (second ? v - g.M : v) * g.lda * 2 + q * 16;
+    }
+    // scale rows of this lane's weight rows (rows past nend repeat the last one)
+    const uint8_t *srow[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+        srow[t] = reinterpret_cast<const uint8_t *>(g.sb) + min(n0 + 16 * t + n16, nend - 1) * g.ld_sb * (SF32 ? 4 : 1);
+    // weight load j covers rows 4j .. 4j + 3: lane l -> row 4j + l/16, LDS
+    // chunk l%16 holding source chunk (l%16) ^ (row & 15)
+    uint32_t w_off[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + (lane >> 4);
+        w_off[j] = (uint32_t)((lane >> 4) * g.ldb + 16 * ((lane & 15) ^ (r & 15)));
+    }
+
+    // two accumulators per tile (even and odd K-steps), so that consecutive
+    // MFMAs do not wait for each other's results; added at the end
+    v4f acc[MT][TN][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) acc[mt][t][0] = acc[mt][t][1] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#pragma nounroll
+    for (int64_t kp = 0; kp < g.K; kp += PASS_K) {
+        const int64_t k0 = kp + (int64_t)wave * SLICE_K;   // this wave's slice
+        const bool live = k0 < g.K;                         // K % 512 == 0: whole slices
+        if (kp > 0) __syncthreads();   // every wave is done with the previous pass's LDS
+        if (live) {
+            // The slice's 16 scales of each of this lane's weight rows and
+            // its activation fragments, then its weight rows.  All are asm
+            // loads counted by the explicit waits below: a compiler-visible
+            // load would get a compiler wait that counts only its own loads
+            // and so also waits for the weight loads issued after it.
+            u32x4 sv[TN][SV];
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+#pragma unroll
+                for (int v = 0; v < SV; ++v) sv[t][v] = gload_x4(srow[t] + (k0 / 32) * (SF32 ? 4 : 1) + 16 * v);
+            u32x4 af[MT][16];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int s = 0; s < 16; ++s) af[mt][s] = gload_x4(arow[mt] + (k0 + 32 * s) * 2);
+#pragma unroll
+            for (int j = 0; j < XW; ++j) {
+                const int64_t r0 = n0 + 4 * j, left = nend - r0;
+                const uint64_t bytes = left > 0 ? (uint64_t)((left - 1) * g.ldb + (g.K - k0) / 2) : 0;
+                dma_x4(w_off[j & 3], buf_rsrc(g.b + r0 * g.ldb + k0 / 2, bytes),
+                       lds_u32(&sW[wave][0]) + j * 1024);
+            }
+            // The wave reads only the LDS its own loads wrote: no barrier.
+            // Column tile t's rows are loads 4t .. 4t + 3, so its MFMAs start
+            // once they (and everything issued before them) have landed,
+            // while the later tiles' loads are still in flight.
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (TN - 1)) : "memory");
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+#pragma unroll
+                for (int v = 0; v < SV; ++v) asm volatile("" : "+v"(sv[t][v]));
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int s = 0; s < 16; ++s) asm volatile("" : "+v"(af[mt][s]));
+            // E8M0 bytes 0 and 255 need the exact conversion; any other byte
+            // is 2^(e - 127) = e << 23.  Lane (n, q) tests dword q of its
+            // row's 16 bytes, so the wave covers every byte once.
+            bool exact = SF32;
+            if constexpr (!SF32) {
+                uint32_t hit = 0;
+#pragma unroll
+                for (int t = 0; t < TN; ++t) {
+                    const uint32_t x = q == 0 ? sv[t][0].x : q == 1 ? sv[t][0].y : q == 2 ? sv[t][0].z : sv[t][0].w;
+                    hit |= ((x - 0x01010101u) & ~x) | ((0xFEFEFEFEu - x) & x);   // a 00 or an FF byte
+                }
+                exact = __builtin_amdgcn_ballot_w64((hit & 0x80808080u) != 0u) != 0;
+            }
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                if (t > 0) {
+                    // nothing moves across the wait: the tile before it
+                    // computes while this tile's rows land
+                    __builtin_amdgcn_sched_barrier(0);
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (TN - 1 - t)) : "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                float sc[16];
+                if (exact) {
+#pragma unroll
+                    for (int s = 0; s < 16; ++s)
+                        sc[s] = SF32 ? f32_scale_nb(sv[t][s >> 2][s & 3])
+                                     : e8m0_scale_nb((sv[t][0][s >> 2] >> (8 * (s & 3))) & 0xFFu);
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 16; ++s) sc[s] = u2f(((sv[t][0][s >> 2] >> (8 * (s & 3))) & 0xFFu) << 23);
+                }
+                // the tile's 16 code words in one batch of LDS reads (one
+                // latency per tile instead of one per K-step)
+                uint32_t pc[16];
+#pragma unroll
+                for (int s = 0; s < 16; ++s)
+                    pc[s] = *reinterpret_cast<const uint32_t *>(&sW[wave][(16 * t + n16) * ROW_B + 16 * (s ^ n16) + 4 * q]);
+                // dequantize four K-steps ahead of their MFMAs, into two
+                // alternating register sets: an MFMA never waits for the
+                // conversion just before it, and a conversion never
+                // overwrites the operand of an MFMA still in flight
+                v8bf wf[2][4];
+                auto dequant = [&](int g4) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int s1 = 0; s1 < 4; ++s1) {
+                        const int s = 4 * g4 + s1;
+                        const uint32_t p = pc[s];
+                        const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[s], 0);
+                        const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[s], 1);
+                        const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[s], 2);
+                        const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[s], 3);
+                        wf[g4 & 1][s1] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+                    }
+                };
+                dequant(0);
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    if (g4 < 3) dequant(g4 + 1);
+#pragma unroll
+                    for (int s1 = 0; s1 < 4; ++s1) {
+                        const int s = 4 * g4 + s1;
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            acc[mt][t][s & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                __builtin_bit_cast(v8bf, af[mt][s]), wf[g4 & 1][s1], acc[mt][t][s & 1], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+
+    // acc[mt][t][r] = D[4q + r][n16] of the 16 x 16 tile (rows: activation
+    // rows of tile mt, columns: weight rows 16t ..); the 8 waves' partial
+    // sums are added in wave order
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(&sW[0][0]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[((wave * MT + mt) * TN + t) * 256 + r * 64 + lane] = acc[mt][t][0][r] + acc[mt][t][1][r];
+    __syncthreads();
+    for (int o = threadIdx.x; o < MT * TN * 256; o += NT) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w * MT * TN * 256 + o];
+        const int p = o >> 8, e = o & 255, r = e >> 6, l = e & 63;
+        const int mt = p / TN, t = p % TN;
+        const int64_t vr = 16 * mt + 4 * (l >> 4) + r, n = n0 + 16 * t + (l & 15);
+        if (vr < VM && n < nend) {
+            const bool second = dual && vr >= g.M;
+            store_cw<CT>(second ? g.c1 : g.c, (second ? vr - g.M : vr) * g.ldc + n, v);
+        }
+    }
+}
+
+template <int R, int MT>
+static hipError_t launch_decode_r(GemmArgs g, hipStream_t s) {
+    // rows per workgroup: the weight spread evenly over the CUs, in whole
+    // 4-row loads, at most R
+    const int64_t cus = num_cus_w(), per = (g.N + cus - 1) / cus, rows = (per + 3) / 4 * 4;
+    g.rows_wg = (int)(rows > R ? R : rows < 16 ? 16 : rows);
+    const dim3 grid((unsigned)((g.N + g.rows_wg - 1) / g.rows_wg)), blk(dk::NT);
+    const bool f = g.scale_fmt == LSMX_SCALE_F32;
+#define LSMX_D(CT, F) hipLaunchKernelGGL((gemm_bf16f4_decode_kernel<MT, R, CT, F>), grid, blk, 0, s, g)
+#define LSMX_DC(F)                                                    \
+    do {                                                              \
+        if (g.c_dtype == LSMX_F32) LSMX_D(LSMX_F32, F);               \
+        else if (g.c_dtype == LSMX_BF16) LSMX_D(LSMX_BF16, F);        \
+        else LSMX_D(LSMX_F16, F);                                     \
+    } while (0)
+    if (f) LSMX_DC(true);
+    else LSMX_DC(false);
+#undef LSMX_DC
+#undef LSMX_D
+    return hipGetLastError();
+}
+
+#ifndef LSMX_DECODE_R
+#define LSMX_DECODE_R 64
+#endif
+#ifndef LSMX_DECODE_MAX_M
+#define LSMX_DECODE_MAX_M 16
+#endif
+// up to 16 virtual rows: 64 weight rows per workgroup; 17 .. 32 (the dual
+// form): 32, so that the second activation tile's registers fit
+static hipError_t launch_decode(const GemmArgs &g, hipStream_t s) {
+    const int64_t vm = g.a1 ? 2 * g.M : g.M;
+    return vm <= 16 ? launch_decode_r<LSMX_DECODE_R, 1>(g, s) : launch_decode_r<32, 2>(g, s);
+}
+
+// The decode kernel's scale loads: 16-byte aligned rows of either format
+// (the same test for both, so that E8M0 bytes and fp32 powers of two of the
+// same scales pick the same kernel and give the same bits).
+static bool decode_ok(const GemmArgs &g) {
+    return g.K % dk::SLICE_K == 0 && (reinterpret_cast<uintptr_t>(g.sb) & 15) == 0 && g.ld_sb % 16 == 0;
+}
+
 // ------------------------------------------------------------------ GEMV
 // For one or two activation rows per batch (decode) the whole cost is reading
 // W once, and the matrix cores have almost nothing to do.  This kernel reads
@@ -1037,8 +1330,9 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
     }
 }
 
+// one activation row per batch (from two rows on the decode kernel is faster)
 #ifndef LSMX_GEMV_MAX_M
-#define LSMX_GEMV_MAX_M 2
+#define LSMX_GEMV_MAX_M 1
 #endif
 constexpr int64_t kGemvMaxLds = 64 * 1024;   // activation bytes staged per workgroup
 
@@ -1241,6 +1535,7 @@ hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
     // GEMV when the dual form's 2M activation rows of K bf16 fit in LDS (the
     // test depends on M and K only, so single and dual launches agree)
     if (g.M <= LSMX_GEMV_MAX_M && 2 * g.M * g.K * 2 <= kGemvMaxLds) return launch_gemv(g, s);
+    if (g.M <= LSMX_DECODE_MAX_M && decode_ok(g)) return launch_decode(g, s);
     if (g.M <= LSMX_SKINNY_MAX_M && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
     if (g.ws && ring_ok(g)) {
         const int sp = gemm_bf16f4_splits(g.M, g.N, g.K, g.a1 != nullptr);

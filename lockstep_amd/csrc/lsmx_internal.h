@@ -74,6 +74,8 @@ struct GemmArgs {
     int splits = 1;
     int64_t k_split = 0;
     float *ws = nullptr;
+    // decode-shape weight-only kernel: weight rows per workgroup
+    int rows_wg = 0;
 };
 
 struct DenseArgs {

@@ -82,8 +82,8 @@ def cfg3_weight(dev, mods, oracle):
 
 @pytest.mark.parametrize("M", [1, 16, 128, 1024, 8192])
 def test_cfg3_weight_only_sweep(dev, mods, oracle, cfg3_weight, M):
-    """The bench's cfg3 rows: each M runs its own kernel (GEMV, skinny,
-    128 x 64 ring, 256 x 256 ring) on the full [14336, 4096] weight."""
+    """The bench's cfg3 rows: each M runs its own kernel (GEMV, decode,
+    split-K 128 x 256 ring, 256 x 256 ring) on the full [14336, 4096] weight."""
     fp4, mg, _ = mods
     wpk, we8, rpk, re8 = cfg3_weight
     g = torch.Generator(device=dev).manual_seed(3000 + M)

@@ -145,6 +145,53 @@ def test_weight_only_bf16_x_fp4(dev, mods, oracle, out_dtype, M, N, K):
         assert oracle.max_rel(got.float().cpu().numpy(), ref) <= TOL[out_dtype]
 
 
+@pytest.mark.parametrize("M,N,K", [(2, 700, 512), (3, 300, 1536), (8, 1000, 4096), (16, 520, 8192),
+                                   (16, 260, 4608), (5, 14336, 4096)])
+def test_weight_only_decode_shapes(dev, mods, oracle, M, N, K):
+    """2 <= M <= 16 with K % 512 == 0 runs the decode kernel: 512-deep slices
+    per wave, 4096-deep passes (K = 8192: two; 4608: a second pass with one
+    live slice), ragged weight rows.  fp32 output vs the fp64 oracle; E8M0
+    bytes and fp32 powers of two give the same bits; the dual form gives the
+    single form's bits for both batches."""
+    fp4, mg, dg, _ = mods
+    g = torch.Generator(device=dev).manual_seed(M * 131 + N + K)
+    a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    a1 = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    codes, s32 = fp4.quantize_mxfp4(w)
+    wpk = fp4.pack_fp4(codes)
+    we8 = fp4.scale_to_e8m0(s32)
+    c = mg.mxfp4_gemm_bf16(a, wpk, we8, out_dtype=torch.float32)
+    ref = oracle.reference_gemm_wonly(a.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy())
+    assert oracle.max_rel(c.cpu().numpy(), ref) <= 1e-5
+    assert torch.equal(mg.mxfp4_gemm_bf16(a, wpk, s32, out_dtype=torch.float32), c)
+    c0, c1 = dg.dual_mxfp4(a, a1, wpk, we8, out_dtype=torch.float32)
+    assert torch.equal(c0, c)
+    assert torch.equal(c1, mg.mxfp4_gemm_bf16(a1, wpk, we8, out_dtype=torch.float32))
+
+
+def test_weight_only_decode_nan_scale_byte(dev, mods, oracle):
+    """An E8M0 byte 255 (NaN) in one block of a weight row makes that output
+    column NaN and leaves the others as the oracle computes them (the decode
+    kernel then takes its exact scale conversion for the whole wave)."""
+    fp4, mg, _, _ = mods
+    M, N, K = 4, 300, 1024
+    g = torch.Generator(device=dev).manual_seed(77)
+    a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    bad = we8.clone()
+    bad[7, 5] = 255
+    bad[123, 31] = 255
+    c = mg.mxfp4_gemm_bf16(a, wpk, bad, out_dtype=torch.float32).cpu().numpy()
+    assert np.isnan(c[:, 7]).all() and np.isnan(c[:, 123]).all()
+    keep = np.ones(N, dtype=bool)
+    keep[[7, 123]] = False
+    ref = oracle.reference_gemm_wonly(a.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy())
+    assert not np.isnan(c[:, keep]).any()
+    assert oracle.max_rel(c[:, keep], ref[:, keep]) <= 1e-5
+
+
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 512), (128, 14336, 512), (1000, 1000, 256)])
 def test_weight_only_tile_paths(dev, mods, oracle, M, N, K):
     """Large M runs 256 x 256 tiles, mid M (cfg3's M = 128) 128 x 128 tiles:

@@ -51,7 +51,7 @@ def test_packed_gemm_non_power_of_two_scales_poison_their_outputs(dev, mods, ora
 @pytest.mark.parametrize("M", [1, 16, 256])
 @pytest.mark.parametrize("act", [torch.bfloat16, torch.float32])
 def test_weight_only_non_power_of_two_scales_poison_their_columns(dev, mods, M, act):
-    """M = 1 runs the GEMV, 16 the skinny kernel, 256 the tiled kernel (bf16)
+    """M = 1 runs the GEMV, 16 the decode kernel, 256 the tiled kernel (bf16)
     or the exact-split kernel (fp32)."""
     fp4, mg, _ = mods
     N, K = 256, 512
