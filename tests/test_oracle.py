@@ -284,6 +284,42 @@ def test_reference_gemm_brute_force_tiny(oracle):
             assert got[m, n] == s
 
 
+def test_reference_gemm_wonly_brute_force_tiny(oracle):
+    """The weight-only oracle (fp4_linear.py:40 with X left unquantized) by a
+    scalar triple loop: x * (E2M1 value * 2^(e - 127)) summed in fp64, with
+    E8M0 byte 0 (2^-127: all of weight row 1) and exponents 2^-9 .. 2^8, and
+    the rows/cols subset selection.  The activations are multiples of 1/2 in
+    [-4, 4], so within a weight row every product is a multiple of 2^-11 below
+    2^13 and every sum is exact in fp64: the comparison is equality."""
+    rng = np.random.default_rng(5)
+    M, N, K = 3, 4, 96
+    x = rng.integers(-8, 9, (M, K)).astype(np.float64) / 2.0
+    cw = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    ew = rng.integers(118, 136, (N, K // 32)).astype(np.uint8)
+    ew[1, :] = 0
+    got = oracle.reference_gemm_wonly(x, oracle.pack_fp4(cw), ew)
+    want = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            s = 0.0
+            for k in range(K):
+                e = int(ew[n, k // 32])
+                s += x[m, k] * float(oracle.E2M1_VALUES[cw[n, k]]) * (2.0 ** -127 if e == 0 else 2.0 ** (e - 127))
+            want[m, n] = s
+    assert np.array_equal(got, want)
+    rows, cols = np.array([2, 0]), np.array([3, 1])
+    assert np.array_equal(oracle.reference_gemm_wonly(x, oracle.pack_fp4(cw), ew, rows=rows, cols=cols),
+                          want[np.ix_(rows, cols)])
+    # a plausible mistake, the scale applied per K element instead of per
+    # 32-block, fails the comparison
+    wrong = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            wrong[m, n] = sum(x[m, k] * float(oracle.E2M1_VALUES[cw[n, k]]) * 2.0 ** (int(ew[n, min(k, K // 32 - 1)]) - 127)
+                              for k in range(K))
+    assert not np.array_equal(got, wrong)
+
+
 def test_reference_gemm_matches_dequantized_matmul(oracle):
     # tests/test_fp4.py:85-92 on the oracle
     a = gen.normal(11, (8, 64))
