@@ -481,7 +481,16 @@ LSMX_DEV int swz(int row) { return (row >> 1) & 7; }
 // column strip, so every weight fragment is dequantized by one wave instead
 // of four: the dequantization is VALU work that does not shrink with the
 // tile's row count).
-template <int NB, int CT, int BR, int BN, int S, bool SPLITK = false, int WGM = 4>
+// NLW loader waves issue the stage loads (all 8, or waves 0-3 only: the two
+// waves of a SIMD share its matrix core, the older one (0-3) wins issue
+// arbitration and reaches the barrier first, so the younger one's
+// instruction stream sets the stage's pace and is kept to LDS reads,
+// dequantization and MFMAs).
+template <bool V>
+struct LoaderC {
+    static constexpr bool value = V;
+};
+template <int NB, int CT, int BR, int BN, int S, bool SPLITK = false, int WGM = 4, int NLW = wr::NW>
 __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g) {
     using namespace wr;
     constexpr int RPB = BR / NB;        // A rows per batch per workgroup
@@ -489,18 +498,20 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     constexpr int TM = BR / 32 / WGM, TN = BN / 32 / WGN;   // 32 x 32 tiles per wave
     static_assert(NB == 1 || TM * 32 <= RPB, "a wave's rows lie in one batch");
     constexpr int A_SLOT = BR * A_ROW_B, W_SLOT = BN * W_ROW_B;
-    constexpr int XA = A_SLOT / 1024 / NW;       // A load instructions per wave per stage
-    constexpr int L = XA + 1;                    // + one W load (scales: one more every 8 stages)
-    constexpr int WW = BN / 32;                  // waves with a W load of their own (32 rows each)
+    constexpr int XA = A_SLOT / 1024 / NLW;      // A load instructions per loader wave per stage
+    constexpr int WW = BN / 32;                  // W load instructions per stage (32 rows each)
+    constexpr int XWL = (WW + NLW - 1) / NLW;    // W loads per loader wave (some may be empty)
+    constexpr int L = XA + XWL;                  // (scales: one more every 8 stages)
     constexpr int SWV = BN >= 64 ? BN / 64 : 1;  // distinct scale loads (64 rows each)
-    static_assert(TM >= 1 && TN >= 1 && XA >= 1 && S >= 3, "tile");
+    static_assert(TM >= 1 && TN >= 1 && XA >= 1 && S >= 3 && (A_SLOT / 1024) % NLW == 0 && NLW <= NW, "tile");
+    static_assert(NLW >= SWV, "every scale block needs a loader");
     __shared__ __attribute__((aligned(16))) uint8_t sA[S][A_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t sW[S][W_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t sS[2][BN * 16];   // [group & 1][row][16 scale bytes]
-    // landing place of the W loads of waves past WW: they read nothing (an
-    // empty buffer descriptor: every lane out of range) and write zeros here,
-    // so that every wave counts the same loads
-    __shared__ __attribute__((aligned(16))) uint8_t sNull[WW < NW ? 1024 : 16];
+    // landing place of the loader waves' W loads past WW: they read nothing
+    // (an empty buffer descriptor: every lane out of range) and write zeros
+    // here, so that every loader counts the same loads
+    __shared__ __attribute__((aligned(16))) uint8_t sNull[XWL * NLW > WW ? 1024 : 16];
 
     const int tiles_m = (int)((g.M + RPB - 1) / RPB), tiles_n = (int)((g.N + BN - 1) / BN);
     const int tile = SPLITK ? (int)blockIdx.x / g.splits : (int)blockIdx.x;
@@ -517,9 +528,10 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     const int wm = wave / WGN, wn = wave % WGN;
     const int frow = lane & 31, half = lane >> 5;
 
-    // ---- DMA addressing.  A load i of wave w covers slot rows
-    // (i*NW + w)*8 .. +7: lane -> row + lane/8, LDS chunk lane%8 holding source
-    // chunk (lane%8) ^ swz(row).  All 8 rows of one instruction lie in one batch.
+    // ---- DMA addressing (loader waves).  A load i of loader w covers slot
+    // rows (i*NLW + w)*8 .. +7: lane -> row + lane/8, LDS chunk lane%8 holding
+    // source chunk (lane%8) ^ swz(row).  All 8 rows of one instruction lie in
+    // one batch.
     const int64_t lda_b = g.lda * 2;
     const int arow_l = lane >> 3;
     // Per load: the first byte and byte count of its rows at K offset 0,
@@ -530,7 +542,7 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     uint64_t a_bytes[XA];
 #pragma unroll
     for (int i = 0; i < XA; ++i) {
-        const int r0 = (i * NW + wave) * 8;            // first slot row, wave-uniform
+        const int r0 = (i * NLW + wave) * 8;           // first slot row, wave-uniform
         const int b = NB == 2 ? r0 / RPB : 0;
         const int rb = r0 - b * RPB;                    // row inside the batch tile
         const int row = r0 + arow_l;
@@ -540,17 +552,25 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         const int64_t left = g.M - (m0 + rb), rows = left < 8 ? (left > 0 ? left : 0) : 8;
         a_bytes[i] = rows > 0 ? (uint64_t)((rows - 1) * lda_b + (g.K - kb0) * 2) : 0;
     }
-    // W: wave w < WW loads slot rows w*32 .. +31, lane -> row lane%32,
-    // 16-byte half lane/32
-    const bool w_real = wave < WW;
+    // W: load j of loader w covers slot rows (j*NLW + w)*32 .. +31 (when that
+    // is below BN), lane -> row lane%32, 16-byte half lane/32
     const uint32_t w_off = (uint32_t)((lane & 31) * g.ldb + (lane >> 5) * 16);
-    const uint8_t *w_base = g.b + (n0 + (w_real ? wave : 0) * 32) * g.ldb + kb0 / 2;
-    const int64_t w_left = w_real ? g.N - (n0 + wave * 32) : 0, w_rows = w_left < 32 ? (w_left > 0 ? w_left : 0) : 32;
-    const uint64_t w_bytes = w_rows > 0 ? (uint64_t)((w_rows - 1) * g.ldb + (g.K - kb0) / 2) : 0;
-    const uint32_t w_lds = w_real ? lds_u32(&sW[0][0]) + wave * 1024 : lds_u32(&sNull[0]);
-    const uint32_t w_slot = w_real ? W_SLOT : 0;
-    // scales: wave w loads 16 bytes of weight rows (w % SWV)*64 + lane (waves
-    // w and w + SWV write the same bytes, so every wave counts the same loads)
+    const uint8_t *w_base[XWL];
+    uint64_t w_bytes[XWL];
+    uint32_t w_lds[XWL], w_slot[XWL];
+#pragma unroll
+    for (int j = 0; j < XWL; ++j) {
+        const int wi = j * NLW + wave;
+        const bool real = wi < WW;
+        w_base[j] = g.b + (n0 + (real ? wi : 0) * 32) * g.ldb + kb0 / 2;
+        const int64_t left = real ? g.N - (n0 + wi * 32) : 0, rows = left < 32 ? (left > 0 ? left : 0) : 32;
+        w_bytes[j] = rows > 0 ? (uint64_t)((rows - 1) * g.ldb + (g.K - kb0) / 2) : 0;
+        w_lds[j] = real ? lds_u32(&sW[0][0]) + wi * 1024 : lds_u32(&sNull[0]);
+        w_slot[j] = real ? W_SLOT : 0;
+    }
+    // scales: loader w loads 16 bytes of weight rows (w % SWV)*64 + lane
+    // (loaders w and w + SWV write the same bytes, so every loader counts the
+    // same loads)
     const int s_w = wave % SWV;
     const int64_t s_rows = g.N - n0;
     const uint8_t *s_base = reinterpret_cast<const uint8_t *>(g.sb) + n0 * g.ld_sb + kb0 / 32;
@@ -567,11 +587,12 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         if (q < XA) {
             const uint64_t bytes = a_bytes[q] > 0 ? a_bytes[q] - (uint64_t)ko : 0;
             dma_x4(a_off[q], buf_rsrc(a_base[q] + ko, bytes),
-                   lds_u32(&sA[0][0]) + slot * A_SLOT + (q * NW + wave) * 1024);
+                   lds_u32(&sA[0][0]) + slot * A_SLOT + (q * NLW + wave) * 1024);
         } else {
+            const int j = q - XA;
             const int64_t kw = (int64_t)kt * W_ROW_B;
-            const uint64_t bytes = w_bytes > 0 ? w_bytes - (uint64_t)kw : 0;
-            dma_x4(w_off, buf_rsrc(w_base + kw, bytes), w_lds + slot * w_slot);
+            const uint64_t bytes = w_bytes[j] > 0 ? w_bytes[j] - (uint64_t)kw : 0;
+            dma_x4(w_off, buf_rsrc(w_base[j] + kw, bytes), w_lds[j] + slot * w_slot[j]);
         }
     };
 
@@ -584,28 +605,34 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // prologue: scales of stages 0..7, stages 0 .. S-2 in flight
-    issue_scales(0);
-#pragma unroll
-    for (int p = 0; p < S - 1; ++p)
-#pragma unroll
-        for (int q = 0; q < L; ++q) issue(p < nk ? p : nk - 1, p, q);
-
     int rowA[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) rowA[i] = wm * (TM * 32) + i * 32 + frow;
+    auto body = [&](auto loader_c) __attribute__((always_inline)) {
+    constexpr bool LOADER = decltype(loader_c)::value;
+    // prologue: scales of stages 0..7, stages 0 .. S-2 in flight
+    if constexpr (LOADER) {
+        issue_scales(0);
+#pragma unroll
+        for (int p = 0; p < S - 1; ++p)
+#pragma unroll
+            for (int q = 0; q < L; ++q) issue(p < nk ? p : nk - 1, p, q);
+    }
     for (int u = 0; u < nk; ++u) {
         const int slot = u % S;
         // this thread's loads of stage u have landed (only stages u + 1 ..
         // u + S - 2 may be outstanding, and a scale load issued before the
         // newest of them is waited for too); after the barrier everyone's
         // have, and slot (u + S - 1) % S = (u - 1) % S is no longer read
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((S - 2) * L) : "memory");
+        // (a wave that issues no loads only meets the barrier)
+        if constexpr (LOADER) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((S - 2) * L) : "memory");
+        else asm volatile("s_barrier" ::: "memory");
         const int kn = u + S - 1 < nk ? u + S - 1 : nk - 1;
         const int sn = (u + S - 1) % S;
         // scales of the next group of 8 stages, first of this stage's loads
         // (the next stage's vmcnt wait then also covers it)
-        if ((u & 7) == 6 && u + 2 < nk) issue_scales((u + 2) >> 3);
+        if constexpr (LOADER)
+            if ((u & 7) == 6 && u + 2 < nk) issue_scales((u + 2) >> 3);
         // all of the stage's LDS reads up front (one latency per stage): W
         // blocks and scales of this lane's 4 columns, then A fragments of the
         // 4 K-steps
@@ -641,9 +668,10 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
                 fw[j] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
             }
             // loads of stage u + 2, spread over the K-steps
+            if constexpr (LOADER)
 #pragma unroll
-            for (int q = 0; q < L; ++q)
-                if ((q * 4) / L == st) issue(kn, sn, q);
+                for (int q = 0; q < L; ++q)
+                    if ((q * 4) / L == st) issue(kn, sn, q);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -651,6 +679,9 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[st][i], fw[j], acc[i][j], 0, 0, 0);
         }
     }
+    };
+    if (wave < NLW) body(LoaderC<true>{});
+    else body(LoaderC<false>{});
     // no load may still be writing this workgroup's LDS when it exits
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -733,12 +764,12 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
         }
 }
 
-template <int NB, int BR, int BN, int S>
+template <int NB, int BR, int BN, int S, int WGM = 4, int NLW = wr::NW>
 static hipError_t launch_ring(const GemmArgs &g, hipStream_t s) {
     constexpr int RPB = BR / NB;
     const int tiles = (int)(((g.M + RPB - 1) / RPB) * ((g.N + BN - 1) / BN));
     const dim3 grid(tiles), blk(wr::NT);
-#define LSMX_R(CT) hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT, BR, BN, S>), grid, blk, 0, s, g)
+#define LSMX_R(CT) hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT, BR, BN, S, false, WGM, NLW>), grid, blk, 0, s, g)
     if (g.c_dtype == LSMX_F32) LSMX_R(LSMX_F32);
     else if (g.c_dtype == LSMX_BF16) LSMX_R(LSMX_BF16);
     else LSMX_R(LSMX_F16);
@@ -1432,8 +1463,14 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 #ifndef LSMX_W4_RING
 #define LSMX_W4_RING 1
 #endif
+#ifndef LSMX_RING_WGM
+#define LSMX_RING_WGM 2
+#endif
+#ifndef LSMX_RING_NLW
+#define LSMX_RING_NLW 8
+#endif
     // the ring kernel is worth it from half a wave of 256 x 256 tiles on (M = 1024, N = 14336: 224 tiles)
-    if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3>(g, s);
+    if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3, LSMX_RING_WGM, LSMX_RING_NLW>(g, s);
     if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
     if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
     // a few hundred rows: 128 x 64 tiles through a 4-slot DMA ring (N =
