@@ -618,56 +618,92 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
 #pragma unroll
             for (int q = 0; q < L; ++q) issue(p < nk ? p : nk - 1, p, q);
     }
-    for (int u = 0; u < nk; ++u) {
-        const int slot = u % S;
-        // this thread's loads of stage u have landed (only stages u + 1 ..
-        // u + S - 2 may be outstanding, and a scale load issued before the
-        // newest of them is waited for too); after the barrier everyone's
-        // have, and slot (u + S - 1) % S = (u - 1) % S is no longer read
-        // (a wave that issues no loads only meets the barrier)
+    // A stage's head: the W blocks and scales of this lane's columns and the
+    // A fragments of its first K-step; the rest of its A fragments are read
+    // one K-step ahead.  With 4 or more slots the head of stage u + 1 is read
+    // during the last K-step of stage u, so that a stage's MFMAs start right
+    // after its barrier; that needs stage u + 1 landed at the barrier of
+    // stage u, which a 3-slot ring cannot afford (measured: the wait for it
+    // costs more than the head read saves), so there the head is read after
+    // the barrier.
+    constexpr bool AHEAD = S >= 4;
+    u32x4 wblk[TN];
+    uint32_t sraw[TN];
+    v8bf fa0[TM];
+    auto read_head = [&](int uu) __attribute__((always_inline)) {
+        const int sl = uu % S;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = wn * (TN * 32) + j * 32 + frow;
+            wblk[j] = *reinterpret_cast<const u32x4 *>(&sW[sl][(wn * TN + j) * 1024 + half * 512 + frow * 16]);
+            sraw[j] = sS[(uu >> 3) & 1][col * 16 + 2 * (uu & 7) + half];
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int r = rowA[i];
+            fa0[i] = *reinterpret_cast<const v8bf *>(&sA[sl][r * A_ROW_B + (((4 * half) ^ swz(r)) << 4)]);
+        }
+    };
+    if constexpr (AHEAD) {
+        // stage 0 (and its scales) landed for every wave
         if constexpr (LOADER) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((S - 2) * L) : "memory");
         else asm volatile("s_barrier" ::: "memory");
+        read_head(0);
+    }
+    for (int u = 0; u < nk; ++u) {
+        const int slot = u % S;
+        // this thread's loads of stage u + 1 (AHEAD) or u have landed (only
+        // the later stages up to u + S - 2 may be outstanding, and a scale
+        // load issued before the newest of them is waited for too); after
+        // the barrier everyone's have, and slot (u + S - 1) % S = (u - 1) % S
+        // is no longer read (a wave that issues no loads only meets the
+        // barrier)
+        constexpr int NOUT = (AHEAD ? S - 3 : S - 2) * L;
+        if constexpr (LOADER) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NOUT) : "memory");
+        else asm volatile("s_barrier" ::: "memory");
+        if constexpr (!AHEAD) read_head(u);
         const int kn = u + S - 1 < nk ? u + S - 1 : nk - 1;
         const int sn = (u + S - 1) % S;
         // scales of the next group of 8 stages, first of this stage's loads
         // (the next stage's vmcnt wait then also covers it)
         if constexpr (LOADER)
             if ((u & 7) == 6 && u + 2 < nk) issue_scales((u + 2) >> 3);
-        // all of the stage's LDS reads up front (one latency per stage): W
-        // blocks and scales of this lane's 4 columns, then A fragments of the
-        // 4 K-steps
-        u32x4 wblk[TN];
-        uint32_t sraw[TN];
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = wn * (TN * 32) + j * 32 + frow;
-            wblk[j] = *reinterpret_cast<const u32x4 *>(&sW[slot][(wn * TN + j) * 1024 + half * 512 + frow * 16]);
-            sraw[j] = sS[(u >> 3) & 1][col * 16 + 2 * (u & 7) + half];
-        }
-        v8bf fa[4][TM];
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int r = rowA[i];
-                fa[st][i] = *reinterpret_cast<const v8bf *>(&sA[slot][r * A_ROW_B + (((4 * half + st) ^ swz(r)) << 4)]);
-            }
+        u32x4 wcur[TN];
         float sc[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) sc[j] = e8m0_scale_f32(sraw[j]);
+        for (int j = 0; j < TN; ++j) {
+            wcur[j] = wblk[j];
+            sc[j] = e8m0_scale_f32(sraw[j]);
+        }
+        v8bf fa[2][TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[0][i] = fa0[i];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             v8bf fw[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const uint32_t p = wblk[j][st];
+                const uint32_t p = wcur[j][st];
                 const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 0);
                 const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 1);
                 const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 2);
                 const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc[j], 3);
                 fw[j] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
             }
-            // loads of stage u + 2, spread over the K-steps
+            // the next K-step's A fragments, or the next stage's head (its
+            // slot landed before this stage's barrier; past the last stage it
+            // holds a re-load of the last stage, read and discarded)
+            if (st < 3) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int r = rowA[i];
+                    fa[(st + 1) & 1][i] = *reinterpret_cast<const v8bf *>(
+                        &sA[slot][r * A_ROW_B + (((4 * half + st + 1) ^ swz(r)) << 4)]);
+                }
+            } else if constexpr (AHEAD) {
+                read_head(u + 1);
+            }
+            // loads of stage u + S - 1, spread over the K-steps
             if constexpr (LOADER)
 #pragma unroll
                 for (int q = 0; q < L; ++q)
@@ -676,7 +712,7 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[st][i], fw[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[st & 1][i], fw[j], acc[i][j], 0, 0, 0);
         }
     }
     };
