@@ -269,16 +269,29 @@ __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
 // rows 32w + 8(l/16) + i, i = 0..7 (eight 16-byte loads; each instruction
 // reads four 256-byte row segments).
 //   rows:    for each of its rows a lane and the 3 other lanes of its quad
-//            hold one 32-column block: DPP max, hardware FP4 conversion
-//            (e2m1_pack_hw16), 4 bytes of codes per lane and row
-//            (64 contiguous bytes per row and instruction).
+//            hold one 32-column block: DPP max, hardware FP4 conversion,
+//            4 bytes of codes per lane and row (64 contiguous bytes per row
+//            and instruction).
 //   columns: a lane's 8 rows of a column are a quarter of its block: max
 //            over them, then over the 4 lanes l, l^16, l^32, l^48 of the
 //            wave; each lane then converts its 4 row pairs of every column
 //            with the column's scale (one dword per column), the dwords go
 //            to LDS, and after one barrier each column's 64 bytes of codes
-//            (the tile's 128 rows) are written by 4 lanes.
-// Scales are E8M0, row-major or K-major; R and C are multiples of 128.
+//            (the tile's 128 rows) are written by 4 adjacent lanes.
+// The kernel is bound by vector-ALU issue unless each element costs only a
+// few operations, so a wave whose 32 rows hold no Inf or NaN (nearly every
+// wave) takes a short path:
+//   - maxima on packed 16-bit magnitudes (unsigned order of the magnitude
+//     bits of a bf16 or fp16 is the order of |x|, with Inf and NaN on top);
+//   - the block scale from the bits of the absmax in three integer
+//     operations (block_e8m0_16);
+//   - each element widened to fp32 and multiplied by 1 - 2^-20 once, then
+//     converted along both axes by the hardware's round-to-nearest-even
+//     (tie_down16).
+// A wave with an Inf or NaN in its rows writes its outputs again with the
+// full scale rule and NaN codes (q2_convert_special).  Scales are E8M0,
+// row-major or K-major; R and C are multiples of 128.  The common path holds
+// under 96 registers, so 5 waves share each SIMD.
 namespace q2 {
 constexpr int T = 128;      // tile edge
 constexpr int NT = 256;     // threads (4 waves)
@@ -295,9 +308,232 @@ LSMX_DEV void bits16(uint32_t w, uint32_t &lo, uint32_t &hi) {
     }
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+// Lane-wise max of two pairs of unsigned 16-bit values (v_pk_max_u16).
+LSMX_DEV uint32_t pk_max16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                  __builtin_bit_cast(u16x2, b)));
+}
+
+// fp32 bits of the larger of the two 16-bit magnitudes in m.
+template <typename T>
+LSMX_DEV uint32_t wider_half(uint32_t m) {
+    if constexpr (__is_same(T, f16_t))
+        return f2u((float)__builtin_bit_cast(_Float16, (uint16_t)max(m & 0xFFFFu, m >> 16)));
+    else
+        return max(m << 16, m & 0xFFFF0000u);
+}
+
+// fp32 bits of 16-bit magnitude half H (0: low, 1: high) of m.
+template <typename T, int H>
+LSMX_DEV uint32_t half_bits(uint32_t m) {
+    uint32_t lo, hi;
+    bits16<T>(m, lo, hi);
+    return H ? hi : lo;
+}
+
+// lsmx::block_e8m0 for a block of 16-bit values, given the fp32 bits am of
+// its absmax, finite (am < 0x7F800000).  block_e8m0 raises the exponent by
+// one when amax lies within 88 fp32 ulps below a power of two (the float32
+// rounding of fp4.py's log2); a widened bf16 (fp16) value has its low 16
+// (13) bits clear, so it is never that close, and the scale exponent is the
+// biased exponent of amax minus 2, at least 25 (fp4.py's clamp of amax to
+// 1e-30 = 0x0DA24260 has biased exponent 27).  A zero block has scale 1.
+LSMX_DEV uint32_t block_e8m0_16(uint32_t am) {
+    const uint32_t e8 = max(am >> 23, 27u) - 2u;
+    return am == 0u ? 127u : e8;
+}
+
+// An element x of a 16-bit input, widened to fp32 and multiplied by
+// 1 - 2^-20 (exact for the values below: x has at most 11 significant bits,
+// a midpoint at most 3).  The product lies strictly between x and the next
+// 16-bit value toward zero: a midpoint of E2M1 at any scale (0.25 .. 5 times
+// 2^e) drops just below it, and no other value crosses one, so the
+// hardware's round-to-nearest-even of the product (v_cvt_scalef32_pk_fp4_f32)
+// is fp4.py's round-to-nearest with ties toward the smaller magnitude
+// (fp4.py:50-53).  Zeros keep their sign and Infs stay Inf.
+LSMX_DEV float tie_down16(uint32_t bits) { return u2f(bits) * u2f(0x3F7FFFF0u); }
+
+// E2M1 codes of f[0..7] / sc (sc a power of two), f[2j] and f[2j+1] in the
+// low and high nibble of byte j.
+LSMX_DEV uint32_t cvt_fp4_x8(const float (&f)[8], float sc) {
+    uint32_t w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, f[0], f[1], sc, 0);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[2], f[3], sc, 1);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[4], f[5], sc, 2);
+    return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, f[6], f[7], sc, 3);
+}
+
+// lsmx::block_e8m0 for a block of 16-bit values with any absmax: an Inf
+// block has scale 2^127 (fp4.py clamps the exponent to 127), a NaN block the
+// E8M0 NaN.
+LSMX_DEV uint32_t block_e8m0_16x(uint32_t am) {
+    return am > 0x7F800000u ? 255u : (am == 0x7F800000u ? 254u : block_e8m0_16(am));
+}
+
+// Codes of the 8 elements f (tie_down16 of 16-bit values, NaNs as they are)
+// of a block with E8M0 byte e8, Inf and NaN included: the hardware maps
+// +-Inf to +-6 (code 7 with the sign); a NaN block gives magnitude 7 with
+// the element's sign if the element is a NaN, else 0 (lsmx::e2m1_code).
+LSMX_DEV uint32_t codes8_any(const float (&f)[8], uint32_t e8) {
+    uint32_t nan_codes = 0x77777777u;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t b = f2u(f[k]);
+        nan_codes |= ((b & 0x7FFFFFFFu) > 0x7F800000u ? (b >> 31) : 0u) << (4 * k + 3);
+    }
+    const uint32_t w = cvt_fp4_x8(f, u2f(min(e8, 254u) << 23));
+    return e8 == 255u ? nan_codes : w;
+}
+
+// Element k of a 16-bit block for codes8_any: tie_down16 of its fp32 bits,
+// or the NaN as it is (so that its sign survives).
+LSMX_DEV float nudge_keep_nan(uint32_t b) {
+    return (b & 0x7FFFFFFFu) > 0x7F800000u ? u2f(b) : tie_down16(b);
+}
+
+// v_cvt_scalef32_pk_fp4_f32 into byte j of w (j a constant once unrolled).
+LSMX_DEV uint32_t cvt_fp4_pair(uint32_t w, float a, float b, float sc, int j) {
+    switch (j) {
+        case 0: return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, sc, 0);
+        case 1: return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, sc, 1);
+        case 2: return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, sc, 2);
+        default: return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, sc, 3);
+    }
+}
+
+// The conversion of a wave's 8 x 8 elements per lane along both axes, given
+// the row-block maxima am and the column maxima cmx (packed 16-bit, already
+// reduced over the wave), when its rows hold no Inf or NaN.  Rows go two at
+// a time: each element is widened and nudged once, converted with its row
+// block's scale and, paired with the element below it, with its column
+// block's scale, so only 16 widened values are live at a time.  Row codes
+// and scales go to memory, column codes and scales to LDS.
+template <typename T, int SFMT, bool ROWS>
+LSMX_DEV void q2_convert(const u32x4 (&raw)[8], const uint32_t (&am)[8], const uint32_t (&cmx)[4],
+                         uint32_t (*ccode)[17], uint32_t *cscale, int64_t r0, int64_t c0, int lane, int w,
+                         uint8_t *__restrict__ codes_r, int64_t ld_cr, uint8_t *__restrict__ scale_r, int64_t ld_sr) {
+    const int v = lane & 15, g = lane >> 4;
+    const int rl = 32 * w + 8 * g;
+    const int64_t slice = c0 / 128;
+    uint32_t e8c[8], dw[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        e8c[e] = block_e8m0_16((e & 1) ? half_bits<T, 1>(cmx[e >> 1]) : half_bits<T, 0>(cmx[e >> 1]));
+        dw[e] = 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float f[2][8];  // rows 2j and 2j+1, widened and nudged
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                uint32_t lo, hi;
+                bits16<T>(raw[2 * j + h][p], lo, hi);
+                f[h][2 * p] = tie_down16(lo);
+                f[h][2 * p + 1] = tie_down16(hi);
+            }
+            if constexpr (ROWS) {
+                const int i = 2 * j + h;
+                const uint32_t e8 = block_e8m0_16(am[i]);
+                const int64_t r = r0 + rl + i;
+                *reinterpret_cast<uint32_t *>(codes_r + r * ld_cr + (c0 + 8 * v) / 2) = cvt_fp4_x8(f[h], u2f(e8 << 23));
+                if ((v & 3) == 0) {  // the quad's block byte
+                    if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR)
+                        scale_r[(slice * ld_sr + r) * 4 + (v >> 2)] = (uint8_t)e8;
+                    else
+                        scale_r[r * ld_sr + c0 / 32 + (v >> 2)] = (uint8_t)e8;
+                }
+            }
+        }
+        // column e: rows 2j, 2j+1 into byte j (row rl in the low nibble)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dw[e] = cvt_fp4_pair(dw[e], f[0][e], f[1][e], u2f(e8c[e] << 23), j);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        ccode[8 * v + e][4 * w + g] = dw[e];
+        if (g == 0) reinterpret_cast<uint8_t *>(cscale)[4 * (8 * v + e) + w] = (uint8_t)e8c[e];
+    }
+}
+
+// The same outputs for a wave whose rows hold an Inf or NaN, with the scale
+// rule and codes of block_e8m0_16x and codes8_any.  Rare: rows and columns
+// are widened separately to keep its registers below the common path's.
+template <typename T, int SFMT, bool ROWS>
+LSMX_DEV void q2_convert_special(u32x4 (&raw)[8], const uint32_t (&am)[8], const uint32_t (&cmx)[4],
+                                 uint32_t (*ccode)[17], uint32_t *cscale, int64_t r0, int64_t c0, int lane, int w,
+                                 uint8_t *__restrict__ codes_r, int64_t ld_cr, uint8_t *__restrict__ scale_r,
+                                 int64_t ld_sr) {
+    const int v = lane & 15, g = lane >> 4;
+    const int rl = 32 * w + 8 * g;
+    const int64_t slice = c0 / 128;
+    if constexpr (ROWS) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float f[8];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                uint32_t lo, hi;
+                bits16<T>(raw[i][p], lo, hi);
+                f[2 * p] = nudge_keep_nan(lo);
+                f[2 * p + 1] = nudge_keep_nan(hi);
+            }
+            const uint32_t e8 = block_e8m0_16x(am[i]);
+            const int64_t r = r0 + rl + i;
+            *reinterpret_cast<uint32_t *>(codes_r + r * ld_cr + (c0 + 8 * v) / 2) = codes8_any(f, e8);
+            if ((v & 3) == 0) {
+                if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR)
+                    scale_r[(slice * ld_sr + r) * 4 + (v >> 2)] = (uint8_t)e8;
+                else
+                    scale_r[r * ld_sr + c0 / 32 + (v >> 2)] = (uint8_t)e8;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(raw[i]));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t e8 = block_e8m0_16x((e & 1) ? half_bits<T, 1>(cmx[e >> 1]) : half_bits<T, 0>(cmx[e >> 1]));
+        float f[8];  // this lane's 8 rows of column 8v + e
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            f[i] = nudge_keep_nan((e & 1) ? half_bits<T, 1>(raw[i][e >> 1]) : half_bits<T, 0>(raw[i][e >> 1]));
+        ccode[8 * v + e][4 * w + g] = codes8_any(f, e8);  // row rl in the low nibble
+        if (g == 0) reinterpret_cast<uint8_t *>(cscale)[4 * (8 * v + e) + w] = (uint8_t)e8;
+    }
+}
+
+// Block maxima of a wave's 8 x 8 elements per lane, on packed 16-bit
+// magnitudes: am[i] = fp32 bits of row i's block absmax (the quad's 32
+// columns), cmx = the column maxima over the wave's 32 rows (lanes l, l^16,
+// l^32, l^48), two 16-bit halves per dword.  Returns the largest am[i].
+template <typename T>
+LSMX_DEV uint32_t q2_maxima(const u32x4 (&raw)[8], uint32_t (&am)[8], uint32_t (&cmx)[4]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t m[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            m[p] = raw[i][p] & 0x7FFF7FFFu;
+            cmx[p] = i == 0 ? m[p] : pk_max16(cmx[p], m[p]);
+        }
+        am[i] = group_max<4>(wider_half<T>(pk_max16(pk_max16(m[0], m[1]), pk_max16(m[2], m[3]))));
+    }
+    uint32_t top = am[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) top = max(top, am[i]);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        cmx[p] = pk_max16(cmx[p], (uint32_t)__shfl_xor((int)cmx[p], 16, 64));
+        cmx[p] = pk_max16(cmx[p], (uint32_t)__shfl_xor((int)cmx[p], 32, 64));
+    }
+    return top;
+}
+
 // ROWS = false: the column form only (lsmx_quantize_mxfp4_t of a 16-bit x).
 template <typename T, int SFMT, bool ROWS = true>
-__global__ __launch_bounds__(q2::NT) void quantize_2d_kernel(
+__global__ __launch_bounds__(q2::NT, 5) void quantize_2d_kernel(
     const T *__restrict__ x, int64_t R, int64_t C, int64_t ldx, uint8_t *__restrict__ codes_r, int64_t ld_cr,
     uint8_t *__restrict__ scale_r, int64_t ld_sr, uint8_t *__restrict__ codes_c, int64_t ld_cc,
     uint8_t *__restrict__ scale_c, int64_t ld_sc) {
@@ -317,93 +553,37 @@ __global__ __launch_bounds__(q2::NT) void quantize_2d_kernel(
     for (int i = 0; i < 8; ++i)
         raw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (r0 + rl + i) * ldx + c0 + 8 * v));
 
-    // ---- rows: blocks of 32 columns = the 4 lanes of a quad; the column
-    // maxima are gathered on the way
-    uint32_t cm[8];
+    uint32_t am[8], cmx[4];
+    const uint32_t top = q2_maxima<T>(raw, am, cmx);
+    q2_convert<T, SFMT, ROWS>(raw, am, cmx, ccode, cscale, r0, c0, lane, w, codes_r, ld_cr, scale_r, ld_sr);
+    if (__any(top >= 0x7F800000u)) {
+        // rare: an Inf or NaN in the wave's rows.  Its outputs are written
+        // again with the full rules, from a second load of its words (from
+        // L2), so that no register stays live for this path through the
+        // common one.  The empty asm hides that the lane index and the load
+        // are the ones above: otherwise the compiler keeps the first load
+        // and every per-lane address of the common path for reuse here.
+        int lane2 = lane;
+        asm volatile("" : "+v"(lane2));
+        const int rl2 = 32 * w + 8 * (lane2 >> 4);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) cm[e] = 0;
-    const int64_t slice = c0 / 128;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        uint32_t b[8];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) bits16<T>(raw[i][p], b[2 * p], b[2 * p + 1]);
-        uint32_t am = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            am = max(am, b[e] & 0x7FFFFFFFu);
-            cm[e] = max(cm[e], b[e] & 0x7FFFFFFFu);
-        }
-        if constexpr (!ROWS) continue;
-        am = group_max<4>(am);
-        const uint32_t e8 = block_e8m0(am);
-        const uint32_t wd = __any(e8 == 255u) ? e2m1_pack_exact<8>(b, e8) : e2m1_pack_hw16<8>(b, e8);
-        const int64_t r = r0 + rl + i;
-        *reinterpret_cast<uint32_t *>(codes_r + r * ld_cr + (c0 + 8 * v) / 2) = wd;
-        // the 4 block bytes of this row's 128 columns, gathered by lane v == 0
-        const uint32_t e4 = e8 | ((uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 4) & 63) << 2, (int)e8) << 8) |
-                            ((uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 8) & 63) << 2, (int)e8) << 16) |
-                            ((uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 12) & 63) << 2, (int)e8) << 24);
-        if (v == 0) {
-            if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR)
-                reinterpret_cast<uint32_t *>(scale_r)[slice * ld_sr + r] = e4;
-            else
-                *reinterpret_cast<uint32_t *>(scale_r + r * ld_sr + c0 / 32) = e4;
-        }
-    }
-
-    // ---- columns: |x| max over the wave's 32 rows (lanes l, l^16, l^32, l^48)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        cm[e] = max(cm[e], (uint32_t)__shfl_xor((int)cm[e], 16, 64));
-        cm[e] = max(cm[e], (uint32_t)__shfl_xor((int)cm[e], 32, 64));
-    }
-    uint32_t e8c[8];
-    bool nan_blk = false;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        e8c[e] = block_e8m0(cm[e]);
-        nan_blk |= e8c[e] == 255u;
-    }
-    // the column pass re-expands the raw words instead of keeping 64
-    // widened elements live across the row pass
-#pragma unroll
-    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(raw[i]));
-    const bool exact = __any(nan_blk);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        uint32_t col[8];  // this lane's 8 rows of column 8v + e
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            uint32_t lo, hi;
-            bits16<T>(raw[i][e >> 1], lo, hi);
-            col[i] = (e & 1) ? hi : lo;
-        }
-        uint32_t dw;  // codes of rows rl .. rl+7, first row in the low nibble
-        if (exact) {
-            dw = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) dw |= e2m1_code(col[i], e8c[e]) << (4 * i);
-        } else {
-            dw = e2m1_pack_hw16<8>(col, e8c[e]);
-        }
-        ccode[8 * v + e][4 * w + g] = dw;
-    }
-    // this wave's column scales: byte w of each column's K-major dword
-    if (g == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            reinterpret_cast<uint8_t *>(cscale)[4 * (8 * v + e) + w] = (uint8_t)e8c[e];
+        for (int i = 0; i < 8; ++i)
+            raw[i] = *reinterpret_cast<const u32x4 *>(x + (r0 + rl2 + i) * ldx + c0 + 8 * (lane2 & 15));
+        q2_maxima<T>(raw, am, cmx);
+        q2_convert_special<T, SFMT, ROWS>(raw, am, cmx, ccode, cscale, r0, c0, lane2, w, codes_r, ld_cr, scale_r,
+                                          ld_sr);
     }
     __syncthreads();
     {
-        // column t / 2, half t % 2: 32 bytes of its 64 = dwords 8h .. 8h+7
-        const int col = t >> 1, h = t & 1;
-        const uint32_t *src = &ccode[col][8 * h];
-        const u32x4 q0 = u32x4{src[0], src[1], src[2], src[3]}, q1 = u32x4{src[4], src[5], src[6], src[7]};
-        uint8_t *dst = codes_c + (c0 + col) * ld_cc + r0 / 2 + 32 * h;
-        *reinterpret_cast<u32x4 *>(dst) = q0;
-        *reinterpret_cast<u32x4 *>(dst + 16) = q1;
+        // column 64k + t / 4, quarter t % 4 (16 of its 64 bytes): 4 adjacent
+        // lanes write each column's 64 bytes in one instruction
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int col = 64 * k + (t >> 2), q = t & 3;
+            const uint32_t *src = &ccode[col][4 * q];
+            *reinterpret_cast<u32x4 *>(codes_c + (c0 + col) * ld_cc + r0 / 2 + 16 * q) =
+                u32x4{src[0], src[1], src[2], src[3]};
+        }
         if (t < q2::T) {
             const uint32_t e4 = cscale[t];
             if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR)

@@ -361,6 +361,36 @@ def test_quantize_both_axes_ties_and_specials(dev, fp4mod, oracle, dtype):
     _check_2d(fp4mod, oracle, xh, dtype, dev)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_quantize_both_axes_scale_range(dev, fp4mod, oracle, dtype):
+    """Block absmaxes over the dtype's whole exponent range: 8 x 8 patches
+    of N(0,1) scaled by 2^k, so every 32-block along either axis mixes four
+    exponents.  Includes subnormal inputs, for bf16 whole tiles below
+    fp4.py's 1e-30 clamp (scale byte 25), amaxes one 16-bit ulp below a
+    power of two, and tiles near the dtype's largest finite value."""
+    R, C = 256, 512
+    rng = np.random.default_rng(23 if dtype == "bf16" else 29)
+    lo, hi = (-140, 124) if dtype == "bf16" else (-24, 13)
+    k = rng.integers(lo, hi, (R // 8, C // 8))
+    k[0:4, 0:4] = lo + 5                                   # one 32 x 32 tile entirely tiny
+    k[4:8, 8:12] = hi                                      # one tile near the top of the range
+    x = rng.standard_normal((R, C)) * np.exp2(np.repeat(np.repeat(k, 8, 0), 8, 1).astype(np.float64))
+    # amaxes one ulp below a power of two: 0.99609375 (bf16) / 0.99951171875 (fp16) * 2^j
+    below = 1.0 - (2.0 ** -8 if dtype == "bf16" else 2.0 ** -11)
+    for j, (r, c) in enumerate([(40, 70), (100, 300), (200, 33), (77, 500)]):
+        x[r, c] = below * 2.0 ** (k[r // 8, c // 8] + 3)
+    x = x.astype(np.float32)
+    xh = gen.to_bf16_bits(x) if dtype == "bf16" else x.astype(np.float16).view(np.uint16)
+    rc, rs = oracle.quantize_mxfp4(xh, 32, dtype)
+    e8 = oracle.scale_to_e8m0(rs)
+    if dtype == "bf16":
+        assert (e8 == 25).any() and e8.max() > 200
+    else:
+        assert e8.min() < 110 and e8.max() > 130
+    assert (rc & 7).max() == 7
+    _check_2d(fp4mod, oracle, xh, dtype, dev)
+
+
 def test_quantize_both_axes_falls_back_for_other_inputs(dev, fp4mod, oracle):
     """fp32 input, or sizes that are not multiples of 128, run the two
     one-axis kernels and give the same bytes."""
