@@ -250,27 +250,57 @@ __global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(
 // term runs through v_mfma_f32_32x32x16_bf16 against the exact bf16 weight.
 // The products are exact in fp32, so only the fp32 accumulation rounds, as
 // in an fp32 matmul.  Per K-step the terms are added hi, mid, lo.
-// Tile: 128 rows x 128 weight columns per workgroup of 4 waves (2 x 2, 64 x
-// 64 per wave), 64-deep K stages staged through VGPRs into a double-buffered
-// LDS tile (256 bytes of fp32 per row per stage).  The K positions are those
-// of the bf16 kernel above: at K-step s lane half h supplies X[row][32h + 8s
-// .. +8] and codes 8s .. 8s+7 of the weight's block h of the stage.
+// Tile: BR rows x BN weight columns per workgroup of 4 waves, 64-deep K
+// stages, the widest tile whose grid still fills the CUs: 64 x 128 or
+// 64 x 64 (2 x 2 waves of 32 x BN/2), or for small outputs 32 x 32 with the
+// 4 waves splitting each stage's four 16-deep K-steps (cfg1's 256 x 1024
+// output is 256 such workgroups); their partial tiles are added in wave
+// order through LDS at the end.  The split happens once per element, as
+// the activations are staged: each thread loads its 16-byte chunks two
+// stages ahead into VGPRs and, after a stage's MFMAs, writes their terms to
+// a double-buffered LDS tile of NTERM bf16 planes (128 bytes per row and
+// plane per stage).  The K positions are those of the bf16 kernel above: at
+// K-step s lane half h supplies X[row][32h + 8s .. +8] and codes 8s .. 8s+7
+// of the weight's block h of the stage.
+static int num_cus_w();
+
+// A compile-time slot index passed to a generic lambda.
+template <int Q>
+struct SlotC {
+    static constexpr int value = Q;
+};
+
 namespace xf {
-constexpr int BR = 128, BN = 128, BK = 64, NT = 256;
-constexpr int RT = 2, CTW = 2;     // 32 x 32 MFMA tiles per wave (rows, columns)
+constexpr int BK = 64, NT = 256;
+constexpr int ROW_B = BK * 2;     // bytes per row of one bf16 term plane per stage
 }  // namespace xf
 
-template <int AT, bool SF32, int CT>
+// The bf16 terms of x (fp32 bits xb): hi = tr(x), mid = tr(x - hi),
+// lo = tr(x - hi - mid), exact for |x| >= 2^-110 (there lo is at least a
+// bf16 subnormal's ulp); Inf and NaN pass through hi alone (a NaN whose
+// payload lies in the low 16 bits keeps a quiet bit).
+LSMX_DEV void split_bf16_terms(uint32_t xb, uint32_t &hb, uint32_t &mb, uint32_t &lb) {
+    const bool special = (xb & 0x7F800000u) == 0x7F800000u;
+    hb = (xb >> 16) | (special && (xb & 0xFFFFu) ? 0x40u : 0u);
+    const float r1 = special ? 0.0f : u2f(xb) - u2f(hb << 16);
+    mb = f2u(r1) >> 16;
+    lb = f2u(r1 - u2f(mb << 16)) >> 16;
+}
+
+template <int AT, bool SF32, int CT, int BR, int BN, int KS>
 __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
     using namespace xf;
     constexpr int ES = AT == LSMX_F32 ? 4 : 2;        // activation bytes
     constexpr int NTERM = AT == LSMX_F32 ? 3 : 2;     // bf16 terms per activation
-    constexpr int ROW_B = BK * ES;                    // bytes per row per stage
-    constexpr int CPR = ROW_B / 16;                   // 16-byte chunks per row (16 or 8)
-    constexpr int XA = BR * CPR / NT;                 // A chunks per thread per stage
-    constexpr int XW = BN * 2 / NT;                   // W chunks per thread per stage (1)
-    __shared__ __attribute__((aligned(16))) uint8_t sA[2][BR * ROW_B];   // 2 x 32 / 16 KiB
-    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * 32];      // [half][col][16 B]
+    constexpr int WM = KS == 1 ? 2 : 1, WN = KS == 1 ? 2 : 1;  // wave grid over the tile
+    static_assert(WM * WN * KS == 4 && BR == 32 * WM, "4 waves: 2 x 2 tiles, or one tile split 4 ways along K");
+    constexpr int CTW = BN / 32 / WN;                 // 32-column MFMA tiles per wave
+    constexpr int EPC = 16 / ES;                      // activations per 16-byte source chunk (4 or 8)
+    constexpr int CPR = BK / EPC;                     // source chunks per row per stage (16 or 8)
+    constexpr int XA = BR * CPR / NT;                 // source chunks per thread per stage (4 or 2)
+    constexpr int WCH = BN * 2;                       // 16-byte W chunks per stage
+    __shared__ __attribute__((aligned(16))) uint8_t sX[2][NTERM][BR * ROW_B];  // 2 x 3 x 8 KiB (fp32)
+    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * 32];            // [half][col][16 B]
     __shared__ uint32_t sS[2][BN];
 
     const int tiles_m = (int)((g.M + BR - 1) / BR), tiles_n = (int)((g.N + BN - 1) / BN);
@@ -278,153 +308,170 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
     tile_coords_w(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BR, n0 = (int64_t)tn * BN;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = KS == 1 ? wave >> 1 : 0, wn = KS == 1 ? wave & 1 : 0;
+    const int wk = KS == 1 ? 0 : wave;                // this wave's K-steps: wk, wk + KS, ... of each stage
     const int frow = lane & 31, half = lane >> 5;
     const int nk = (int)(g.K / BK);
 
-    // 16-byte chunk c of row r sits at chunk c ^ swz(r) of the LDS row; the
-    // swizzle moves whole 32-byte pairs for fp32 (a fragment is two chunks)
-    auto swz = [](int r) { return ES == 4 ? (a_swz(r) << 1) : a_swz(r); };
+    // source chunk q = i * NT + t: row q / CPR, activations EPC * (q % CPR)
+    // .. +EPC, i.e. 2 * EPC bytes of each term plane at byte 2 * EPC * (q %
+    // CPR) of the row, whose 16-byte chunk sits at chunk ^ a_swz(row)
     const uint8_t *ga[XA];
-    int a_off[XA];
+    int x_off[XA];
 #pragma unroll
     for (int i = 0; i < XA; ++i) {
         const int q = i * NT + t;
         const int row = q / CPR, c = q % CPR;
         ga[i] = g.a + min(m0 + row, g.M - 1) * g.lda * ES + c * 16;
-        a_off[i] = row * ROW_B + ((c ^ swz(row)) << 4);
+        const int pb = 2 * EPC * c;  // byte in the plane row
+        x_off[i] = row * ROW_B + (((pb >> 4) ^ a_swz(row)) << 4) + (pb & 15);
     }
-    const uint8_t *gw[XW];
-    int w_off[XW];
-#pragma unroll
-    for (int i = 0; i < XW; ++i) {
-        const int q = i * NT + t;
-        const int row = q >> 1, h = q & 1;
-        gw[i] = g.b + min(n0 + row, g.N - 1) * g.ldb + h * 16;
-        w_off[i] = h * (BN * 16) + row * 16;
-    }
+    const int wq = t < WCH ? t : 0;  // W chunk of this thread (threads >= WCH load none)
+    const uint8_t *gw = g.b + min(n0 + (wq >> 1), g.N - 1) * g.ldb + (wq & 1) * 16;
+    const int w_off = (wq & 1) * (BN * 16) + (wq >> 1) * 16;
     const int64_t s_row = min(n0 + (t % BN), g.N - 1) * g.ld_sb;
 
-    u32x4 ra[XA], rw[XW];
-    uint32_t rs;
-    auto gload = [&](int kt) {
+    // two register slots of staged loads: stage k lives in slot k % 2 from
+    // its load (issued two stages ahead) until its terms go to LDS
+    u32x4 ra[2][XA], rw[2];
+    uint32_t rs[2];
+    auto gload = [&](int kt, auto slot) {
+        constexpr int q = decltype(slot)::value;
 #pragma unroll
-        for (int i = 0; i < XA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(ga[i] + (int64_t)kt * ROW_B);
-#pragma unroll
-        for (int i = 0; i < XW; ++i) rw[i] = *reinterpret_cast<const u32x4 *>(gw[i] + (int64_t)kt * 32);
-        rs = load_scale2<SF32>(g.sb, s_row + (int64_t)kt * 2);
+        for (int i = 0; i < XA; ++i) ra[q][i] = *reinterpret_cast<const u32x4 *>(ga[i] + (int64_t)kt * BK * ES);
+        if (t < WCH) rw[q] = *reinterpret_cast<const u32x4 *>(gw + (int64_t)kt * 32);
+        rs[q] = load_scale2<SF32>(g.sb, s_row + (int64_t)kt * 2);
     };
-    auto swrite = [&](int buf) {
+    auto swrite = [&](int buf, auto slot) {
+        constexpr int q = decltype(slot)::value;
 #pragma unroll
-        for (int i = 0; i < XA; ++i) *reinterpret_cast<u32x4 *>(&sA[buf][a_off[i]]) = ra[i];
+        for (int i = 0; i < XA; ++i) {
+            if constexpr (ES == 4) {
+                uint32_t tb[3][4];
 #pragma unroll
-        for (int i = 0; i < XW; ++i) *reinterpret_cast<u32x4 *>(&sW[buf][w_off[i]]) = rw[i];
-        if (t < BN) sS[buf][t] = rs;
+                for (int e = 0; e < 4; ++e) split_bf16_terms(ra[q][i][e], tb[0][e], tb[1][e], tb[2][e]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    *reinterpret_cast<u32x2 *>(&sX[buf][p][x_off[i]]) =
+                        u32x2{tb[p][0] | (tb[p][1] << 16), tb[p][2] | (tb[p][3] << 16)};
+            } else {
+                uint32_t hw[4], mw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    uint32_t h0, m0_, l0, h1, m1, l1;
+                    split_bf16_terms(f2u((float)__builtin_bit_cast(_Float16, (uint16_t)(ra[q][i][e] & 0xFFFFu))), h0, m0_, l0);
+                    split_bf16_terms(f2u((float)__builtin_bit_cast(_Float16, (uint16_t)(ra[q][i][e] >> 16))), h1, m1, l1);
+                    hw[e] = h0 | (h1 << 16);
+                    mw[e] = m0_ | (m1 << 16);
+                }
+                *reinterpret_cast<u32x4 *>(&sX[buf][0][x_off[i]]) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4 *>(&sX[buf][1][x_off[i]]) = u32x4{mw[0], mw[1], mw[2], mw[3]};
+            }
+        }
+        if (t < WCH) *reinterpret_cast<u32x4 *>(&sW[buf][w_off]) = rw[q];
+        if (t < BN) sS[buf][t] = rs[q];
     };
 
-    v16f acc[RT][CTW];
+    v16f acc[CTW];
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
+    for (int j = 0; j < CTW; ++j)
 #pragma unroll
-        for (int j = 0; j < CTW; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
 
-    gload(0);
-    swrite(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
+    // stage kt from LDS buffer kt % 2; stage kt + 1 (in slot `slot`) goes
+    // to the other buffer and stage kt + 3 is loaded into the freed slot
+    auto step = [&](int kt, auto slot) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
-        v8bf fw[CTW][4];
+        constexpr int NS = 4 / KS;                    // K-steps of 16 per wave per stage
+        v8bf fw[CTW][NS];
 #pragma unroll
         for (int j = 0; j < CTW; ++j) {
-            const int col = wn * 64 + j * 32 + frow;
+            const int col = wn * (BN / WN) + j * 32 + frow;
             const u32x4 pw = *reinterpret_cast<const u32x4 *>(&sW[buf][half * (BN * 16) + col * 16]);
             const float sc = e8m0_scale_f32((sS[buf][col] >> (8 * half)) & 0xFF);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 0);
-                const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 1);
-                const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 2);
-                const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw[s], sc, 3);
-                fw[j][s] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+            for (int ss = 0; ss < NS; ++ss) {
+                const uint32_t cw = KS == 1 ? pw[ss] : pw[wk];
+                const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, sc, 0);
+                const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, sc, 1);
+                const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, sc, 2);
+                const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(cw, sc, 3);
+                fw[j][ss] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
             }
         }
+        const int row = wm * 32 + frow;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            v8bf fa[RT][NTERM];
+        for (int ss = 0; ss < NS; ++ss) {
+            const int s = wk + KS * ss;
+            v8bf fa[NTERM];
 #pragma unroll
-            for (int i = 0; i < RT; ++i) {
-                const int row = wm * 64 + i * 32 + frow;
-                float x[8];
-                if constexpr (ES == 4) {
-                    const int c = 2 * (4 * half + s);   // fp32 chunks 2c', 2c'+1: X[row][32h + 8s .. +8]
-                    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(&sA[buf][row * ROW_B + ((c ^ swz(row)) << 4)]);
-                    const u32x4 v1 = *reinterpret_cast<const u32x4 *>(&sA[buf][row * ROW_B + (((c + 1) ^ swz(row)) << 4)]);
-                    x[0] = u2f(v0.x); x[1] = u2f(v0.y); x[2] = u2f(v0.z); x[3] = u2f(v0.w);
-                    x[4] = u2f(v1.x); x[5] = u2f(v1.y); x[6] = u2f(v1.z); x[7] = u2f(v1.w);
-                } else {
-                    const int c = 4 * half + s;
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(&sA[buf][row * ROW_B + ((c ^ swz(row)) << 4)]);
-                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+            for (int p = 0; p < NTERM; ++p)
+                fa[p] = *reinterpret_cast<const v8bf *>(&sX[buf][p][row * ROW_B + (((4 * half + s) ^ a_swz(row)) << 4)]);
 #pragma unroll
-                    for (int p = 0; p < 4; ++p) {
-                        x[2 * p] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[p] & 0xFFFFu));
-                        x[2 * p + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[p] >> 16));
-                    }
-                }
-                v8bf hi, mid, lo;
+            for (int j = 0; j < CTW; ++j)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    // truncation split: hi keeps the top 8 significant bits,
-                    // mid the next 8, lo the rest (exact for |x| >= 2^-110,
-                    // where lo is at least a bf16 subnormal's ulp); inf and
-                    // NaN pass through hi alone
-                    const uint32_t xb = f2u(x[e]);
-                    const bool special = (xb & 0x7F800000u) == 0x7F800000u;
-                    const uint32_t hb = (xb >> 16) | (special && (xb & 0xFFFFu) ? 0x40u : 0u);
-                    const float r1 = special ? 0.0f : x[e] - u2f(hb << 16);
-                    const uint32_t mb = f2u(r1) >> 16;
-                    const float r2 = r1 - u2f(mb << 16);
-                    hi[e] = __builtin_bit_cast(__bf16, (uint16_t)hb);
-                    mid[e] = __builtin_bit_cast(__bf16, (uint16_t)mb);
-                    lo[e] = __builtin_bit_cast(__bf16, (uint16_t)(f2u(r2) >> 16));
-                }
-                fa[i][0] = hi;
-                fa[i][1] = mid;
-                if constexpr (NTERM == 3) fa[i][NTERM - 1] = lo;
-            }
-#pragma unroll
-            for (int i = 0; i < RT; ++i)
-#pragma unroll
-                for (int j = 0; j < CTW; ++j)
-#pragma unroll
-                    for (int p = 0; p < NTERM; ++p)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][p], fw[j][s], acc[i][j], 0, 0, 0);
+                for (int p = 0; p < NTERM; ++p)
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p], fw[j][ss], acc[j], 0, 0, 0);
         }
-        if (kt + 1 < nk) swrite(buf ^ 1);
+        if (kt + 1 < nk) swrite(buf ^ 1, slot);
+        if (kt + 3 < nk) gload(kt + 3, slot);
         __syncthreads();
+    };
+    constexpr SlotC<0> S0{};
+    constexpr SlotC<1> S1{};
+    gload(0, S0);
+    swrite(0, S0);
+    if (1 < nk) gload(1, S1);
+    if (2 < nk) gload(2, S0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, S1);                   // stage kt + 1 sits in slot 1
+        if (kt + 1 < nk) step(kt + 1, S0);
     }
 
+    if constexpr (KS > 1) {
+        // waves 1 .. KS-1 hand their partial tiles to wave 0 through LDS
+        // (the staging planes are free after the last barrier), which adds
+        // them in wave order
+        float *red = reinterpret_cast<float *>(&sX[0][0][0]);
+        static_assert(CTW == 1 && (KS - 1) * 16 * 64 * 4 <= (int)sizeof(sX), "reduction buffer");
+        if (wk > 0) {
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int j = 0; j < CTW; ++j) {
-            const int64_t col = n0 + wn * 64 + j * 32 + frow;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int64_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-                if (row < g.M && col < g.N) store_cw<CT>(g.c, row * g.ldc + col, acc[i][j][e]);
-            }
+            for (int e = 0; e < 16; ++e) red[((wk - 1) * 16 + e) * 64 + lane] = acc[0][e];
         }
+        __syncthreads();
+        if (wk > 0) return;
+#pragma unroll
+        for (int w2 = 0; w2 < KS - 1; ++w2)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[0][e] += red[(w2 * 16 + e) * 64 + lane];
+    }
+#pragma unroll
+    for (int j = 0; j < CTW; ++j) {
+        const int64_t col = n0 + wn * (BN / WN) + j * 32 + frow;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t row = m0 + wm * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+            if (row < g.M && col < g.N) store_cw<CT>(g.c, row * g.ldc + col, acc[j][e]);
+        }
+    }
 }
 
 hipError_t launch_gemm_xf4(const GemmArgs &g, int a_dtype, hipStream_t s) {
-    const int tiles = (int)(((g.M + xf::BR - 1) / xf::BR) * ((g.N + xf::BN - 1) / xf::BN));
-    const dim3 grid(tiles), blk(xf::NT);
+    // the widest tile whose grid still fills the CUs: 64 x 128, 64 x 64, or
+    // 32 x 32 tiles split four ways along K
+    auto tiles = [&](int br, int bn) { return ((g.M + br - 1) / br) * ((g.N + bn - 1) / bn); };
+    const int cus = num_cus_w();
+    const int shape = tiles(64, 128) >= cus ? 0 : (tiles(64, 64) >= cus ? 1 : 2);
+    const dim3 grid((unsigned)(shape == 0 ? tiles(64, 128) : shape == 1 ? tiles(64, 64) : tiles(32, 32))),
+        blk(xf::NT);
     const bool f = g.scale_fmt == LSMX_SCALE_F32;
-#define LSMX_X(AT, F, CT) hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT>), grid, blk, 0, s, g)
+#define LSMX_X(AT, F, CT)                                                                           \
+    do {                                                                                            \
+        if (shape == 0) hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT, 64, 128, 1>), grid, blk, 0, s, g); \
+        else if (shape == 1) hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT, 64, 64, 1>), grid, blk, 0, s, g); \
+        else hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT, 32, 32, 4>), grid, blk, 0, s, g);       \
+    } while (0)
 #define LSMX_XC(AT, F)                                           \
     do {                                                         \
         if (g.c_dtype == LSMX_F32) LSMX_X(AT, F, LSMX_F32);      \

@@ -307,3 +307,41 @@ def test_weight_only_split_k(dev, mods, oracle, M, N, K):
     assert torch.equal(c1, mg.mxfp4_gemm_bf16(a1, wpk, we8, out_dtype=torch.float32))
     b16 = mg.mxfp4_gemm_bf16(a, wpk, we8)
     assert torch.equal(b16, c.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("adt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(256, 1024, 1024), (1000, 2100, 512), (4096, 4096, 256), (512, 2048, 256),
+                                   (1, 300, 128), (70, 130, 384)])
+def test_weight_only_wide_activations(dev, mods, oracle, adt, M, N, K):
+    """fp32 and fp16 activations (lsmx_gemm_wonly_f4): each activation is
+    split exactly into bf16 terms, so Y = X . deq(W)^T has the arithmetic of
+    an fp32 matmul (fp4.py:75-78 dequantization, fp4_linear.py:40's
+    fake-quant forward with an unquantized X).  All three tile shapes on
+    256 CUs (64 x 128; 64 x 64 at 512 x 2048; 32 x 32 split four ways along
+    K for the smaller outputs), ragged edges; fp32 output <=
+    1e-5 vs fp64; bf16 output is the RNE of the fp32 one; fp32 scales give
+    the same bits as E8M0 bytes; a row holding +-Inf gives the oracle's
+    non-finite pattern."""
+    fp4, mg, _, _ = mods
+    g = torch.Generator(device=dev).manual_seed(M + 3 * N + K)
+    x = torch.randn((M, K), device=dev, generator=g)
+    x[:, ::7] *= 1e-3                                            # terms mid and lo carry real bits
+    x = x.to(adt)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    _, ws32 = fp4.quantize_mxfp4(w)
+    c = mg.mxfp4_gemm_bf16(x, wpk, we8, out_dtype=torch.float32)
+    ref = oracle.reference_gemm_wonly(x.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy())
+    assert oracle.max_rel(c.cpu().numpy(), ref) <= 1e-5
+    assert torch.equal(mg.mxfp4_gemm_bf16(x, wpk, ws32, out_dtype=torch.float32), c)
+    assert torch.equal(mg.mxfp4_gemm_bf16(x, wpk, we8), c.to(torch.bfloat16))
+    if M > 1:
+        xs = x.clone()
+        xs[M // 2, K // 3] = float("inf")
+        xs[M - 1, 5] = float("-inf")
+        cs = mg.mxfp4_gemm_bf16(xs, wpk, we8, out_dtype=torch.float32).cpu().numpy()
+        rs = oracle.reference_gemm_wonly(xs.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy())
+        assert np.array_equal(np.isnan(cs), np.isnan(rs)) and np.array_equal(np.isposinf(cs), np.isposinf(rs))
+        assert np.array_equal(np.isneginf(cs), np.isneginf(rs))
+        fin = np.isfinite(rs)
+        assert oracle.max_rel(cs[fin], rs[fin]) <= 1e-5
