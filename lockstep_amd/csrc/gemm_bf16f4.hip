@@ -264,12 +264,6 @@ __global__ __launch_bounds__(w4::NT, BR == 256 ? 1 : 2) void gemm_bf16f4_kernel(
 // of the weight's block h of the stage.
 static int num_cus_w();
 
-// A compile-time slot index passed to a generic lambda.
-template <int Q>
-struct SlotC {
-    static constexpr int value = Q;
-};
-
 namespace xf {
 constexpr int BK = 64, NT = 256;
 constexpr int ROW_B = BK * 2;     // bytes per row of one bf16 term plane per stage

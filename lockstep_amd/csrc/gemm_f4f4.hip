@@ -88,16 +88,6 @@ LSMX_DEV void stage_barrier() {
     else asm volatile("s_barrier" ::: "memory");
 }
 
-// compile-time arguments of the stage code: ring slot, loader wave or not
-template <int V>
-struct SlotC {
-    static constexpr int value = V;
-};
-template <bool V>
-struct BoolC {
-    static constexpr bool value = V;
-};
-
 namespace f4 {
 constexpr int BM = 256, BN = 256;
 constexpr int GROUP_M = 4;

@@ -5,6 +5,17 @@
 
 namespace lsmx {
 
+// Compile-time arguments passed to the generic lambdas of the pipelined
+// kernels: a ring or register slot, a loader wave or not.
+template <int V>
+struct SlotC {
+    static constexpr int value = V;
+};
+template <bool V>
+struct BoolC {
+    static constexpr bool value = V;
+};
+
 struct QuantArgs {
     const void *x;
     int x_dtype;
