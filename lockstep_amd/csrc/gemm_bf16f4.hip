@@ -800,32 +800,48 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     const int64_t cbase = n0 + wn * (TN * 32);
     if (((reinterpret_cast<uintptr_t>(cb) & 15) == 0) && g.ldc % 4 == 0 && g.ldc < ((int64_t)1 << 26) &&
         rbase + TM * 32 <= g.M && cbase + TN * 32 <= g.N) {
-        // this wave's block lies inside C: a 4x4 transpose inside
-        // each quad of lanes gives every lane 4 consecutive columns of one
-        // row, one 8-byte (16-bit C) or 16-byte (fp32 C) store each, at a
-        // wave-uniform row pointer plus a fixed lane offset
+        // this wave's block lies inside C: a 4x4 transpose inside each quad
+        // of lanes gives every lane 4 consecutive columns of one row (fp32
+        // C: one 16-byte store each); for 16-bit C lanes 4 apart then trade
+        // halves so each lane stores 8 columns (pack16_rows8).  Every store
+        // is a wave-uniform row pointer plus a fixed lane offset.
         constexpr int EB = CT == LSMX_F32 ? 4 : 2;
         const int q = frow & 3;
         const uint8_t *cw = reinterpret_cast<const uint8_t *>(cb) + (rbase * g.ldc + cbase) * EB;
-        const uint32_t loff = (uint32_t)(((4 * half + q) * g.ldc + (frow & ~3)) * EB);
+        if constexpr (CT == LSMX_F32) {
+            const uint32_t loff = (uint32_t)(((4 * half + q) * g.ldc + (frow & ~3)) * EB);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-                uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 8 * gq) * g.ldc * EB;
+                for (int gq = 0; gq < 4; ++gq) {
+                    uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 8 * gq) * g.ldc * EB;
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
-                                  acc[i][j][4 * gq + 3]};
-                    uint8_t *p = crow + loff + j * 32 * EB;
-                    if constexpr (CT == LSMX_F32) {
+                    for (int j = 0; j < TN; ++j) {
+                        float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                      acc[i][j][4 * gq + 3]};
                         quad_transpose(x, q);
-                        *reinterpret_cast<u32x4 *>(p) = u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
-                    } else {
-                        *reinterpret_cast<u32x2 *>(p) = quad_pack16<CT>(x, q);
+                        *reinterpret_cast<u32x4 *>(crow + loff + j * 32 * EB) =
+                            u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
                     }
                 }
-            }
+        } else {
+            const bool odd = (frow & 4) != 0;
+            const uint32_t loff = (uint32_t)(((4 * half + q + (odd ? 8 : 0)) * g.ldc + (frow & ~7)) * EB);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 16 * p) * g.ldc * EB;
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const float x0[4] = {acc[i][j][8 * p], acc[i][j][8 * p + 1], acc[i][j][8 * p + 2],
+                                             acc[i][j][8 * p + 3]};
+                        const float x1[4] = {acc[i][j][8 * p + 4], acc[i][j][8 * p + 5], acc[i][j][8 * p + 6],
+                                             acc[i][j][8 * p + 7]};
+                        *reinterpret_cast<u32x4 *>(crow + loff + j * 32 * EB) = pack16_rows8<CT>(x0, x1, q, odd);
+                    }
+                }
+        }
         return;
     }
 #pragma unroll

@@ -532,25 +532,42 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             constexpr int EB = CT == LSMX_F32 ? 4 : 2;  // bytes per output element
             const uint8_t *cw = reinterpret_cast<const uint8_t *>(g.c) +
                                 ((m0 + wm * (TM * 32)) * g.ldc + n0 + wn * (TN * 32)) * EB;
-            const uint32_t loff = (uint32_t)(((4 * half + q) * g.ldc + (frow & ~3)) * EB);
+            if constexpr (CT == LSMX_F32) {
+                const uint32_t loff = (uint32_t)(((4 * half + q) * g.ldc + (frow & ~3)) * EB);
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int gq = 0; gq < 4; ++gq) {
-                    uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 8 * gq) * g.ldc * EB;
+                    for (int gq = 0; gq < 4; ++gq) {
+                        uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 8 * gq) * g.ldc * EB;
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) {
-                        float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
-                                      acc[i][j][4 * gq + 3]};
-                        uint8_t *p = crow + loff + j * 32 * EB;
-                        if constexpr (CT == LSMX_F32) {
+                        for (int j = 0; j < TN; ++j) {
+                            float x[4] = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                          acc[i][j][4 * gq + 3]};
                             quad_transpose(x, q);
-                            *reinterpret_cast<u32x4 *>(p) = u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
-                        } else {
-                            *reinterpret_cast<u32x2 *>(p) = quad_pack16<CT>(x, q);
+                            *reinterpret_cast<u32x4 *>(crow + loff + j * 32 * EB) =
+                                u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
                         }
                     }
-                }
+            } else {
+                // 16 bytes per lane (pack16_rows8): rows 16p + 4*half + q
+                // and +8, 8 columns at (frow & ~7)
+                const bool odd = (frow & 4) != 0;
+                const uint32_t loff = (uint32_t)(((4 * half + q + (odd ? 8 : 0)) * g.ldc + (frow & ~7)) * EB);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        uint8_t *crow = const_cast<uint8_t *>(cw) + (i * 32 + 16 * p) * g.ldc * EB;
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) {
+                            const float x0[4] = {acc[i][j][8 * p], acc[i][j][8 * p + 1], acc[i][j][8 * p + 2],
+                                                 acc[i][j][8 * p + 3]};
+                            const float x1[4] = {acc[i][j][8 * p + 4], acc[i][j][8 * p + 5], acc[i][j][8 * p + 6],
+                                                 acc[i][j][8 * p + 7]};
+                            *reinterpret_cast<u32x4 *>(crow + loff + j * 32 * EB) = pack16_rows8<CT>(x0, x1, q, odd);
+                        }
+                    }
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
