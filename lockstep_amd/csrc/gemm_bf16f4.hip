@@ -1560,7 +1560,7 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 #define LSMX_RING_WGM 2
 #endif
 #ifndef LSMX_RING_NLW
-#define LSMX_RING_NLW 8
+#define LSMX_RING_NLW 4
 #endif
     // the ring kernel is worth it from half a wave of 256 x 256 tiles on (M = 1024, N = 14336: 224 tiles)
     if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3, LSMX_RING_WGM, LSMX_RING_NLW>(g, s);
