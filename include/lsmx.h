@@ -162,12 +162,13 @@ int lsmx_gemm_bf16f4(const void *a, int64_t lda, const uint8_t *w_pk, int64_t ld
  * the library does not split this shape.  It splits K in 2 or 4 slices when
  * the whole-K 128 x 256 output tiles would fill less than half of the CUs
  * (a few hundred activation rows against a wide weight, e.g. M = 128
- * against N = 14336); the decision depends on M, N and K only. */
+ * against N = 14336: 128 x 128 tiles in 2 slices); the decision depends on
+ * M, N and K only. */
 int64_t lsmx_gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, int dual);
 
 /* lsmx_gemm_bf16f4 (a1 = c1 = NULL) or lsmx_gemm_dual_bf16f4 (both set)
  * with a caller-provided device workspace, which lets the library split K
- * (lsmx_gemm_bf16f4_workspace): each K slice of a 128 x 256 output tile is
+ * (lsmx_gemm_bf16f4_workspace): each K slice of a 128-row output tile is
  * one workgroup that writes an fp32 partial tile to the workspace, and a
  * second kernel on the same stream adds the slices in slice order (a fixed
  * order: repeated calls, and the single and dual forms, give identical

@@ -1576,26 +1576,45 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 // A few hundred activation rows against a wide weight (M = 128, N = 14336:
 // 56 output tiles of 128 x 256 for 256 CUs) leave most CUs idle with whole-K
 // tiles, and narrower tiles make every CU re-read the whole activation
-// panel.  Instead each 128 x 256 tile is cut into 2 or 4 K slices (>= 512
-// deep, a whole group of E8M0 scale loads), one workgroup each; the fp32
-// partial tiles meet in a caller-provided workspace.  The decision depends
-// on M, N and K only (128-row tiles per batch in both forms), so the single
-// and the dual launch of one M give identical bits.
-int gemm_bf16f4_splits(int64_t M, int64_t N, int64_t K, bool /*dual*/) {
-    if (M <= LSMX_SKINNY_MAX_M) return 1;  // the GEMV and skinny kernels own these
-    const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256), cus = num_cus_w();
-    if (2 * tiles > cus) return 1;
-    for (int sp = 4; sp >= 2; sp /= 2)
-        if (tiles * sp <= cus && K % (512 * sp) == 0) return sp;
-    return 1;
+// panel.  Instead each output tile of 128 rows (per batch) by 256 or 128
+// weight columns is cut into 2 or 4 K slices (>= 512 deep, a whole group of
+// E8M0 scale loads), one workgroup each; the fp32 partial tiles meet in a
+// caller-provided workspace.  Of the plans that fit one wave of workgroups,
+// the one with the most workgroups wins, and among those the one with the
+// fewest partial bytes: M = 128 against N = 14336 runs 112 tiles of 128 x
+// 128 in 2 slices (224 workgroups, 14.7 MB of partials) rather than 56 tiles
+// of 128 x 256 in 4.  The plan depends on M, N and K only (128-row tiles per
+// batch in both forms), so the single and the dual launch of one M give
+// identical bits.
+struct SplitPlan {
+    int splits, bn;
+};
+static SplitPlan splitk_plan(int64_t M, int64_t N, int64_t K) {
+    SplitPlan best{1, 256};
+    if (M <= LSMX_SKINNY_MAX_M) return best;  // the GEMV and skinny kernels own these
+    const int64_t mt = (M + 127) / 128, cus = num_cus_w();
+    if (2 * mt * ((N + 255) / 256) > cus) return best;  // whole-K tiles fill half of the CUs
+    int64_t best_wg = 0, best_bytes = 0;
+    for (int bn = 256; bn >= 128; bn /= 2)
+        for (int sp = 2; sp <= 4; sp *= 2) {
+            const int64_t nt = (N + bn - 1) / bn, wg = mt * nt * sp, bytes = sp * nt * bn;
+            if (wg > cus || K % (512 * sp) != 0) continue;
+            if (wg > best_wg || (wg == best_wg && bytes < best_bytes)) {
+                best = SplitPlan{sp, bn};
+                best_wg = wg;
+                best_bytes = bytes;
+            }
+        }
+    return best;
 }
+int gemm_bf16f4_splits(int64_t M, int64_t N, int64_t K, bool /*dual*/) { return splitk_plan(M, N, K).splits; }
 
 // Workspace: the fp32 partial tiles [splits][NB][Mp][Np] (Mp = M rounded up
-// to 128 rows, Np = N rounded up to 256 columns).
+// to 128 rows, Np = N rounded up to the plan's tile width).
 int64_t gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, bool dual) {
-    const int sp = gemm_bf16f4_splits(M, N, K, dual);
-    if (sp < 2) return 0;
-    return (int64_t)sp * (dual ? 2 : 1) * ((M + 127) / 128 * 128) * ((N + 255) / 256 * 256) * 4;
+    const SplitPlan p = splitk_plan(M, N, K);
+    if (p.splits < 2) return 0;
+    return (int64_t)p.splits * (dual ? 2 : 1) * ((M + 127) / 128 * 128) * ((N + p.bn - 1) / p.bn * p.bn) * 4;
 }
 
 // C[b][m][n] = sum over slices s = 0, 1, ... of partial[s][b][m][n], in that
@@ -1637,9 +1656,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 #ifndef LSMX_SK_SLOTS
 #define LSMX_SK_SLOTS 4
 #endif
-template <int NB>
+// Wave layouts of the split-K tiles: 128 x 256 single, 1 x 8 waves (each all
+// 128 rows and a 32-column strip, so each weight fragment is dequantized
+// once); 128 x 128 single, 2 x 4 (64 x 32 per wave); dual (256 A rows), 4 x 2
+// waves for both widths.
+template <int NB, int BN>
 static hipError_t launch_ring_splitk(GemmArgs g, int splits, hipStream_t s) {
-    constexpr int BR = 128 * NB, BN = 256;
+    constexpr int BR = 128 * NB;
+    constexpr int WGM = NB == 2 ? 4 : (BN == 256 ? 1 : 2);
+    constexpr int SL = NB == 1 ? LSMX_SK_SLOTS : 3;
     const int64_t tiles = ((g.M + 127) / 128) * ((g.N + BN - 1) / BN);
     g.splits = splits;
     g.k_split = g.K / splits;
@@ -1649,7 +1674,7 @@ static hipError_t launch_ring_splitk(GemmArgs g, int splits, hipStream_t s) {
     const dim3 rgrid((unsigned)((threads + 255) / 256)), rblk(256);
 #define LSMX_RS(CT)                                                                                              \
     do {                                                                                                         \
-        hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT, BR, BN, NB == 1 ? LSMX_SK_SLOTS : 3, true, NB == 1 ? 1 : 4>), grid, blk, 0, s, g); \
+        hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT, BR, BN, SL, true, WGM>), grid, blk, 0, s, g);        \
         hipLaunchKernelGGL((splitk_reduce_kernel<CT>), rgrid, rblk, 0, s, g.ws, splits, NB, Mp, Np, g.c, g.c1, \
                            g.ldc, g.M, g.N);                                                                     \
     } while (0)
@@ -1658,6 +1683,10 @@ static hipError_t launch_ring_splitk(GemmArgs g, int splits, hipStream_t s) {
     else LSMX_RS(LSMX_F16);
 #undef LSMX_RS
     return hipGetLastError();
+}
+template <int NB>
+static hipError_t launch_ring_splitk(GemmArgs g, SplitPlan p, hipStream_t s) {
+    return p.bn == 256 ? launch_ring_splitk<NB, 256>(g, p.splits, s) : launch_ring_splitk<NB, 128>(g, p.splits, s);
 }
 
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
@@ -1668,8 +1697,8 @@ hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
     if (g.M <= LSMX_DECODE_MAX_M && decode_ok(g)) return launch_decode(g, s);
     if (g.M <= LSMX_SKINNY_MAX_M && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
     if (g.ws && ring_ok(g)) {
-        const int sp = gemm_bf16f4_splits(g.M, g.N, g.K, g.a1 != nullptr);
-        if (sp > 1) return g.a1 ? launch_ring_splitk<2>(g, sp, s) : launch_ring_splitk<1>(g, sp, s);
+        const SplitPlan p = splitk_plan(g.M, g.N, g.K);
+        if (p.splits > 1) return g.a1 ? launch_ring_splitk<2>(g, p, s) : launch_ring_splitk<1>(g, p, s);
     }
     return g.a1 ? launch_w4_any<2>(g, s) : launch_w4_any<1>(g, s);
 }

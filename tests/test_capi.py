@@ -231,3 +231,21 @@ def test_two_axis_quantizer_validates_before_launch():
     assert _rc("lsmx_quantize_mxfp4_2d", *args(C.BF16, 256, 256, C.SCALE_F32)) == C.ERR_DTYPE
     rc = _rc("lsmx_quantize_mxfp4_2d", *args(C.BF16, 200, 256, C.SCALE_E8M0_KMAJOR))
     assert rc == C.ERR_SHAPE and "multiples of 128" in C.last_error()
+
+
+def test_split_k_plan_through_workspace_size():
+    """The split-K plan of the bf16 x MXFP4 GEMM, read through the workspace
+    size it asks for (fp32 partials [splits][batches][Mp][Np]; 256 CUs when
+    no device is present).  Of the plans that fit one wave of workgroups the
+    widest wins, then the one with the fewest partial bytes: M = 128 against
+    N = 14336 takes 128 x 128 tiles in 2 slices (224 workgroups) rather than
+    128 x 256 in 4; M = 256 keeps 128 x 256 in 2; whole-K shapes and skinny
+    M ask for nothing."""
+    L = C.load()
+    ws = lambda M, N, K, dual=0: L.lsmx_gemm_bf16f4_workspace(M, N, K, dual)   # noqa: E731
+    assert ws(128, 14336, 4096) == 2 * 128 * 14336 * 4
+    assert ws(128, 14336, 4096, 1) == 2 * 2 * 128 * 14336 * 4
+    assert ws(256, 14336, 2048) == 2 * 256 * 14336 * 4
+    assert ws(64, 2304, 4096) == 4 * 128 * 2304 * 4
+    assert ws(200, 1000, 2048) == 4 * 256 * 1024 * 4
+    assert ws(1024, 14336, 4096) == 0 and ws(16, 14336, 4096) == 0

@@ -277,11 +277,13 @@ def test_kmajor_scales_give_identical_gemm(dev, mods, oracle, M, N, K):
     assert oracle.max_rel(c_km.cpu().numpy(), ref) <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 14336, 4096), (200, 1000, 2048), (256, 4096, 1024), (64, 2304, 4096)])
+@pytest.mark.parametrize("M,N,K", [(128, 14336, 4096), (200, 1000, 2048), (256, 4096, 1024), (64, 2304, 4096),
+                                   (256, 14336, 2048)])
 def test_weight_only_split_k(dev, mods, oracle, M, N, K):
     """Mid-size M against a wide weight splits K (lsmx_gemm_bf16f4_ws): each
     slice's fp32 partial tile goes to a workspace and a second kernel adds
-    the slices in slice order.  vs fp64; repeated calls and the dual form
+    the slices in slice order.  128 x 128 tiles in 2 or 4 slices at the
+    first four shapes, 128 x 256 tiles in 2 at the last.  vs fp64; repeated calls and the dual form
     give the same bits; a call at another shape in between (sharing the
     cached workspace) does not disturb them."""
     fp4, mg, dg, _ = mods
