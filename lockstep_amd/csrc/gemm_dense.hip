@@ -256,42 +256,69 @@ __global__ __launch_bounds__(dn::NT, (dense_lds_bytes<DT, MODE, SHB>() <= 80 * 1
 }
 
 // y[cols, ldy] = x[rows, ldx]^T through a 64 x 64 LDS tile.  Full tiles of
-// 16-byte aligned rows move 16 bytes per load and per store (a thread gathers
-// 16/sizeof(T) elements of a column from LDS into one store); edge tiles and
-// unaligned operands go element by element.
+// 16-byte aligned rows: each thread loads 16 bytes of a row; the tile sits in
+// LDS as dwords of E = 4 / sizeof(T) consecutive elements, one padding dword
+// per row, so that the dword column reads below touch 64 distinct banks.  A
+// thread then reads E dwords down one dword column (E consecutive rows),
+// transposes that E x E block in registers (v_perm_b32) and writes one dword
+// to each of E output rows; consecutive lanes take consecutive row blocks,
+// so each output row receives 64 (bytes), 128 (16-bit) or 256 (32-bit)
+// contiguous bytes per store instruction.  Edge tiles and unaligned operands
+// go element by element.
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_kernel(const T *__restrict__ x, int64_t rows, int64_t cols,
                                                         int64_t ldx, T *__restrict__ y, int64_t ldy, int vec) {
-    constexpr int V = 16 / (int)sizeof(T);   // elements per 16 bytes
-    constexpr int CPR = 64 / V;              // 16-byte chunks per tile row
-    constexpr int P = 64 + V;                // padded LDS row (keeps 16-byte alignment)
-    __shared__ __attribute__((aligned(16))) T tile[64][P];
+    constexpr int E = 4 / (int)sizeof(T);    // elements per dword
+    constexpr int WPR = 64 / E;              // dwords per tile row
+    constexpr int P = WPR + 1;               // padded LDS row, in dwords
+    __shared__ uint32_t tile[64 * P];
     const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
     const int t = threadIdx.x;
     const bool full = vec && r0 + 64 <= rows && c0 + 64 <= cols;
-    for (int q = t; q < 64 * CPR; q += 256) {
-        const int r = q / CPR, cc = (q % CPR) * V;
-        if (full) {
-            *reinterpret_cast<uint4 *>(&tile[r][cc]) = *reinterpret_cast<const uint4 *>(x + (r0 + r) * ldx + c0 + cc);
-        } else {
-#pragma unroll
-            for (int k = 0; k < V; ++k)
-                if (r0 + r < rows && c0 + cc + k < cols) tile[r][cc + k] = x[(r0 + r) * ldx + c0 + cc + k];
+    if (full) {
+        for (int q = t; q < 64 * WPR / 4; q += 256) {
+            const int r = q / (WPR / 4), w4 = (q % (WPR / 4)) * 4;
+            const uint4 v = *reinterpret_cast<const uint4 *>(x + (r0 + r) * ldx + c0 + w4 * E);
+            uint32_t *d = &tile[r * P + w4];
+            d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
         }
+        __syncthreads();
+        for (int q = t; q < (64 / E) * WPR; q += 256) {
+            const int p = q % (64 / E), w = q / (64 / E);   // rows E*p .., dword column w
+            uint32_t a[E], o[E];
+#pragma unroll
+            for (int k = 0; k < E; ++k) a[k] = tile[(E * p + k) * P + w];
+            if constexpr (E == 4) {
+                // o[i] = byte i of a[0], a[1], a[2], a[3]
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t sel = 0x0C0C0000u | ((uint32_t)(4 + i) << 8) | (uint32_t)i;
+                    o[i] = __builtin_amdgcn_perm(a[1], a[0], sel) | (__builtin_amdgcn_perm(a[3], a[2], sel) << 16);
+                }
+            } else if constexpr (E == 2) {
+                o[0] = __builtin_amdgcn_perm(a[1], a[0], 0x05040100u);
+                o[1] = __builtin_amdgcn_perm(a[1], a[0], 0x07060302u);
+            } else {
+                o[0] = a[0];
+            }
+#pragma unroll
+            for (int i = 0; i < E; ++i)
+                *reinterpret_cast<uint32_t *>(y + (c0 + E * w + i) * ldy + r0 + E * p) = o[i];
+        }
+        return;
+    }
+    // element by element through a [64][65] view of the same LDS
+    T *te = reinterpret_cast<T *>(tile);
+    constexpr int PE = 65;
+    static_assert(64 * PE * sizeof(T) <= sizeof(tile), "edge-tile view fits");
+    for (int q = t; q < 64 * 64; q += 256) {
+        const int r = q / 64, cc = q % 64;
+        if (r0 + r < rows && c0 + cc < cols) te[r * PE + cc] = x[(r0 + r) * ldx + c0 + cc];
     }
     __syncthreads();
-    for (int q = t; q < 64 * CPR; q += 256) {
-        const int oc = q / CPR, rr = (q % CPR) * V;   // output row oc = input column, elements rr .. rr+V-1
-        if (full) {
-            T v[V];
-#pragma unroll
-            for (int k = 0; k < V; ++k) v[k] = tile[rr + k][oc];
-            *reinterpret_cast<uint4 *>(y + (c0 + oc) * ldy + r0 + rr) = *reinterpret_cast<const uint4 *>(v);
-        } else {
-#pragma unroll
-            for (int k = 0; k < V; ++k)
-                if (c0 + oc < cols && r0 + rr + k < rows) y[(c0 + oc) * ldy + r0 + rr + k] = tile[rr + k][oc];
-        }
+    for (int q = t; q < 64 * 64; q += 256) {
+        const int oc = q / 64, rr = q % 64;   // output row oc = input column, element rr
+        if (c0 + oc < cols && r0 + rr < rows) y[(c0 + oc) * ldy + r0 + rr] = te[rr * PE + oc];
     }
 }
 

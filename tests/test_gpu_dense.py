@@ -219,9 +219,10 @@ def test_empty_and_zero_k(dev, mods):
 
 @pytest.mark.parametrize("elem", [1, 2, 4])
 @pytest.mark.parametrize("rows,cols,pad", [(1, 1, 5), (33, 65, 5), (256, 96, 5), (1000, 3, 5), (128, 192, 0),
-                                           (192, 320, 0), (100, 80, 0)])
+                                           (192, 320, 0), (100, 80, 0), (512, 640, 0), (200, 130, 0)])
 def test_transpose_exact(dev, mods, elem, rows, cols, pad):
-    """Element-by-element (pad 5: unaligned rows) and 16-byte (pad 0) paths, full and edge tiles."""
+    """Element-by-element (pad 5: unaligned rows) and 16-byte (pad 0) paths, full and edge tiles; the full
+    tiles transpose blocks of 4 bytes, 2 halves or 1 dword in registers."""
     C = mods[3]
     dt = {1: torch.uint8, 2: torch.int16, 4: torch.int32}[elem]
     x = torch.randint(0, 100, (rows, cols + pad), dtype=torch.int32).to(dt).to(dev)[:, :cols]
