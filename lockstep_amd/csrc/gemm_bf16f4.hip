@@ -546,6 +546,11 @@ __global__ __launch_bounds__(wr::NT, 1) void gemm_bf16f4_ring_kernel(GemmArgs g)
     constexpr int SWV = BN >= 64 ? BN / 64 : 1;  // distinct scale loads (64 rows each)
     static_assert(TM >= 1 && TN >= 1 && XA >= 1 && S >= 3 && (A_SLOT / 1024) % NLW == 0 && NLW <= NW, "tile");
     static_assert(NLW >= SWV, "every scale block needs a loader");
+    // The scales of stages 8g+8 .. 8g+15 are issued first among stage 8g+6's
+    // loads and first read right after the barrier of stage 8g+7 (4 slots) or
+    // 8g+8 (3 slots); the wait at that barrier leaves (S - 3) L or (S - 2) L
+    // loads outstanding, which covers the scale load only for these depths.
+    static_assert(S == 3 || S == 4, "the scale prefetch distance assumes a 3- or 4-slot ring");
     __shared__ __attribute__((aligned(16))) uint8_t sA[S][A_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t sW[S][W_SLOT];
     __shared__ __attribute__((aligned(16))) uint8_t sS[2][BN * 16];   // [group & 1][row][16 scale bytes]
@@ -1649,10 +1654,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
     }
 }
 
-// Ring depth of the single form's split-K kernel (24 KiB per slot): 3, 4 and
-// 6 slots time within 3% of each other for M = 64 .. 256 against a 14336 x
-// 4096 weight, 4 the fastest, so the loads in flight do not set its pace.
-// The dual form's 40 KiB slots fit 3.
+// Ring depth of the single form's split-K kernel (24 KiB per slot): 3 and 4
+// slots time within 3% of each other for M = 64 .. 256 against a 14336 x
+// 4096 weight, 4 the faster, so the loads in flight do not set its pace
+// (deeper rings would need the scale loads issued earlier).  The dual form's
+// 40 KiB slots fit 3.
 #ifndef LSMX_SK_SLOTS
 #define LSMX_SK_SLOTS 4
 #endif
