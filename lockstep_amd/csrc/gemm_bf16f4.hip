@@ -1338,7 +1338,10 @@ static bool decode_ok(const GemmArgs &g) {
 // VM is the number of virtual activation rows (M, or 2M in dual mode).
 namespace gv {
 constexpr int NT = 512;   // 8 waves
-constexpr int RPW = 4;    // weight rows per wave
+// weight rows per wave: 2 rows (896 workgroups at N = 14336) stream a
+// 14336 x 4096 weight in 8.6 us against 9.6 us with 4 rows (448, which
+// leaves some CUs one workgroup and others two); 1 row takes 9.1-10.4 us
+constexpr int RPW = 2;
 constexpr int UB = 2;     // groups of 64 blocks per lane in flight
 }  // namespace gv
 
