@@ -342,6 +342,31 @@ __global__ void scale_to_e8m0_kernel(const float *__restrict__ s, int64_t rows, 
     else out[orow * ldo + blk] = e;
 }
 
+// The K-major output four blocks at a time: thread i converts blocks 4g ..
+// 4g+3 of output row o (o = i mod orows, g = i / orows) and writes their
+// dword, so that consecutive threads write consecutive dwords (and, for
+// transposed input, read consecutive floats).  The number of blocks is a
+// multiple of 4.
+__global__ void scale_to_e8m0_km4_kernel(const float *__restrict__ s, int64_t orows, int64_t groups, int64_t lds,
+                                         bool tin, uint8_t *__restrict__ out, int64_t ldo, bool out4) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= orows * groups) return;
+    const int64_t g = i / orows, o = i - g * orows;
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t blk = 4 * g + k;
+        w |= f32_scale_e8m0(f2u(tin ? s[blk * lds + o] : s[o * lds + blk])) << (8 * k);
+    }
+    uint8_t *d = out + (g * ldo + o) * 4;
+    if (out4) {
+        *reinterpret_cast<uint32_t *>(d) = w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[k] = (uint8_t)(w >> (8 * k));
+    }
+}
+
 template <int DT, int MODE, bool SHB, bool SCALED, int CT, bool ATOMIC>
 static void launch_d(const DenseArgs &g, hipStream_t s) {
     const int tiles = (int)(((g.M + dn::BM - 1) / dn::BM) * ((g.N + dn::BN - 1) / dn::BN));
@@ -399,6 +424,13 @@ hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t
 
 hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int layout, uint8_t *out,
                                 int64_t ldo, hipStream_t s) {
+    if (layout & LSMX_E8M0_OUT_KMAJOR) {
+        const bool tin = layout & LSMX_E8M0_IN_T;
+        const int64_t orows = tin ? cols : rows, groups = (tin ? rows : cols) / 4, n = orows * groups;
+        hipLaunchKernelGGL(scale_to_e8m0_km4_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sc, orows,
+                           groups, lds, tin, out, ldo, (reinterpret_cast<uintptr_t>(out) & 3) == 0);
+        return hipGetLastError();
+    }
     const int64_t n = rows * cols;
     hipLaunchKernelGGL(scale_to_e8m0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sc, rows, cols, lds,
                        layout, out, ldo);

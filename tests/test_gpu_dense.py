@@ -231,6 +231,42 @@ def test_transpose_exact(dev, mods, elem, rows, cols, pad):
     assert torch.equal(y.cpu(), x.t().cpu())
 
 
+@pytest.mark.parametrize("tin", [False, True])
+@pytest.mark.parametrize("misalign", [0, 1])
+def test_scale_to_e8m0_layouts(dev, mods, oracle, tin, misalign):
+    """lsmx_scale_to_e8m0 in all four layouts: powers of two 2^-127 .. 2^127 give the oracle's exponent bytes,
+    anything else 0xFF; the K-major output (four blocks per thread, whole-dword stores, byte stores at an odd
+    address) holds the row-major output's bytes regrouped, and no byte outside it is written."""
+    C = mods[3]
+    rng = np.random.default_rng(11)
+    orows, blocks = 300, 40
+    s = np.ldexp(np.ones((orows, blocks)), rng.integers(-127, 128, size=(orows, blocks))).astype(np.float32)
+    bad = rng.random((orows, blocks)) < 0.05
+    s[bad] = rng.choice(np.float32([1.5, -2.0, 0.0, np.inf, 3.0]), size=int(bad.sum()))
+    want = oracle.scale_to_e8m0(s)
+    want[bad] = 0xFF
+    src = np.ascontiguousarray(s.T) if tin else s      # IN_T: element (block, row)
+    lds = src.shape[1] + 3
+    x = torch.zeros((src.shape[0], lds), dtype=torch.float32)
+    x[:, :src.shape[1]] = torch.from_numpy(src)
+    x = x.to(dev)
+    lay = C.E8M0_IN_T if tin else 0
+    ldo = blocks + 5
+    y = torch.full((orows * ldo,), 7, dtype=torch.uint8, device=dev)
+    C.call("lsmx_scale_to_e8m0", x.data_ptr(), src.shape[0], src.shape[1], lds, lay, y.data_ptr(), ldo,
+           C.stream_of(y))
+    yr = y.cpu().numpy().reshape(orows, ldo)
+    assert np.array_equal(yr[:, :blocks], want) and (yr[:, blocks:] == 7).all()
+    ldk = orows + 2
+    buf = torch.full((misalign + blocks // 4 * ldk * 4,), 7, dtype=torch.uint8, device=dev)
+    C.call("lsmx_scale_to_e8m0", x.data_ptr(), src.shape[0], src.shape[1], lds, lay | C.E8M0_OUT_KMAJOR,
+           buf.data_ptr() + misalign, ldk, C.stream_of(buf))
+    raw = buf.cpu().numpy()
+    yk = raw[misalign:].reshape(blocks // 4, ldk, 4)
+    assert np.array_equal(yk[:, :orows, :], want.reshape(orows, blocks // 4, 4).transpose(1, 0, 2))
+    assert (yk[:, orows:, :] == 7).all() and (raw[:misalign] == 7).all()
+
+
 # ----------------------------------------------------------- mxfp4_gemm_fp8
 def e4m3_of_codes(dev, fp4, codes):
     return fp4.codes_to_e4m3(torch.from_numpy(codes).to(dev))
