@@ -132,7 +132,7 @@ def test_full_size_8192_cubed_sampled(dev, mods, oracle):
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", [(1, 256, 4096), (2, 300, 640), (1, 14336, 4096), (16, 300, 512), (100, 512, 128),
-                                   (256, 256, 1024), (513, 1024, 256)])
+                                   (256, 256, 1024), (513, 1024, 256), (1, 300, 640), (1, 17, 8192), (1, 1, 128)])
 def test_weight_only_bf16_x_fp4(dev, mods, oracle, out_dtype, M, N, K):
     fp4, mg, _, _ = mods
     a = gen.to_bf16_bits(gen.normal(M + 5 * K, (M, K)))
