@@ -1571,6 +1571,24 @@ static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
 #define LSMX_RING_NLW 4
 #endif
     // the ring kernel is worth it from half a wave of 256 x 256 tiles on (M = 1024, N = 14336: 224 tiles)
+#ifndef LSMX_HALF_TILE
+#define LSMX_HALF_TILE 1
+#endif
+#ifndef LSMX_HALF_S
+#define LSMX_HALF_S 4
+#endif
+#ifndef LSMX_HALF_NLW
+#define LSMX_HALF_NLW 4
+#endif
+    // single form whose 256 x 256 tiles leave CUs idle while 128 x 256 tiles
+    // still fit in one wave of workgroups: 128-row tiles, 1 x 8 waves (each
+    // all 128 rows and a 32-column strip), loads from waves 0-3.  cfg2's
+    // single batch (M = 2048 against a 4096 x 4096 weight, 128 -> 256
+    // workgroups) 97 -> 63 us; M = 1024 against 8192 x 4096 91 -> 62 us
+    if constexpr (NB == 1)
+        if (LSMX_HALF_TILE && ring_ok(g) && tiles(256, 256) < cus && tiles(128, 256) <= cus &&
+            2 * tiles(128, 256) > cus)
+            return launch_ring<NB, 128, 256, LSMX_HALF_S, 1, LSMX_HALF_NLW>(g, s);
     if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3, LSMX_RING_WGM, LSMX_RING_NLW>(g, s);
     if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
     if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
