@@ -192,10 +192,11 @@ def test_weight_only_decode_nan_scale_byte(dev, mods, oracle):
     assert oracle.max_rel(c[:, keep], ref[:, keep]) <= 1e-5
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 4096, 512), (128, 14336, 512), (1000, 1000, 256)])
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 512), (128, 14336, 512), (1000, 1000, 256), (1500, 4000, 512)])
 def test_weight_only_tile_paths(dev, mods, oracle, M, N, K):
-    """Large M runs 256 x 256 tiles, mid M (cfg3's M = 128) 128 x 128 tiles:
-    both match the fp64 oracle on sampled rows, and give the same bits."""
+    """Large M runs 256 x 256 tiles, mid M (cfg3's M = 128) 128 x 128 tiles, and a single launch whose
+    256 x 256 tiles would leave CUs idle 128 x 256 tiles (1500 x 4000, ragged in both): all match the fp64
+    oracle on sampled rows, and give the same bits."""
     fp4, mg, _, _ = mods
     g = torch.Generator(device=dev).manual_seed(M + N)
     a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
@@ -210,7 +211,8 @@ def test_weight_only_tile_paths(dev, mods, oracle, M, N, K):
     assert torch.equal(part, c[:64 + M // 4])
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (100, 300, 256), (1, 256, 128), (2, 520, 384), (1, 4096, 4096)])
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 4096), (100, 300, 256), (1, 256, 128), (2, 520, 384), (1, 4096, 4096),
+                                   (1500, 4000, 512)])
 def test_dual_batch_matches_single_and_oracle(dev, mods, oracle, M, N, K):
     """cfg2 (and ragged shapes): two bf16 batches share one MXFP4 weight."""
     fp4, mg, dg, _ = mods
