@@ -139,7 +139,10 @@ int lsmx_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n_words, void *s
  * form (not a positive power of two in [2^-127, 2^127]) is taken as E8M0
  * NaN: the outputs that use it are NaN, where the reference's fp32
  * multiply (mxfp4_gemm.py:148-150) would scale by it.  E8M0 byte 0 is
- * 2^-127. */
+ * 2^-127.  K-major E8M0 scales with K % 256 == 0 run the fastest kernel
+ * (16 x 16 x 128 scaled MFMA on 256-code stages); the other formats and K
+ * % 256 != 0 run a 32 x 32 x 64 kernel on 128-code stages.  Every format of
+ * the same scales gives the same bits. */
 int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_t ld_sa,
                    const uint8_t *bt_pk, int64_t ldb, const void *b_scale, int64_t ld_sb,
                    int scale_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N,
@@ -162,8 +165,13 @@ int lsmx_gemm_bf16f4(const void *a, int64_t lda, const uint8_t *w_pk, int64_t ld
  * the library does not split this shape.  It splits K in 2 or 4 slices when
  * the whole-K 128 x 256 output tiles would fill less than half of the CUs
  * (a few hundred activation rows against a wide weight, e.g. M = 128
- * against N = 14336: 128 x 128 tiles in 2 slices); the decision depends on
- * M, N and K only. */
+ * against N = 14336: 128 x 128 tiles in 2 slices).  The answer depends on
+ * M, N and K only, but the split itself runs only for E8M0 scales whose rows
+ * are 16-byte aligned with a stride that is a multiple of 16 bytes; other
+ * scales (fp32, or E8M0 rows of another alignment) run the whole-K kernels
+ * and leave a given workspace unused, with other bits than the split form
+ * (same tolerance).  The Python layer converts fp32 weight scales to E8M0
+ * bytes first, so both forms of a weight take the same kernels there. */
 int64_t lsmx_gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, int dual);
 
 /* lsmx_gemm_bf16f4 (a1 = c1 = NULL) or lsmx_gemm_dual_bf16f4 (both set)

@@ -130,13 +130,26 @@ def require_device(*tensors: torch.Tensor) -> None:
 
 
 _workspaces: dict = {}
+_captured: list = []
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A device workspace of at least nbytes for the split-K GEMMs, one per
-    (device, stream): calls on one stream are ordered, so they may share it.
-    Kept for later calls; grown by replacing it with a larger one (the old
-    one returns to torch's caching allocator, stream-ordered)."""
+    """A device workspace of at least nbytes for the split-K GEMMs.
+
+    Eager calls share one per (device, stream): calls on one stream are
+    ordered, so they may share it.  It is kept for later calls and grown by
+    replacing it with a larger one (the old one returns to torch's caching
+    allocator, stream-ordered).
+
+    A call made while the current stream is being captured into a graph gets
+    a workspace of its own that is never freed: the graph's replays write to
+    that address whenever they run, so it may neither be handed to another
+    tensor (as a replaced cache entry would be) nor shared with other
+    graphs, which can be replayed concurrently on other streams."""
+    if torch.cuda.is_current_stream_capturing():
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _captured.append(ws)
+        return ws
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:

@@ -6,55 +6,56 @@
 // mxfp4_gemm_packed) and cuda/mxfp4_mma_gemm.cu:69-184, with both operands
 // K-contiguous ("TN"), packed two E2M1 codes per byte, low nibble first.
 // Instead of promoting an FP8 product to fp32 every 32-block and multiplying
-// by fp32 scales, v_mfma_scale_f32_32x32x64_f8f6f4 (cbsz = blgp = 4, FP4)
-// applies one E8M0 scale per lane per operand inside the instruction: for
-// that instruction each lane supplies the 32 codes (16 bytes, four VGPRs) of
-// one row and one 32-block, which is exactly one MX block, and the byte of
-// the scale register selected by op_sel.
+// by fp32 scales, the scaled MFMAs (v_mfma_scale_f32_{32x32x64,16x16x128}_
+// f8f6f4, cbsz = blgp = 4: FP4) apply one E8M0 scale per lane per operand
+// inside the instruction: each lane supplies the 32 codes (16 bytes, four
+// VGPRs) of one row and one 32-block, which is exactly one MX block, and the
+// byte of its scale register selected by op_sel.
 //
-// Tiling: 256 x 256 macro tile, WGM x WGN waves (default 4 x 2, two waves per
-// SIMD), each wave a (256/WGM) x (256/WGN) sub-tile of 32 x 32 MFMA tiles
-// with fp32 accumulators.  A pipeline stage holds KS MFMA K-steps of 64
-// codes: KS = 4 stages 128 bytes of every row (256 codes), KS = 2 stages 64.
-// Whole 128-byte rows matter: the direct-to-LDS path is limited by the
-// number of L2 requests, and a 64-byte row segment costs a request for half
-// a cache line (measured: 19 B/clk per CU for 16 rows x 64 B per load
-// instruction, 36 B/clk for 8 rows x 128 B).
+// Two kernels share one design: a 256 x 256 macro tile per workgroup of 8
+// waves (4 x 2, each 64 x 128, two waves per SIMD) with fp32 accumulators;
+// a persistent schedule, one workgroup per CU walking tiles pid, pid + grid,
+// ...; and a ring of LDS stage slots filled by direct-to-LDS loads
+// (buffer_load_dwordx4 ... lds: lane l's bytes land at M0 + 16 l, no VGPR
+// staging) that runs across tile boundaries, so the first stages of the next
+// tile are in flight while the current tile finishes and writes its output.
+// The loads come from inline asm with an explicit s_waitcnt vmcnt: the
+// compiler cannot prove that ring slots do not alias and would otherwise
+// wait for every outstanding load before each LDS read.
 //
-// Persistent schedule: one workgroup per CU walks tiles pid, pid + grid, ...
-// A ring of S stage slots in LDS is filled by direct-to-LDS loads
-// (global_load_lds_dwordx4 / _dword: lane l's bytes land at M0 + l*size, no
-// VGPR staging) and runs across tile boundaries, so the first stages of the
-// next tile are already in flight while the current tile finishes and writes
-// its output.  The loads come from inline asm with an explicit
-// s_waitcnt vmcnt: the compiler cannot prove that ring slots do not alias and
-// would otherwise wait for every outstanding load before each LDS read.
+//  * gemm_f4f4_mx16_kernel (K-major E8M0 scales, K % 256 == 0; the fast
+//    path): v_mfma_scale_f32_16x16x128_f8f6f4 on 128-byte stage rows in a
+//    2-slot ring of 64 KiB stages.  Whole 128-byte rows matter: the
+//    direct-to-LDS path is limited by the number of L2 requests (measured:
+//    19 B/clk per CU for 16 rows x 64 B per load instruction, 36 B/clk for
+//    8 rows x 128 B).
+//  * gemm_f4f4_kernel (fp32 or row-major E8M0 scales, or K % 256 != 0):
+//    v_mfma_scale_f32_32x32x64_f8f6f4 on 64-byte stage rows in a 3- or
+//    4-slot ring.
 //
-// Per stage and wave: while the MFMAs of K-step st run, the fragments of
-// K-step st + 1 are read from LDS between them.  Once the slot has been read
-// (before K-step 2 with KS = 4, the last K-step with KS = 2), one s_barrier
-// (after the stage's own reads completed and the next stage's loads landed)
-// frees it; the remaining MFMAs then run with the refill of that slot and the
-// next stage's scale and K-step-0 fragment reads interleaved, so the matrix
-// core never waits on a burst of memory instructions.  Refills past the last
-// stage re-load the workgroup's last tile (tile indices are clamped,
-// lsmx_sched.h) into a slot that is never read again, which keeps the loop
-// free of branches and the outstanding-load count constant.
+// Per stage and wave the MFMAs of one K-step run while the fragments of the
+// next are read from LDS between them.  Once the slot has been read, one
+// s_barrier (after the stage's own reads completed and the next stage's
+// loads landed) frees it; the remaining MFMAs then run with the refill of
+// that slot and the next stage's scale and first fragment reads
+// interleaved, so the matrix core never waits on a burst of memory
+// instructions.  Refills past the last stage re-load the workgroup's last
+// tile (tile indices are clamped, lsmx_sched.h) into a slot that is never
+// read again, which keeps the loop free of branches and the
+// outstanding-load count constant.
 //
 // Only waves 0-3 issue the refill loads.  The two waves of a SIMD share its
 // matrix core; the older one (0-3) wins issue arbitration and reaches the
 // stage barrier first, so the younger one's instruction stream sets the pace
 // and is kept to MFMAs and LDS reads.  The refill tile changes only in the
 // last S stages of a tile, so each tile runs two stage loops ("phases") and
-// the refill panels are computed between them, not per stage; with a 2-slot
-// ring, stages run in pairs with compile-time slots, which makes every LDS
-// address a loop-invariant register plus an immediate.
+// the refill panels are computed between them, not per stage.
 //
-// LDS layout per stage: rows of 16*CPR bytes (CPR = 2*KS chunks of 16 bytes);
-// chunk c of row r lives at r*16*CPR + 16*(c ^ swz(r)), which keeps the 16
-// lanes a ds_read_b128 serves per cycle on distinct banks.  The DMA writes
-// slots in lane order, so the swizzle is applied by choosing each lane's
-// source address.
+// LDS layout per stage: rows of 16*CPR bytes (CPR 16-byte chunks); chunk c
+// of row r lives at r*16*CPR + 16*(c ^ swz(r)), which keeps the lanes a
+// ds_read_b128 serves per cycle on distinct banks.  The DMA writes slots in
+// lane order, so the swizzle is applied by choosing each lane's source
+// address.
 #include "lsmx_dma.h"
 #include "lsmx_store.h"
 #include "lsmx_internal.h"
@@ -79,12 +80,9 @@ __device__ v16f mfma_scale_f4(v4i a, v4i b, v16f c, int cbsz, int blgp, int opse
 // their only vector-memory operations are the previous tile's C stores,
 // which then stay in flight across the next tile's stages instead of
 // holding the wave (vmcnt counts stores too).
-#ifndef LSMX_F4_NLW_WAIT
-#define LSMX_F4_NLW_WAIT 0
-#endif
 template <bool LOADER, int N>
 LSMX_DEV void stage_barrier() {
-    if constexpr (LOADER || LSMX_F4_NLW_WAIT) wait_vm_barrier<N>();
+    if constexpr (LOADER) wait_vm_barrier<N>();
     else asm volatile("s_barrier" ::: "memory");
 }
 
@@ -106,13 +104,14 @@ LSMX_DEV int f4_swz(int row) {
 // K/32 bytes; K-major E8M0 scales ([K/128][rows][4]) give the dwords of one
 // 128-code slice for consecutive rows as one contiguous run -- one 64-byte
 // request per 16 rows instead of one per row.
-template <int SFMT, int CT, int S, int WGM, int WGN, int KS>
-__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g) {
+template <int SFMT, int S, int CT>
+__global__ __launch_bounds__(512, 1) void gemm_f4f4_kernel(GemmArgs g) {
     using namespace f4;
+    constexpr int WGM = 4, WGN = 2;            // waves: 64 x 128 each, two per SIMD
+    constexpr int KS = 2;                      // MFMA K-steps per stage (64-byte rows)
     constexpr bool SF32 = SFMT == LSMX_SCALE_F32;
     constexpr bool SKM = SFMT == LSMX_SCALE_E8M0_KMAJOR;
     constexpr int NW = WGM * WGN;
-    constexpr int NTH = 64 * NW;
     constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
     constexpr int NMF = TM * TN;               // MFMAs per K-step
     constexpr int BKB = 32 * KS;               // bytes of K per row per stage
@@ -130,13 +129,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     constexpr int NLW = 4;
     constexpr int XA = (TILE_B / 16) / (64 * NLW);  // 16-byte DMA slots per loader lane per operand
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    static_assert(KS == 2 || KS == 4, "2 or 4 K-steps per stage");
     // scale loads: every loader wave loads 64 rows of A's and of B's scales
-    // per slice, except for K-major E8M0 scales with KS = 4: one 1 KiB slice
-    // (256 rows) per dwordx4 load, loader wave w takes operand (w >> 1) & 1,
-    // slice w & 1.
-    constexpr bool SX4 = SKM && KS == 4;
-    constexpr int LS = SX4 ? 1 : 2 * NSL;
+    constexpr int LS = 2 * NSL;
     constexpr int L = 2 * XA + LS;                   // loads per thread per stage
     constexpr int NRD = TM + TN;                     // fragment (and scale) reads per K-step / stage
     constexpr int OPM = (L + NMF - 1) / NMF;         // refill ops per MFMA, last K-step
@@ -190,7 +184,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     // tile, of its A and B code rows and of the scale slices this wave loads,
     // and the scale bytes one stage advances.  Wave-uniform; recomputed only
     // when the refill target moves on to the next tile.
-    constexpr int NSD = SX4 ? 1 : LS;  // scale descriptors per stage
+    constexpr int NSD = LS;  // scale descriptors per stage
     struct Panel {
         const uint8_t *p;
         int64_t n;
@@ -199,7 +193,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     int64_t sstep[NSD];
 #pragma unroll
     for (int r = 0; r < NSD; ++r) {
-        const bool to_b = SX4 ? ((wave >> 1) & 1) : (r & 1);
+        const bool to_b = r & 1;
         const int64_t sld = to_b ? g.ld_sb : g.ld_sa;
         sstep[r] = SKM ? NSL * sld * 4 : SF32 ? NSL * 16 : NSL * 4;
     }
@@ -210,9 +204,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
         pB = Panel{g.b + rn0 * g.ldb, min(g.N - rn0, (int64_t)BN) * g.ldb};
 #pragma unroll
         for (int r = 0; r < NSD; ++r) {
-            // SX4: operand (wave >> 1) & 1, slice wave & 1
-            const bool to_b = SX4 ? ((wave >> 1) & 1) : (r & 1);
-            const int j = SX4 ? (wave & 1) : (r >> 1);  // scale slice within the stage
+            const bool to_b = r & 1;
+            const int j = r >> 1;  // scale slice within the stage
             const int64_t r0 = to_b ? rn0 : rm0, sld = to_b ? g.ld_sb : g.ld_sa;
             // scalar part of this slice's address; the lane adds its row
             // offset.  Rows past the operand read other scales or zeros:
@@ -253,26 +246,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
             else dma_x4(offB0 + i * stepB, rsB, m0);
             return;
         }
-        if constexpr (SX4) {
-            const bool xb = (wave >> 1) & 1;
-            const int j = wave & 1;
-            dma_x4((uint32_t)lane * 16, rsS[0], lds_u32(xb ? &sSB[s][j][0] : &sSA[s][j][0]));
-            return;
-        }
         const int r = q - 2 * XA;
         const bool to_b = r & 1;
         const int j = r >> 1;
         const uint32_t m0 = lds_u32(to_b ? &sSB[s][j][(wave & 3) * 64 * SSL] : &sSA[s][j][(wave & 3) * 64 * SSL]);
-        if constexpr (SF32) dma_x4(to_b ? offSB : offSA, rsS[SX4 ? 0 : r], m0);
-        else dma_x1(to_b ? offSB : offSA, rsS[SX4 ? 0 : r], m0);
+        if constexpr (SF32) dma_x4(to_b ? offSB : offSA, rsS[r], m0);
+        else dma_x1(to_b ? offSB : offSA, rsS[r], m0);
     };
 
-    // K positions: at K-step st, lane half h supplies 16-byte chunk
-    // c = (KS/2)*2*h + st of its row -- for KS = 4 the four blocks of scale
-    // slice h, for KS = 2 blocks 2h and 2h+1 -- so one scale register per
-    // fragment row serves the whole stage and op_sel = st picks the block's
-    // byte.  A and B use the same assignment, so the sum is unchanged.
-    auto chunk_of = [&](int st) { return (KS == 4 ? 4 : 2) * half + st; };
+    // K positions: at K-step st, lane half h supplies 16-byte chunk 2h + st
+    // of its row (blocks 2h and 2h + 1), so one scale register per fragment
+    // row serves the whole stage and op_sel = st picks the block's byte.  A
+    // and B use the same assignment, so the sum is unchanged.
+    auto chunk_of = [&](int st) { return 2 * half + st; };
     auto read_frag = [&](int s, int st, int q, v4i (&fa)[TM], v4i (&fb)[TN]) {
         const int c = chunk_of(st);
         const int r = q < TM ? rowA0 + q * 32 : rowB0 + (q - TM) * 32;
@@ -284,15 +270,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     };
     // scale register of fragment row q: the bytes of blocks chunk_of(0..KS-1)
     auto read_scale = [&](int s, int q, uint32_t (&sa)[TM], uint32_t (&sb)[TN]) {
-        const uint8_t *tab = q < TM ? sSA[s][KS == 4 ? half : 0] : sSB[s][KS == 4 ? half : 0];
+        const uint8_t *tab = q < TM ? sSA[s][0] : sSB[s][0];
         const int r = q < TM ? rowA0 + q * 32 : rowB0 + (q - TM) * 32;
         uint32_t v;
         if constexpr (SF32) {
             const u32x4 f = *reinterpret_cast<const u32x4 *>(tab + r * 16);
             v = (f32_scale_e8m0(f[0]) | (f32_scale_e8m0(f[1]) << 8) | (f32_scale_e8m0(f[2]) << 16) |
                  (f32_scale_e8m0(f[3]) << 24)) >> (16 * half);
-        } else if constexpr (KS == 4) {
-            v = *reinterpret_cast<const uint32_t *>(tab + r * 4);
         } else {
             v = *reinterpret_cast<const uint16_t *>(tab + r * 4 + 2 * half);
         }
@@ -305,8 +289,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     constexpr bool LOADER = decltype(loader_c)::value;
     v16f acc[TM][TN];
     uint32_t scA[TM], scB[TN], nA[TM], nB[TN];
-    // fragment buffers: KS = 4 keeps three K-steps' fragments at once (see the stage loop)
-    v4i fa[KS == 4 ? 3 : 2][TM], fb[KS == 4 ? 3 : 2][TN];
+    v4i fa[2][TM], fb[2][TN];
 
     // ---- prologue: fill the ring, publish stage 0, read its step-0 operands
     if constexpr (LOADER) {
@@ -358,20 +341,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
 
         // one pipeline stage (stage u, ring slot u % S) whose refill loads
         // k-step rk of the current refill tile
-        // SLOT < 0: ring slot u % S computed at run time; SLOT >= 0: the
-        // caller knows u % S == SLOT, so every LDS address of the stage is a
-        // loop-invariant register plus an immediate offset.
-        auto run_stage = [&](const int rk, auto slot_c) __attribute__((always_inline)) {
-            constexpr int SLOT = decltype(slot_c)::value;
-            const int s = SLOT >= 0 ? SLOT : u % S;
-            const int sn = SLOT >= 0 ? (SLOT + 1) % S : (u + 1) % S;
-            // Descriptors of the refill stage.  With KS = 4 part c is built
-            // after the stage's MFMA c, so that its scalar arithmetic overlaps
-            // the matrix core instead of delaying the stage's first MFMA on
-            // both waves of a SIMD.  The empty asm passes rk through an SGPR
-            // so that the IR optimizer cannot hoist a part above the
-            // scheduling fence in front of it.
-            constexpr int NPART = 3;
+        auto run_stage = [&](const int rk) __attribute__((always_inline)) {
+            const int s = u % S;
+            const int sn = (u + 1) % S;
+            // Descriptors of the refill stage, built before the stage's
+            // MFMAs.  The empty asm passes rk through an SGPR so that the IR
+            // optimizer cannot hoist a part above the scheduling fence in
+            // front of it.
             auto refill_desc_part = [&](int c) {
                 int k = __builtin_amdgcn_readfirstlane(rk);
                 asm volatile("" : "+s"(k));
@@ -379,111 +355,46 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
                 else if (c == 1) make_desc_b(k);
                 else make_desc_s(k);
             };
-            if constexpr (KS != 4 && LOADER)
-                for (int c = 0; c < NPART; ++c) refill_desc_part(c);
-            if constexpr (KS == 4) {
-                // K-step 0 reads step 1's fragments, step 1 reads steps 2 and
-                // 3's, so slot s is fully read before step 2.  The barrier
-                // sits there, and the slot's refill is spread over steps 2
-                // and 3 (one load per MFMA) instead of being issued in one
-                // burst: a burst of direct-to-LDS loads blocks issue on every
-                // wave at once and the matrix core goes idle.  Buffers: step
-                // 0 -> 0, 1 -> 1, 2 -> 2, 3 -> 0 (free after step 0); the
-                // next stage's step 0 is read into 1 and moved to 0.
-                constexpr int BUF[4] = {0, 1, 2, 0};
-                constexpr int LH = (L + 1) / 2;                  // refill ops in step 2
-                constexpr int OPH = (LH + NMF - 1) / NMF;
-                constexpr int RP1 = (2 * NRD + NMF - 1) / NMF;   // reads per MFMA in step 1
+            if constexpr (LOADER)
+                for (int c = 0; c < 3; ++c) refill_desc_part(c);
 #pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    if (st == 2) {
-                        // this wave's reads of slot s are complete; once all
-                        // waves pass the barrier slot s is free and stage u+1
-                        // has landed
-                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                        stage_barrier<LOADER, (S - 2) * L>();
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-#pragma unroll
-                    for (int idx = 0; idx < NMF; ++idx) {
-                        const int i = idx / TN, j = idx % TN;
-                        acc[i][j] = mfma_scale_f4(fa[BUF[st]][i], fb[BUF[st]][j], acc[i][j], 4, 4, st, (int)scA[i], st,
-                                                  (int)scB[j]);
-                        if (st == 0) {
-                            if (LOADER && idx < NPART) {
-                                __builtin_amdgcn_sched_barrier(0);
-                                refill_desc_part(idx);
-                            }
-                            if (idx < NRD) read_frag(s, 1, idx, fa[1], fb[1]);
-                        } else if (st == 1) {
-#pragma unroll
-                            for (int r = idx * RP1; r < (idx + 1) * RP1; ++r) {
-                                if (r < NRD) read_frag(s, 2, r, fa[2], fb[2]);
-                                else if (r < 2 * NRD) read_frag(s, 3, r - NRD, fa[0], fb[0]);
-                            }
-                        } else if (st == 2) {
-#pragma unroll
-                            for (int o = idx * OPH; o < (idx + 1) * OPH; ++o)
-                                if (LOADER && o < LH) issue_op(s, o);
-                            if (idx < NRD) read_scale(sn, idx, nA, nB);
-                        } else {
-#pragma unroll
-                            for (int o = LH + idx * OPH; o < LH + (idx + 1) * OPH; ++o)
-                                if (LOADER && o < L) issue_op(s, o);
-                            if (idx < NRD) read_frag(sn, 0, idx, fa[1], fb[1]);
-                        }
-                        // Pin this slot's LDS reads here: the MFMA is a pure
-                        // intrinsic, so without a memory clobber the optimizer
-                        // may hoist every later K-step's reads to the top of
-                        // the stage and keep all their fragments live at once.
-                        asm volatile("" ::: "memory");
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
+            for (int st = 0; st < KS; ++st) {
+                const int fb_cur = st & 1;
+                if (st == KS - 1) {
+                    // this wave's reads of slot s are complete; once all waves
+                    // pass the barrier slot s is free and stage u+1 has landed
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    stage_barrier<LOADER, (S - 2) * L>();
+                    __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
-                for (int i = 0; i < TM; ++i) fa[0][i] = fa[1][i];
+                for (int idx = 0; idx < NMF; ++idx) {
+                    const int i = idx / TN, j = idx % TN;
+                    acc[i][j] = mfma_scale_f4(fa[fb_cur][i], fb[fb_cur][j], acc[i][j], 4, 4, st, (int)scA[i], st,
+                                              (int)scB[j]);
+                    if (st < KS - 1) {
+                        // fragments of the next K-step of this stage
 #pragma unroll
-                for (int j = 0; j < TN; ++j) fb[0][j] = fb[1][j];
-            } else {
-    #pragma unroll
-                for (int st = 0; st < KS; ++st) {
-                    const int fb_cur = st & 1;
-                    if (st == KS - 1) {
-                        // this wave's reads of slot s are complete; once all waves
-                        // pass the barrier slot s is free and stage u+1 has landed
-                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                        stage_barrier<LOADER, (S - 2) * L>();
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-    #pragma unroll
-                    for (int idx = 0; idx < NMF; ++idx) {
-                        const int i = idx / TN, j = idx % TN;
-                        acc[i][j] = mfma_scale_f4(fa[fb_cur][i], fb[fb_cur][j], acc[i][j], 4, 4, st, (int)scA[i], st,
-                                                  (int)scB[j]);
-                        if (st < KS - 1) {
-                            // fragments of the next K-step of this stage
-    #pragma unroll
-                            for (int r = idx * RPM0; r < (idx + 1) * RPM0; ++r)
-                                if (r < NRD) read_frag(s, st + 1, r, fa[fb_cur ^ 1], fb[fb_cur ^ 1]);
-                        } else {
-                            // refill of slot s, then the next stage's scales and
-                            // K-step-0 fragments
-    #pragma unroll
-                            for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
-                                if (LOADER && o < L) issue_op(s, o);
-    #pragma unroll
-                            for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
-                                if (r < NRD) read_scale(sn, r, nA, nB);
-                                else if (r < 2 * NRD) read_frag(sn, 0, r - NRD, fa[0], fb[0]);
-                            }
+                        for (int r = idx * RPM0; r < (idx + 1) * RPM0; ++r)
+                            if (r < NRD) read_frag(s, st + 1, r, fa[fb_cur ^ 1], fb[fb_cur ^ 1]);
+                    } else {
+                        // refill of slot s, then the next stage's scales and
+                        // K-step-0 fragments
+#pragma unroll
+                        for (int o = idx * OPM; o < (idx + 1) * OPM; ++o)
+                            if (LOADER && o < L) issue_op(s, o);
+#pragma unroll
+                        for (int r = idx * RPM1; r < (idx + 1) * RPM1; ++r) {
+                            if (r < NRD) read_scale(sn, r, nA, nB);
+                            else if (r < 2 * NRD) read_frag(sn, 0, r - NRD, fa[0], fb[0]);
                         }
-                        // Pin this slot's LDS reads here: the MFMA is a pure
-                        // intrinsic, so without a memory clobber the optimizer
-                        // may hoist every later K-step's reads to the top of the
-                        // stage and keep all their fragments live at once.
-                        asm volatile("" ::: "memory");
-                        __builtin_amdgcn_sched_barrier(0);
                     }
+                    // Pin this slot's LDS reads here: the MFMA is a pure
+                    // intrinsic, so without a memory clobber the optimizer
+                    // may hoist every later K-step's reads to the top of the
+                    // stage and keep all their fragments live at once.
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
 #pragma unroll
@@ -494,25 +405,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
         // stages kt0 .. kt1-1 of this tile, refilling k-step kt + rk_off;
         // with a 2-slot ring, pairs of stages with compile-time slots
         auto run_range = [&](int kt0, int kt1, int rk_off) __attribute__((always_inline)) {
-            if constexpr (S == 2) {
-                int kt = kt0;
-                if (kt < kt1 && (u & 1)) {
-                    run_stage(kt + rk_off, SlotC<1>{});
-                    ++kt, ++u;
-                }
-                for (; kt + 1 < kt1; kt += 2) {
-                    run_stage(kt + rk_off, SlotC<0>{});
-                    ++u;
-                    run_stage(kt + 1 + rk_off, SlotC<1>{});
-                    ++u;
-                }
-                if (kt < kt1) {
-                    run_stage(kt + rk_off, SlotC<0>{});
-                    ++u;
-                }
-            } else {
-                for (int kt = kt0; kt < kt1; ++kt, ++u) run_stage(kt + rk_off, SlotC<-1>{});
-            }
+            for (int kt = kt0; kt < kt1; ++kt, ++u) run_stage(kt + rk_off);
         };
         run_range(0, nk - ra, ra);
         if constexpr (LOADER) set_refill_origin(mb0, nb0);
@@ -596,24 +489,366 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_f4f4_kernel(GemmArgs g
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Default: 8 waves in a 4 x 2 grid (64 x 128 per wave), two waves per SIMD,
-// so one wave's MFMAs keep the matrix core busy while the other is held by
-// load back-pressure or the stage barrier (measured 8192^3: 2 x 2 waves
-// 487 us, 4 x 2 waves 395 us).
-#ifndef LSMX_F4_WGM
-#define LSMX_F4_WGM 4
-#endif
-#ifndef LSMX_F4_WGN
-#define LSMX_F4_WGN 2
-#endif
-// K-steps per stage of the wide path (E8M0 scales, K % 256 == 0) and its ring
-// depth: 4 K-steps = 128-byte rows, two 64 KiB stages.
-#ifndef LSMX_F4_KS
-#define LSMX_F4_KS 4
-#endif
-#ifndef LSMX_F4_STAGES
-#define LSMX_F4_STAGES 2
-#endif
+// ---------------------------------------------------------------------------
+// The same pipeline on v_mfma_scale_f32_16x16x128_f8f6f4.  Under the chip's
+// power limit the 16 x 16 shape holds a higher clock at the same matrix-core
+// occupancy: per FLOP it reads and writes half the accumulator registers of
+// the 32 x 32 shape.  For this instruction lane 16g + r supplies 16 bytes,
+// one MX block, of row r and K-group g (g = 0..3).  A stage (128 bytes of
+// every row, 8 blocks) is two K-steps of 128 codes; at K-step st lane group g
+// takes block 2g + st, so one scale register per fragment row (the dword of
+// scale slice g >> 1, shifted right by 16 (g & 1)) serves the whole stage and
+// op_sel = st picks the block's byte.  A and B use the same assignment, so
+// the sum is unchanged.
+//
+// Per wave 64 x 128 = 4 x 8 tiles of 16 x 16.  MFMAs run column-block major
+// (j outer, i inner): the 4 A fragments of a K-step stay in registers while
+// the 8 B fragments stream past them, each read two column blocks ahead, so
+// only a few B fragments are live at once.  In K-step 1 the B fragments of
+// column blocks 2..7 are read early; once they have landed the slot is fully
+// read and the stage barrier follows, before the MFMAs of column block JB.
+// Those last (8 - JB) * 4 MFMAs cover the barrier, the refill of the slot
+// (loader waves) and the reads of the next stage's scales and first
+// fragments.  Ring, DMA addressing, schedule and loader waves are those of
+// gemm_f4f4_kernel's wide path.
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ v4f mfma_scale_f4_16(v4i a, v4i b, v4f c, int cbsz, int blgp, int opsel_a, int scale_a, int opsel_b,
+                                int scale_b) __asm("llvm.amdgcn.mfma.scale.f32.16x16x128.f8f6f4.v4i32.v4i32");
+
+template <int JB, int CT>
+__global__ __launch_bounds__(512, 1) void gemm_f4f4_mx16_kernel(GemmArgs g) {
+    using namespace f4;
+    constexpr int S = 2;                             // ring slots
+    constexpr int WGN = 2;                           // waves 4 x 2, 64 x 128 each
+    constexpr int TM = 4, TN = 8;                    // 16 x 16 tiles per wave
+    constexpr int BKB = 128, CPR = 8, RPI = 64 / CPR;
+    constexpr int TILE_B = BM * BKB;                 // bytes per operand per stage
+    constexpr int NSL = 2;                           // 128-code scale slices per stage
+    constexpr int SLB = BM * 4 + 64;                 // slice stride: +64 B keeps lane groups 0-1 and 2-3 on other banks
+    constexpr int NLW = 4;                           // loader waves
+    constexpr int XA = (TILE_B / 16) / (64 * NLW);   // 16-byte DMA slots per loader lane per operand
+    constexpr int L = 2 * XA + 1;                    // loads per loader lane per stage (+1: a 1 KiB scale slice)
+    constexpr int NPOST = (TN - JB) * TM;            // K-step 1 MFMAs after the barrier
+    static_assert(JB >= 2 && JB < TN, "barrier position");
+    static_assert(BN == 256 && BM == 256, "256 x 256 tiles");
+    __shared__ __attribute__((aligned(16))) uint8_t sA[S][TILE_B];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[S][TILE_B];
+    __shared__ __attribute__((aligned(16))) uint8_t sSA[S][NSL * SLB];
+    __shared__ __attribute__((aligned(16))) uint8_t sSB[S][NSL * SLB];
+
+    const int tiles_m = (int)((g.M + BM - 1) / BM), tiles_n = (int)((g.N + BN - 1) / BN);
+    const int tiles = tiles_m * tiles_n;
+    const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int nk = (int)(g.K / (2 * BKB));
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int r16 = lane & 15, grp = lane >> 4;
+
+    // ---- DMA addressing (loader waves), as in gemm_f4f4_kernel.  Scales are
+    // K-major ([K/128][rows][4]): loader wave w loads the 1 KiB slice w & 1
+    // of operand (w >> 1) & 1 of the refill stage with one 16-byte DMA per
+    // lane.
+    const int drow0 = wave * RPI + lane / CPR;
+    const uint32_t offA0 = (uint32_t)(drow0 * g.lda + ((lane % CPR) ^ f4_swz<CPR>(drow0)) * 16);
+    const uint32_t offB0 = (uint32_t)(drow0 * g.ldb + ((lane % CPR) ^ f4_swz<CPR>(drow0)) * 16);
+    const uint32_t stepA = (uint32_t)(NLW * RPI * g.lda), stepB = (uint32_t)(NLW * RPI * g.ldb);
+    const bool s_b = (wave >> 1) & 1;                // this loader's scale operand and slice
+    const int s_j = wave & 1;
+    const int64_t s_ld = s_b ? g.ld_sb : g.ld_sa;
+    const uint64_t s_bytes = ((g.K / 128 - 1) * s_ld + (s_b ? g.N : g.M)) * 4;
+    static_assert(GROUP_M <= 4, "tile_coords divides by group heights up to 4");
+    const TileMap tmap = make_tile_map(tiles_m, tiles_n, GROUP_M);
+    auto tile_of = [&](int ti, int64_t &m0, int64_t &n0) {
+        int tm, tn;
+        ti = imax(0, imin(ti, my_tiles - 1));
+        tile_coords((int)blockIdx.x + ti * (int)gridDim.x, tmap, tm, tn);
+        m0 = (int64_t)tm * BM;
+        n0 = (int64_t)tn * BN;
+    };
+    struct Panel {
+        const uint8_t *p;
+        int64_t n;
+    };
+    Panel pA, pB, pS;
+    const int64_t sstep = NSL * s_ld * 4;            // scale bytes one stage advances
+    auto set_refill_origin = [&](int64_t m0, int64_t n0) {
+        pA = Panel{g.a + m0 * g.lda, min(g.M - m0, (int64_t)BM) * g.lda};
+        pB = Panel{g.b + n0 * g.ldb, min(g.N - n0, (int64_t)BN) * g.ldb};
+        // rows past the operand read other scales or zeros: their products
+        // only reach outputs that are not stored
+        const int64_t sb0 = (s_j * s_ld + (s_b ? n0 : m0)) * 4;
+        pS = Panel{reinterpret_cast<const uint8_t *>(s_b ? g.sb : g.sa) + sb0, (int64_t)s_bytes - sb0};
+    };
+    auto set_refill_tile = [&](int ti) {
+        int64_t m0, n0;
+        tile_of(ti, m0, n0);
+        set_refill_origin(m0, n0);
+    };
+    v4i_rsrc rsA, rsB, rsS;
+    auto make_desc_a = [&](int kt) {
+        const int64_t ko = (int64_t)kt * BKB;
+        rsA = buf_rsrc(pA.p + ko, (uint64_t)(pA.n - ko));
+    };
+    auto make_desc_b = [&](int kt) {
+        const int64_t ko = (int64_t)kt * BKB;
+        rsB = buf_rsrc(pB.p + ko, (uint64_t)(pB.n - ko));
+    };
+    auto make_desc_s = [&](int kt) {
+        const int64_t so = (int64_t)kt * sstep;
+        rsS = buf_rsrc(pS.p + so, (uint64_t)(pS.n - so));
+    };
+    auto issue_op = [&](int s, int q) {
+        if (q < 2 * XA) {
+            const int i = q >> 1;
+            const uint32_t m0 = lds_u32((q & 1) ? &sB[0][0] : &sA[0][0]) + s * TILE_B + (i * NLW + wave) * 1024;
+            if ((q & 1) == 0) dma_x4_at(offA0, i, stepA, rsA, m0);
+            else dma_x4_at(offB0, i, stepB, rsB, m0);
+            return;
+        }
+        dma_x4((uint32_t)lane * 16, rsS, lds_u32(s_b ? &sSB[s][s_j * SLB] : &sSA[s][s_j * SLB]));
+    };
+
+    // ---- fragment and scale reads.  Rows of fragment q start 16 q rows
+    // apart, so the chunk swizzle ((row >> 1) & 7) depends on r16 only and
+    // each read is a per-lane offset plus an immediate.
+    const int fA0 = (wm * 64) * BKB, fB0 = (wn * 128) * BKB;
+    uint32_t loff[2];
+    for (int st = 0; st < 2; ++st) loff[st] = (uint32_t)(r16 * BKB + (((2 * grp + st) ^ ((r16 >> 1) & 7)) << 4));
+    // A lane reads only the two scale bytes its K-group uses (blocks 2g and
+    // 2g + 1: bytes 2 (g & 1) and +1 of slice g >> 1) with a 16-bit read at a
+    // per-lane byte offset; op_sel = st picks the byte.  Reading the dword
+    // and shifting it would make a VALU instruction wait for every scale read
+    // (measured: 245 against 223 us at 8192^3).
+    const uint32_t soff = (uint32_t)((grp >> 1) * SLB + r16 * 4 + 2 * (grp & 1));
+    auto rd_a = [&](int s, int st, int i) -> v4i {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(&sA[s][fA0 + i * 16 * BKB] + loff[st]);
+        return v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+    };
+    auto rd_b = [&](int s, int st, int j) -> v4i {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(&sB[s][fB0 + j * 16 * BKB] + loff[st]);
+        return v4i{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+    };
+    auto rd_sa = [&](int s, int i) -> uint32_t {
+        return *reinterpret_cast<const uint16_t *>(&sSA[s][(wm * 64 + 16 * i) * 4] + soff);
+    };
+    auto rd_sb = [&](int s, int j) -> uint32_t {
+        return *reinterpret_cast<const uint16_t *>(&sSB[s][(wn * 128 + 16 * j) * 4] + soff);
+    };
+
+    auto body = [&](auto loader_c) __attribute__((always_inline)) {
+    constexpr bool LOADER = decltype(loader_c)::value;
+    v4f acc[TM][TN];
+    // A scales live for the whole stage (both K-steps); a B fragment's scale
+    // is read with it and lives only as long as the fragment
+    uint32_t scA[TM], nA[TM], scB[TN];
+    v4i fa[2][TM], fb[TN];
+
+    // ---- prologue: fill the ring, publish stage 0, read its first operands
+    if constexpr (LOADER) {
+        int cur = -1;
+#pragma unroll
+        for (int p = 0; p < S; ++p) {
+            const int ti = stage_tile_iter(p, nk, my_tiles);
+            if (ti != cur) {
+                set_refill_tile(ti);
+                cur = ti;
+            }
+            make_desc_a(p % nk);
+            make_desc_b(p % nk);
+            make_desc_s(p % nk);
+#pragma unroll
+            for (int q = 0; q < L; ++q) issue_op(p, q);
+        }
+    }
+    wait_vm_barrier<(S - 1) * L>();
+#pragma unroll
+    for (int i = 0; i < TM; ++i) scA[i] = rd_sa(0, i);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[0][i] = rd_a(0, 0, i);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        fb[j] = rd_b(0, 0, j);
+        scB[j] = rd_sb(0, j);
+    }
+
+    const bool vec_c = ((reinterpret_cast<uintptr_t>(g.c) & 15) == 0) && (g.ldc % 4 == 0) && g.ldc < ((int64_t)1 << 26);
+    const int qa = S / nk, ra = S % nk;
+    int u = 0;
+    for (int ti = 0; ti < my_tiles; ++ti) {
+        int64_t mb0 = 0, nb0 = 0;
+        if constexpr (LOADER) {
+            tile_of(ti + qa + 1, mb0, nb0);
+            set_refill_tile(ti + qa);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+        auto run_stage = [&](const int rk, auto slot_c) __attribute__((always_inline)) {
+            constexpr int s = decltype(slot_c)::value;
+            constexpr int sn = (s + 1) % S;
+            auto refill_desc_part = [&](int c) {
+                int k = __builtin_amdgcn_readfirstlane(rk);
+                asm volatile("" : "+s"(k));
+                if (c == 0) make_desc_a(k);
+                else if (c == 1) make_desc_b(k);
+                else make_desc_s(k);
+            };
+            // B fragment j of K-step st from slot sl; its scale register
+            // serves both K-steps and is read with the step-0 fragment
+            auto load_b = [&](int sl, int st, int j) __attribute__((always_inline)) {
+                fb[j] = rd_b(sl, st, j);
+                if (st == 0) scB[j] = rd_sb(sl, j);
+            };
+            // next-stage reads after the barrier, in the order they are
+            // needed: A(0, i) with the A scales, B(0, 0..1) with theirs
+            constexpr int NNEXT = 2 * TM + 2;
+            auto next_read = [&](int k) {
+                // 0: A0 1: B0 2: sA0 3: A1 4: sA1 5: A2 6: sA2 7: A3 8: sA3 9: B1
+                if (k == 1) load_b(sn, 0, 0);
+                else if (k == 9) load_b(sn, 0, 1);
+                else {
+                    const int i = k < 2 ? 0 : (k - 1) >> 1;
+                    if (k == 0 || (k > 1 && (k & 1))) fa[0][i] = rd_a(sn, 0, i);
+                    else nA[i] = rd_sa(sn, i);
+                }
+            };
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+#pragma unroll
+                for (int idx = 0; idx < TM * TN; ++idx) {
+                    const int j = idx / TM, i = idx % TM;
+                    if (st == 1 && idx == JB * TM) {
+                        // this wave's reads of slot s are complete; once all
+                        // waves pass the barrier the slot is free and stage
+                        // u + 1 has landed
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        stage_barrier<LOADER, (S - 2) * L>();
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    acc[i][j] = mfma_scale_f4_16(fa[st][i], fb[j], acc[i][j], 4, 4, st, (int)scA[i], st, (int)scB[j]);
+                    if (st == 0) {
+                        if (LOADER && idx < 3) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            refill_desc_part(idx);
+                        }
+                        if (i == 0) {
+                            if (j + 2 < TN) load_b(s, 0, j + 2);
+                            else load_b(s, 1, j + 2 - TN);
+                        }
+                        if (i == 2 && j < TM) fa[1][j] = rd_a(s, 1, j);
+                    } else if (idx < JB * TM) {
+                        // B fragments 2..7 of K-step 1, spread over the MFMAs before the barrier
+                        constexpr int NR = TN - 2;
+#pragma unroll
+                        for (int k = 0; k < NR; ++k)
+                            if (idx == k * (JB * TM - 2) / NR) load_b(s, 1, 2 + k);
+                    } else {
+                        const int p = idx - JB * TM;
+#pragma unroll
+                        for (int k = p * NNEXT / NPOST; k < (p + 1) * NNEXT / NPOST; ++k) next_read(k);
+#pragma unroll
+                        for (int o = p * L / NPOST; o < (p + 1) * L / NPOST; ++o)
+                            if (LOADER) issue_op(s, o);
+                    }
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i) scA[i] = nA[i];
+        };
+        auto run_range = [&](int kt0, int kt1, int rk_off) __attribute__((always_inline)) {
+            int kt = kt0;
+            if (kt < kt1 && (u & 1)) {
+                run_stage(kt + rk_off, SlotC<1>{});
+                ++kt, ++u;
+            }
+            for (; kt + 1 < kt1; kt += 2) {
+                run_stage(kt + rk_off, SlotC<0>{});
+                ++u;
+                run_stage(kt + 1 + rk_off, SlotC<1>{});
+                ++u;
+            }
+            if (kt < kt1) {
+                run_stage(kt + rk_off, SlotC<0>{});
+                ++u;
+            }
+        };
+        run_range(0, nk - ra, ra);
+        if constexpr (LOADER) set_refill_origin(mb0, nb0);
+        run_range(nk - ra, nk, ra - nk);
+
+        // ---- epilogue.  acc[i][j] element e sits at row 16 i + 4 grp + e,
+        //      column 16 j + r16; a 4 x 4 transpose inside each quad of lanes
+        //      gives every lane 4 consecutive columns of row 16 i + 4 grp + q.
+        int64_t m0, n0;
+        tile_of(ti, m0, n0);
+        // lane-dependent epilogue values are derived here from an opaque copy
+        // of the lane id: hoisted out of the tile loop they would stay live
+        // (and spill) through every stage
+        int el = lane;
+        asm volatile("" : "+v"(el));
+        const int q = el & 3, egrp = el >> 4, er16 = el & 15;
+        if (vec_c && m0 + BM <= g.M && n0 + BN <= g.N) {
+            constexpr int EB = CT == LSMX_F32 ? 4 : 2;
+            const uint8_t *cw = reinterpret_cast<const uint8_t *>(g.c) + ((m0 + wm * 64) * g.ldc + n0 + wn * 128) * EB;
+            if constexpr (CT == LSMX_F32) {
+                const uint32_t loffc = (uint32_t)(((4 * egrp + q) * g.ldc + (er16 & ~3)) * EB);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    uint8_t *crow = const_cast<uint8_t *>(cw) + (16 * i) * g.ldc * EB;
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        float x[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+                        quad_transpose(x, q);
+                        *reinterpret_cast<u32x4 *>(crow + loffc + j * 16 * EB) = u32x4{f2u(x[0]), f2u(x[1]), f2u(x[2]), f2u(x[3])};
+                    }
+                }
+            } else {
+                // column blocks j and j + 1 share one 16-byte store per lane
+                // (pack16_rows8 with the second block in place of rows + 8):
+                // lanes with bit 2 clear store 8 columns of block j, the
+                // others 8 columns of block j + 1
+                const bool odd = (el & 4) != 0;
+                const uint32_t loffc = (uint32_t)(((4 * egrp + q) * g.ldc + (odd ? 16 : 0) + 8 * ((el >> 3) & 1)) * EB);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    uint8_t *crow = const_cast<uint8_t *>(cw) + (16 * i) * g.ldc * EB;
+#pragma unroll
+                    for (int jp = 0; jp < TN / 2; ++jp) {
+                        const float x0[4] = {acc[i][2 * jp][0], acc[i][2 * jp][1], acc[i][2 * jp][2], acc[i][2 * jp][3]};
+                        const float x1[4] = {acc[i][2 * jp + 1][0], acc[i][2 * jp + 1][1], acc[i][2 * jp + 1][2],
+                                             acc[i][2 * jp + 1][3]};
+                        *reinterpret_cast<u32x4 *>(crow + loffc + jp * 32 * EB) = pack16_rows8<CT>(x0, x1, q, odd);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    float x[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+                    quad_transpose(x, q);
+                    const int64_t row = m0 + wm * 64 + 16 * i + 4 * egrp + q;
+                    const int64_t col = n0 + wn * 128 + 16 * j + (er16 & ~3);
+                    if (row < g.M)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            if (col + c < g.N) store_c<CT>(g.c, row * g.ldc + col + c, x[c]);
+                }
+        }
+    }
+    };
+    if (wave < NLW) body(BoolC<true>{});
+    else body(BoolC<false>{});
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 
 static int num_cus() {
     static int cus = 0;
@@ -629,25 +864,26 @@ static int num_cus() {
 }
 
 hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s) {
-    constexpr int W = LSMX_F4_WGM, Z = LSMX_F4_WGN;
     const int tiles = (int)(((g.M + f4::BM - 1) / f4::BM) * ((g.N + f4::BN - 1) / f4::BN));
     const int grid = tiles < num_cus() ? tiles : num_cus();
-    const dim3 blk(64 * W * Z);
-#define LSMX_G(F, CT, S, KS) hipLaunchKernelGGL((gemm_f4f4_kernel<F, CT, S, W, Z, KS>), dim3(grid), blk, 0, s, g)
-#define LSMX_GC(F, S, KS)                                             \
-    do {                                                              \
-        if (g.c_dtype == LSMX_F32) LSMX_G(F, LSMX_F32, S, KS);        \
-        else if (g.c_dtype == LSMX_BF16) LSMX_G(F, LSMX_BF16, S, KS); \
-        else LSMX_G(F, LSMX_F16, S, KS);                              \
+#define LSMX_GC(K, ...)                                                                        \
+    do {                                                                                       \
+        if (g.c_dtype == LSMX_F32) hipLaunchKernelGGL((K<__VA_ARGS__, LSMX_F32>), grid, 512, 0, s, g);   \
+        else if (g.c_dtype == LSMX_BF16) hipLaunchKernelGGL((K<__VA_ARGS__, LSMX_BF16>), grid, 512, 0, s, g); \
+        else hipLaunchKernelGGL((K<__VA_ARGS__, LSMX_F16>), grid, 512, 0, s, g);                 \
     } while (0)
-    const bool wide = g.K % (64 * LSMX_F4_KS) == 0;
-    if (g.scale_fmt == LSMX_SCALE_F32) LSMX_GC(LSMX_SCALE_F32, 3, 2);  // 16-byte scale rows: narrow stages
-    else if (g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR && wide) LSMX_GC(LSMX_SCALE_E8M0_KMAJOR, LSMX_F4_STAGES, LSMX_F4_KS);
-    else if (g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) LSMX_GC(LSMX_SCALE_E8M0_KMAJOR, 4, 2);
-    else if (wide) LSMX_GC(LSMX_SCALE_E8M0, LSMX_F4_STAGES, LSMX_F4_KS);
-    else LSMX_GC(LSMX_SCALE_E8M0, 4, 2);
+    // K-major E8M0 scales and whole 256-code stages: the 16 x 16 x 128
+    // kernel, with the stage barrier before column block 4 of its second
+    // K-step.  Row-major E8M0 (one scale request per row), fp32 scales (16
+    // bytes per row per 128 codes) and K % 256 != 0 run the 32 x 32 x 64
+    // kernel on 64-byte stages in a 3- or 4-slot ring; the Python layer
+    // regroups scales to K-major before it calls, so it always takes the
+    // first path when K allows.
+    if (g.K % 256 == 0 && g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) LSMX_GC(gemm_f4f4_mx16_kernel, 4);
+    else if (g.scale_fmt == LSMX_SCALE_F32) LSMX_GC(gemm_f4f4_kernel, LSMX_SCALE_F32, 3);
+    else if (g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) LSMX_GC(gemm_f4f4_kernel, LSMX_SCALE_E8M0_KMAJOR, 4);
+    else LSMX_GC(gemm_f4f4_kernel, LSMX_SCALE_E8M0, 4);
 #undef LSMX_GC
-#undef LSMX_G
     return hipGetLastError();
 }
 

@@ -30,6 +30,16 @@ LSMX_DEV void dma_x4(uint32_t off, v4i_rsrc r, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(off), "s"(r),
                  "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
 }
+// dma_x4 of the lane offset off0 + i * step, formed inside the asm (i a
+// compile-time constant after unrolling, step < 2^24 wave-uniform): the
+// compiler cannot hoist one offset register per i out of the loop.
+LSMX_DEV void dma_x4_at(uint32_t off0, int i, uint32_t step, v4i_rsrc r, uint32_t m0) {
+    uint32_t off;
+    asm volatile("v_mad_u32_u24 %0, %1, %2, %3\n\ts_mov_b32 m0, %5\n\tbuffer_load_dwordx4 %0, %4, 0 offen lds"
+                 : "=&v"(off)
+                 : "i"(i), "s"(step), "v"(off0), "s"(r), "s"(__builtin_amdgcn_readfirstlane(m0))
+                 : "memory");
+}
 LSMX_DEV void dma_x1(uint32_t off, v4i_rsrc r, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(off), "s"(r),
                  "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory");

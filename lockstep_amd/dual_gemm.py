@@ -19,7 +19,7 @@ import torch
 
 from . import _capi as C
 from . import fp4 as _fp4
-from .mxfp4_gemm import _rows16, _scales, kmajor_operand, mxfp4_gemm_bf16
+from .mxfp4_gemm import _rows16, _wscales, kmajor_operand, mxfp4_gemm_bf16
 
 
 def slot_offset(K: int) -> int:
@@ -70,7 +70,7 @@ def dual_mxfp4(a0, a1, w_pk, w_scale, out_dtype=torch.bfloat16):
     if a0.stride(0) != a1.stride(0):
         a0, a1 = a0.contiguous(), a1.contiguous()
     w_pk = _rows16(w_pk)
-    w_scale = _scales(w_scale, N, K // 32)
+    w_scale = _wscales(w_scale, N, K // 32)
     c0 = torch.empty((M, N), device=a0.device, dtype=out_dtype)
     c1 = torch.empty_like(c0)
     if M == 0 or N == 0:

@@ -6,9 +6,11 @@ are the fused quantize+pack kernel (packed nibbles + E8M0 bytes, read straight
 by the scaled MFMA GEMM).  Backward (fp4_linear.py:42-45): unquantized
 straight-through, dX = gy @ w, dW = gy^T @ x at the input precision.
 
-kernel() returns the gfx950 path, or None when no gfx950 GPU is present; the
-reference's off-H100 fake-quant fallback does not exist here: without the
-GPU path the layer raises.
+kernel() returns the packed-operand GEMM (mxfp4_gemm_packed, the callable the
+reference's kernel() returns: fp4_linear.py:16-25) on a gfx950, or None when
+no gfx950 GPU is present.  The reference's off-H100 fake-quant fallback does
+not exist here: without the GPU path the layer raises, and path() says
+"unavailable" where the reference would say "fake-quant".
 
 MXFP4Linear(..., quantized_backward=True) (and mxfp4_matmul_q) also runs the
 backward in MXFP4, which the reference does not: for Y = X W^T with X [T, K]
@@ -38,7 +40,8 @@ from .mxfp4_gemm import mxfp4_gemm_packed
 
 @functools.cache
 def kernel():
-    """The gfx950 MXFP4 GEMM path (quantize + pack + scaled-MFMA GEMM), else None."""
+    """The gfx950 MXFP4 GEMM (mxfp4_gemm_packed: packed codes, scales, out_dtype),
+    else None."""
     if not torch.cuda.is_available():
         return None
     try:
@@ -47,7 +50,7 @@ def kernel():
         return None
     if C.load().lsmx_device_check() != C.OK:
         return None
-    return _forward_hip
+    return mxfp4_gemm_packed
 
 
 def path():
@@ -55,11 +58,13 @@ def path():
 
 
 def _forward_hip(x2: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """The forward of fp4_linear.py:34-40 on the GPU: quantize X and W along K
+    (fused quantize + pack kernels, E8M0 scales) and call kernel()."""
     # K-major E8M0 scales: the layout the GEMM streams fastest (same bits out)
     lay = "kmajor" if x2.shape[-1] % 128 == 0 else "rows"
     xp, xs = fp4.quantize_pack_mxfp4(x2, scale_layout=lay)
     wp, ws = fp4.quantize_pack_mxfp4(w, scale_layout=lay)
-    return mxfp4_gemm_packed(xp, wp, xs, ws, out_dtype=x2.dtype)
+    return kernel()(xp, wp, xs, ws, out_dtype=x2.dtype)
 
 
 def mxfp4_backward(gy: torch.Tensor, x: torch.Tensor, w: torch.Tensor):
@@ -85,11 +90,10 @@ class _MXFP4Matmul(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w):
         ctx.save_for_backward(x, w)
-        k = kernel()
-        if k is None:
+        if kernel() is None:
             raise RuntimeError("MXFP4Linear needs a gfx950 GPU and liblsmx.so (path() == "
                                f"{path()!r}); there is no CPU fallback")
-        return k(x, w)
+        return _forward_hip(x, w)
 
     @staticmethod
     def backward(ctx, gy):
@@ -109,8 +113,7 @@ class _MXFP4MatmulQ(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w):
-        k = kernel()
-        if k is None:
+        if kernel() is None:
             raise RuntimeError("MXFP4Linear needs a gfx950 GPU and liblsmx.so (path() == "
                                f"{path()!r}); there is no CPU fallback")
         T, K = x.shape
@@ -119,7 +122,7 @@ class _MXFP4MatmulQ(torch.autograd.Function):
         if T % 128 or N % 128 or K % 128:
             ctx.fused = False
             ctx.save_for_backward(x, w)
-            return k(x, w)
+            return _forward_hip(x, w)
         ctx.fused = True
         xr, xrs, xc, xcs = fp4.quantize_pack_mxfp4_2d(x, scale_layout="kmajor")
         wr, wrs, wc, wcs = fp4.quantize_pack_mxfp4_2d(w, scale_layout="kmajor")

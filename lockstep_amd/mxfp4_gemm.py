@@ -2,10 +2,11 @@
 
 The reference emulates MXFP4 on Hopper FP8 tensor cores and promotes to an
 fp32 accumulator at every 32-block to apply the scales (mxfp4_gemm.py:1-14).
-gfx950 has block-scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4): each lane
-hands the instruction 32 FP4 codes of one row plus that block's E8M0 scale,
-so no promotion step exists and the packed nibbles go straight from HBM to
-the matrix cores.  Kernel: lockstep_amd/csrc/gemm_f4f4.hip.
+gfx950 has block-scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4 and its
+32 x 32 x 64 form): each lane hands the instruction 32 FP4 codes of one row
+plus that block's E8M0 scale, so no promotion step exists and the packed
+nibbles go straight from HBM to the matrix cores.  Kernels:
+lockstep_amd/csrc/gemm_f4f4.hip.
 
 Same names and signatures as mxfp4_gemm.py:23-174; the `CFG` dict keeps the
 reference's keys for callers that read it, with this build's tile sizes.
@@ -18,10 +19,10 @@ import torch
 from . import _capi as C
 from . import fp4 as _fp4
 
-# Tile configuration of the f4 x f4 kernel that runs at K % 256 == 0 with
-# E8M0 scales (csrc/gemm_f4f4.hip), under the reference's CFG keys:
-# 256 x 256 tiles, SUB*32 = 256 K codes (four 64-code MFMA K-steps) per
-# stage, 4-row tile groups, 8 waves of 64 lanes, a 2-slot LDS ring.
+# Tile configuration of the f4 x f4 kernel that runs at K % 256 == 0
+# (csrc/gemm_f4f4.hip, gemm_f4f4_mx16_kernel), under the reference's CFG
+# keys: 256 x 256 tiles, SUB*32 = 256 K codes (two 128-code MFMA K-steps)
+# per stage, 4-row tile groups, 8 waves of 64 lanes, a 2-slot LDS ring.
 CFG = dict(BLOCK_M=256, BLOCK_N=256, SUB=8, GROUP_M=4, num_warps=8, num_stages=2)
 
 
@@ -54,9 +55,12 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
 
     Scales are fp32 powers of two (as fp4.quantize_mxfp4 returns) or E8M0
     bytes (as fp4.quantize_pack_mxfp4 returns), row-major [rows, K//32] or
-    K-major [K//128, rows, 4] (quantize_pack_mxfp4(..., scale_layout="kmajor"),
-    the fastest form); both operands must use the same format.  Returns
-    C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
+    K-major [K//128, rows, 4] (quantize_pack_mxfp4(..., scale_layout="kmajor"));
+    both operands must use the same format.  Row-major scales are regrouped
+    to K-major E8M0 on the device first (fp32 through lsmx_scale_to_e8m0, a
+    scale that is not a power of two becoming E8M0 NaN; E8M0 bytes through a
+    dword transpose), so every format runs the same kernel and gives the same
+    bits.  Returns C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
     M, Kh = a_pk.shape
     N, Kh2 = bt_pk.shape
     K = Kh * 2
@@ -79,11 +83,12 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
         a_scale, b_scale = a_scale.contiguous(), b_scale.contiguous()
         fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
     else:
-        a_scale = _scales(a_scale, M, K // 32)
-        b_scale = _scales(b_scale, N, K // 32)
-        fmt = _fp4._scale_fmt(a_scale)
-        lsa = a_scale.stride(0) if M > 1 else K // 32
-        lsb = b_scale.stride(0) if N > 1 else K // 32
+        # the reference's spelling (fp32 scales from quantize_mxfp4) and
+        # row-major E8M0 bytes: regroup to the K-major layout the GEMM
+        # streams fastest (one dword per row per 128 codes, rows contiguous)
+        a_scale = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
+        b_scale = _e8m0_kmajor(b_scale, N, K // 32, transposed=False)
+        fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
     C.call("lsmx_gemm_f4f4", a_pk.data_ptr(), a_pk.stride(0) if M > 1 else Kh,
            a_scale.data_ptr(), lsa, bt_pk.data_ptr(), bt_pk.stride(0) if N > 1 else Kh,
            b_scale.data_ptr(), lsb, fmt, c.data_ptr(), _out_code(out_dtype), N, M, N, K,
@@ -113,7 +118,7 @@ def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
     C.require_device(a, w_pk, w_scale)
     a = _rows16(a)
     w_pk = _rows16(w_pk)
-    w_scale = _scales(w_scale, N, K // 32)
+    w_scale = _wscales(w_scale, N, K // 32)
     c = torch.empty((M, N), device=a.device, dtype=out_dtype)
     if M == 0 or N == 0:
         return c
@@ -130,6 +135,19 @@ def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
            w_pk.stride(0) if N > 1 else Kh, w_scale.data_ptr(), w_scale.stride(0) if N > 1 else K // 32,
            _fp4._scale_fmt(w_scale), c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
     return c
+
+
+def _wscales(s: torch.Tensor, rows: int, nkb: int) -> torch.Tensor:
+    """Weight scales for the weight-only kernels as E8M0 bytes [rows, nkb]
+    with 16-byte aligned rows: fp32 powers of two are converted on the device
+    (a non-power of two becomes E8M0 NaN, as the kernels' own fp32 path
+    treats it), so that fp32 and E8M0 forms of one weight run the same
+    kernels -- the ring and split-K kernels read E8M0 rows -- and give the
+    same bits."""
+    s = _scales(s, rows, nkb)
+    if s.dtype == torch.float32:
+        s = _e8m0_rows(s, rows, nkb, transposed=False)
+    return s
 
 
 def mxfp4_linear_w(a, w_pk, w_scale, out_dtype=None):

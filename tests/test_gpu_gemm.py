@@ -238,6 +238,8 @@ def test_fp4_linear_forward_backward(dev, mods, oracle):
     """fp4_linear.py:34-45: MXFP4 forward (X and W quantized), STE backward."""
     fp4, mg, _, fl = mods
     assert fl.path() == "hip-mxfp4"
+    # kernel() returns the packed-operand GEMM, as fp4_linear.py:16-25 does
+    assert fl.kernel() is mg.mxfp4_gemm_packed
     torch.manual_seed(0)
     layer = fl.MXFP4Linear(1024, 512).to(dev)
     x = torch.randn(4, 64, 1024, device=dev, requires_grad=True)

@@ -68,3 +68,44 @@ def test_noalloc_validates_like_the_workspace_form():
                                     14336, 4096, None)
     assert rc == C.ERR_ARG
     assert "a1 and c1" in C.last_error()
+
+
+def test_noalloc_allocates_nothing_and_replays_under_graph_capture():
+    """After a first call on the device (which looks up the scratch address),
+    a call changes neither torch's allocator nor the device's free memory; and
+    the call captured in a CUDA graph replays to the eager bits (the stated
+    use: callers that cannot allocate, such as code under graph capture)."""
+    from lockstep_amd import _capi as C
+    from lockstep_amd import fp4
+    dev = torch.device("cuda", 0)
+    M, N, K = 128, 14336, 4096
+    print(f"[noalloc] capture M={M} N={N} K={K}", flush=True)
+    assert C.load().lsmx_gemm_bf16f4_workspace(M, N, K, 0) > 0, "this shape must use the scratch"
+    a0, _, wpk, we8 = _operands(dev, fp4, M, N, K, seed=5)
+    c = torch.empty((M, N), device=dev, dtype=torch.float32)
+
+    def call():
+        C.call("lsmx_gemm_bf16f4_noalloc", a0.data_ptr(), None, K, wpk.data_ptr(), K // 2, we8.data_ptr(), K // 32,
+               C.SCALE_E8M0, c.data_ptr(), None, C.F32, N, M, N, K, C.stream_of(c))
+
+    call()
+    torch.cuda.synchronize()
+    ref = c.clone()
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    alloc0, reserved0 = torch.cuda.memory_allocated(), torch.cuda.memory_reserved()
+    call()
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert (torch.cuda.memory_allocated(), torch.cuda.memory_reserved()) == (alloc0, reserved0)
+    assert free1 == free0
+    assert torch.equal(c, ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        c.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, ref)
