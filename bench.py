@@ -312,6 +312,9 @@ def main():
     apk, ae8 = fp4.quantize_pack_mxfp4(A, scale_layout="kmajor")
     bpk, be8 = fp4.quantize_pack_mxfp4(B, scale_layout="kmajor")
     sustained_ms = _time_loop(lambda: mxfp4_gemm.mxfp4_gemm_packed(apk, bpk, ae8, be8), n=50)
+    ref_spelling = None
+    if not args.no_configs:
+        ref_spelling = bench_cfg4_reference_spelling(torch, A, B, apk, bpk, ae8, be8)
     del apk, bpk
 
     flop = 2.0 * n * n * n
@@ -320,7 +323,7 @@ def main():
     q_bytes = n * n * (4 + 0.5 + 1.0 / 32)            # fp32 in, packed nibbles + E8M0 out
     quant_gbs = q_bytes / (quant_ms * 1e-3) / 1e9
     value = flop / (ms_per_step * 1e-3) / 1e12
-    gemm_clock = clock_from_profiles("gemm_f4f4_kernel")
+    gemm_clock = clock_from_profiles("gemm_f4f4_mx16_kernel")
 
     out = {
         "metric": f"MXFP4 GEMM TFLOPS at {n}^3 (cfg4: on-the-fly quantize of A and B + f4xf4 GEMM)",
@@ -347,8 +350,8 @@ def main():
                      "frac_hbm": round(quant_gbs / PEAK_HBM_GBS, 4), "bytes_per_launch": int(q_bytes),
                      "how": "8 launches back to back (A, B alternating), events around the batch",
                      "isolated_launch_ms": round(quant_iso_ms, 4)},
-        "roofline": roofline("mfma", "gemm_f4f4_kernel", gemm_tflops, PEAK_FP4_TFLOPS, "TFLOP/s",
-                             traffic_from_profiles("gemm_f4f4_kernel"), gemm_clock),
+        "roofline": roofline("mfma", "gemm_f4f4_mx16_kernel", gemm_tflops, PEAK_FP4_TFLOPS, "TFLOP/s",
+                             traffic_from_profiles("gemm_f4f4_mx16_kernel"), gemm_clock),
         "roofline_quantize": roofline("hbm", "quantize_rows_kernel", quant_gbs, PEAK_HBM_GBS, "GB/s",
                                       traffic_from_profiles("quantize_rows_kernel")),
     }
@@ -375,12 +378,48 @@ def main():
             "ms": round(ms_per_step, 4), "rate": round(value, 1), "unit": "TFLOP/s",
             "roofline": out["roofline"], "roofline_quantize": out["roofline_quantize"],
             "cpu_baseline": cfg4_cpu})
+        out["configs"].insert(len(out["configs"]) - 1, ref_spelling)
     if args.suite:
         lines = bench_reference_rows(torch, dev)
         with open(args.suite, "w") as f:
             for ln in lines:
                 f.write(json.dumps(ln) + "\n")
     print(json.dumps(out), flush=True)
+
+
+def bench_cfg4_reference_spelling(torch, A, B, apk, bpk, ae8, be8):
+    """cfg4 through the reference's own call sequence (fp4_linear.py:36-39):
+    fp4.quantize_mxfp4 (unpacked codes, fp32 scales) and fp4.pack_fp4 per
+    operand, then mxfp4_gemm_packed with the fp32 scales -- which regroups
+    them to K-major E8M0 on the device and runs the kernel of the headline.
+    The GEMM call is timed against the headline's K-major call on the same
+    codes (isolated launches, medians)."""
+    from lockstep_amd import fp4, mxfp4_gemm
+    n = A.shape[0]
+
+    def quant(x):
+        c, s = fp4.quantize_mxfp4(x)
+        return fp4.pack_fp4(c), s
+
+    def step():
+        (pa, sa), (pb, sb) = quant(A), quant(B)
+        return mxfp4_gemm.mxfp4_gemm_packed(pa, pb, sa, sb, out_dtype=torch.bfloat16)
+
+    (pa, sa), (pb, sb) = quant(A), quant(B)
+    assert torch.equal(pa, apk) and torch.equal(pb, bpk)
+    gemm_ref = _time_events(lambda: mxfp4_gemm.mxfp4_gemm_packed(pa, pb, sa, sb, out_dtype=torch.bfloat16))
+    gemm_km = _time_events(lambda: mxfp4_gemm.mxfp4_gemm_packed(apk, bpk, ae8, be8, out_dtype=torch.bfloat16))
+    step_ms = _time_events(step, reps=10)
+    flop = 2.0 * n ** 3
+    return {"workload": f"cfg4 {n}^3 through the reference's spelling: quantize_mxfp4 (fp32 scales) + pack_fp4 "
+                        "per operand, mxfp4_gemm_packed with fp32 scales",
+            "ms": round(step_ms, 4), "rate": round(flop / step_ms / 1e9, 1), "unit": "TFLOP/s",
+            "gemm_call_ms": round(gemm_ref, 4), "gemm_call_kmajor_ms": round(gemm_km, 4),
+            "gemm_call_ratio": round(gemm_ref / gemm_km, 4),
+            "roofline": roofline("mfma", "gemm_f4f4_mx16_kernel after the scale regroup", flop / gemm_ref / 1e9,
+                                 PEAK_FP4_TFLOPS, "TFLOP/s"),
+            "note": "the GEMM call includes the two fp32 -> K-major E8M0 scale conversions (lsmx_scale_to_e8m0); "
+                    "the step adds the unpacked-code quantizer and pack_fp4 of both operands"}
 
 
 def cpu_cfg4(n):
@@ -553,7 +592,7 @@ def bench_cfg5(torch, dev, cpu, T=8192, H=2048, F=8192):
     r = {"workload": f"cfg5 MLP block fwd + MXFP4 bwd (tokens={T}, hidden={H}, ffn={F}, bf16): 6 two-axis "
                      "quantizations + 6 f4 x f4 GEMMs", "ms": round(tot, 4), "rate": round(fl / tot / 1e9, 1),
          "unit": "TFLOP/s", "gemm_ms": round(gemm_ms, 4), "quantize_ms": round(q_ms, 4),
-         "roofline": roofline("mfma", "gemm_f4f4_kernel (6 launches)", fl / gemm_ms / 1e9, PEAK_FP4_TFLOPS,
+         "roofline": roofline("mfma", "gemm_f4f4_mx16_kernel (6 launches)", fl / gemm_ms / 1e9, PEAK_FP4_TFLOPS,
                               "TFLOP/s"),
          "roofline_quantize": roofline("hbm", "quantize_2d_kernel (6 launches)", qbytes / q_ms / 1e6,
                                        PEAK_HBM_GBS, "GB/s"),

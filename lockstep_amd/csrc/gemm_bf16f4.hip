@@ -901,14 +901,8 @@ static bool ring_ok(const GemmArgs &g) {
 // weight is streamed once for both batches.  The summation order of an
 // output element depends on K only, so single and dual launches of the same
 // M and K give identical bits.
-#ifndef LSMX_SKINNY_WK
-#define LSMX_SKINNY_WK 8
-#endif
-#ifndef LSMX_SKINNY_U1
-#define LSMX_SKINNY_U1 2
-#endif
 namespace sk {
-constexpr int WK = LSMX_SKINNY_WK;  // waves per workgroup (K split)
+constexpr int WK = 8;  // waves per workgroup (K split)
 constexpr int CHUNK = 128;
 }  // namespace sk
 
@@ -917,7 +911,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // MT <= 2: at most 128 VGPRs, so two workgroups (16 waves) share a CU.
 template <int MT, int CT>
 __global__ __launch_bounds__(64 * sk::WK, MT <= 2 ? 4 : 2) void gemm_bf16f4_skinny_kernel(GemmArgs g) {
-    constexpr int U = MT == 1 ? LSMX_SKINNY_U1 : 1;  // chunks in flight per wave
+    constexpr int U = MT == 1 ? 2 : 1;  // chunks in flight per wave
     __shared__ float red[sk::WK][MT * CT * 256];
 
     const int lane = threadIdx.x & 63, wk = threadIdx.x >> 6;
@@ -1301,17 +1295,13 @@ static hipError_t launch_decode_r(GemmArgs g, hipStream_t s) {
     return hipGetLastError();
 }
 
-#ifndef LSMX_DECODE_R
-#define LSMX_DECODE_R 64
-#endif
-#ifndef LSMX_DECODE_MAX_M
-#define LSMX_DECODE_MAX_M 16
-#endif
+// up to 16 rows per batch (2 x 16 virtual rows for the dual form)
+constexpr int64_t kDecodeMaxM = 16;
 // up to 16 virtual rows: 64 weight rows per workgroup; 17 .. 32 (the dual
 // form): 32, so that the second activation tile's registers fit
 static hipError_t launch_decode(const GemmArgs &g, hipStream_t s) {
     const int64_t vm = g.a1 ? 2 * g.M : g.M;
-    return vm <= 16 ? launch_decode_r<LSMX_DECODE_R, 1>(g, s) : launch_decode_r<32, 2>(g, s);
+    return vm <= 16 ? launch_decode_r<64, 1>(g, s) : launch_decode_r<32, 2>(g, s);
 }
 
 // The decode kernel's scale loads: 16-byte aligned rows of either format
@@ -1463,9 +1453,7 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
 }
 
 // one activation row per batch (from two rows on the decode kernel is faster)
-#ifndef LSMX_GEMV_MAX_M
-#define LSMX_GEMV_MAX_M 1
-#endif
+constexpr int64_t kGemvMaxM = 1;
 constexpr int64_t kGemvMaxLds = 64 * 1024;   // activation bytes staged per workgroup
 
 static hipError_t launch_gemv(const GemmArgs &g, hipStream_t s) {
@@ -1492,9 +1480,7 @@ static hipError_t launch_gemv(const GemmArgs &g, hipStream_t s) {
 
 // up to 32 rows per batch (M = 16 against a 14336 x 4096 weight: 20 us against 34 us for the 128-row
 // ring tile, whose MFMAs would be 7/8 padding; from M = 64 the ring is faster)
-#ifndef LSMX_SKINNY_MAX_M
-#define LSMX_SKINNY_MAX_M 32
-#endif
+constexpr int64_t kSkinnyMaxM = 32;
 
 static int num_cus_w() {
     static int cus = 0;
@@ -1515,10 +1501,7 @@ static hipError_t launch_skinny(const GemmArgs &g, hipStream_t s) {
     // two 16-row weight tiles per workgroup (the activation loads then serve
     // twice the weight bytes) while that still gives every CU a workgroup;
     // MT <= 2 keeps two workgroups resident per CU either way
-#ifndef LSMX_SKINNY_CT2
-#define LSMX_SKINNY_CT2 1
-#endif
-    const int ct = (LSMX_SKINNY_CT2 && mt <= 4 && (g.N + 31) / 32 >= num_cus_w()) ? 2 : 1;
+    const int ct = (mt <= 4 && (g.N + 31) / 32 >= num_cus_w()) ? 2 : 1;
     const dim3 grid((unsigned)((g.N + 16 * ct - 1) / (16 * ct))), blk(64 * sk::WK);
 #define LSMX_S(MT, CT) hipLaunchKernelGGL((gemm_bf16f4_skinny_kernel<MT, CT>), grid, blk, 0, s, g)
     switch (mt * 10 + ct) {
@@ -1561,40 +1544,22 @@ template <int NB>
 static hipError_t launch_w4_any(const GemmArgs &g, hipStream_t s) {
     auto tiles = [&](int br, int bn) { return ((g.M + br / NB - 1) / (br / NB)) * ((g.N + bn - 1) / bn); };
     const int64_t cus = num_cus_w();
-#ifndef LSMX_W4_RING
-#define LSMX_W4_RING 1
-#endif
-#ifndef LSMX_RING_WGM
-#define LSMX_RING_WGM 2
-#endif
-#ifndef LSMX_RING_NLW
-#define LSMX_RING_NLW 4
-#endif
     // the ring kernel is worth it from half a wave of 256 x 256 tiles on (M = 1024, N = 14336: 224 tiles)
-#ifndef LSMX_HALF_TILE
-#define LSMX_HALF_TILE 1
-#endif
-#ifndef LSMX_HALF_S
-#define LSMX_HALF_S 4
-#endif
-#ifndef LSMX_HALF_NLW
-#define LSMX_HALF_NLW 4
-#endif
     // single form whose 256 x 256 tiles leave CUs idle while 128 x 256 tiles
     // still fit in one wave of workgroups: 128-row tiles, 1 x 8 waves (each
     // all 128 rows and a 32-column strip), loads from waves 0-3.  cfg2's
     // single batch (M = 2048 against a 4096 x 4096 weight, 128 -> 256
     // workgroups) 97 -> 63 us; M = 1024 against 8192 x 4096 91 -> 62 us
     if constexpr (NB == 1)
-        if (LSMX_HALF_TILE && ring_ok(g) && tiles(256, 256) < cus && tiles(128, 256) <= cus &&
+        if (ring_ok(g) && tiles(256, 256) < cus && tiles(128, 256) <= cus &&
             2 * tiles(128, 256) > cus)
-            return launch_ring<NB, 128, 256, LSMX_HALF_S, 1, LSMX_HALF_NLW>(g, s);
-    if (LSMX_W4_RING && ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3, LSMX_RING_WGM, LSMX_RING_NLW>(g, s);
+            return launch_ring<NB, 128, 256, 4, 1, 4>(g, s);
+    if (ring_ok(g) && 2 * tiles(256, 256) >= cus) return launch_ring<NB, 256, 256, 3, 2, 4>(g, s);
     if (tiles(256, 256) >= cus) return launch_w4<NB, 256, 256>(g, s);
     if (tiles(128, 128) >= cus) return launch_w4<NB, 128, 128>(g, s);
     // a few hundred rows: 128 x 64 tiles through a 4-slot DMA ring (N =
     // 14336, K = 4096, M = 128: 48 -> 38 us; M = 64: 44 -> 35 us against the skinny kernel)
-    if (LSMX_W4_RING && ring_ok(g)) return launch_ring<NB, 128, 64, 4>(g, s);
+    if (ring_ok(g)) return launch_ring<NB, 128, 64, 4>(g, s);
     return launch_w4<NB, 128, 64>(g, s);
 }
 
@@ -1617,7 +1582,7 @@ struct SplitPlan {
 };
 static SplitPlan splitk_plan(int64_t M, int64_t N, int64_t K) {
     SplitPlan best{1, 256};
-    if (M <= LSMX_SKINNY_MAX_M) return best;  // the GEMV and skinny kernels own these
+    if (M <= kSkinnyMaxM) return best;  // the GEMV and skinny kernels own these
     const int64_t mt = (M + 127) / 128, cus = num_cus_w();
     if (2 * mt * ((N + 255) / 256) > cus) return best;  // whole-K tiles fill half of the CUs
     int64_t best_wg = 0, best_bytes = 0;
@@ -1680,9 +1645,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 // 4096 weight, 4 the faster, so the loads in flight do not set its pace
 // (deeper rings would need the scale loads issued earlier).  The dual form's
 // 40 KiB slots fit 3.
-#ifndef LSMX_SK_SLOTS
-#define LSMX_SK_SLOTS 4
-#endif
 // Wave layouts of the split-K tiles: 128 x 256 single, 1 x 8 waves (each all
 // 128 rows and a 32-column strip, so each weight fragment is dequantized
 // once); 128 x 128 single, 2 x 4 (64 x 32 per wave); dual (256 A rows), 4 x 2
@@ -1691,7 +1653,7 @@ template <int NB, int BN>
 static hipError_t launch_ring_splitk(GemmArgs g, int splits, hipStream_t s) {
     constexpr int BR = 128 * NB;
     constexpr int WGM = NB == 2 ? 4 : (BN == 256 ? 1 : 2);
-    constexpr int SL = NB == 1 ? LSMX_SK_SLOTS : 3;
+    constexpr int SL = NB == 1 ? 4 : 3;
     const int64_t tiles = ((g.M + 127) / 128) * ((g.N + BN - 1) / BN);
     g.splits = splits;
     g.k_split = g.K / splits;
@@ -1720,9 +1682,9 @@ hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
     // the same M picks the same kernel for the single and the dual form
     // GEMV when the dual form's 2M activation rows of K bf16 fit in LDS (the
     // test depends on M and K only, so single and dual launches agree)
-    if (g.M <= LSMX_GEMV_MAX_M && 2 * g.M * g.K * 2 <= kGemvMaxLds) return launch_gemv(g, s);
-    if (g.M <= LSMX_DECODE_MAX_M && decode_ok(g)) return launch_decode(g, s);
-    if (g.M <= LSMX_SKINNY_MAX_M && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
+    if (g.M <= kGemvMaxM && 2 * g.M * g.K * 2 <= kGemvMaxLds) return launch_gemv(g, s);
+    if (g.M <= kDecodeMaxM && decode_ok(g)) return launch_decode(g, s);
+    if (g.M <= kSkinnyMaxM && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
     if (g.ws && ring_ok(g)) {
         const SplitPlan p = splitk_plan(g.M, g.N, g.K);
         if (p.splits > 1) return g.a1 ? launch_ring_splitk<2>(g, p, s) : launch_ring_splitk<1>(g, p, s);
