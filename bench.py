@@ -687,7 +687,61 @@ def bench_reference_rows(torch, dev, n=4096):
     by = 12.0 * n32
     rows.append({"config": "ref-bench fp4 -> e4m3 expansion, 64 Mi words (512 Mi codes)", "ms": ms,
                  "gbs": by / ms / 1e6, "frac_hbm": by / ms / 1e6 / PEAK_HBM_GBS})
+    rows.extend(dual_numerics(torch, dev))
     return rows
+
+
+def dual_numerics(torch, dev, m=256, n=256):
+    """The reference bench's numerics table for the packed dual accumulator
+    (bench.py:120-160): for K in {16, 32, 64, 128, 512}, random q-grid
+    operands (fp4.random_codes -> codes_to_q), zero-padded to a multiple of
+    64 along K, A2 scaled by 2^slot_offset(K); dual_packed accumulates A1.B1
+    + 2^s A2.B2 in one fp32 accumulator and unpack_dual splits it.  Reports
+    the share of outputs where both products come back exact (vs the fp64
+    products), in bf16 and, when the scaled A2 is representable, e4m3.
+
+    Every K here needs more than fp32's 24 mantissa bits (bits = 2 *
+    bitlen(144 K) + 1 >= 25), so whether an output survives depends on the
+    order in which its partial sums are rounded: here the MFMA's order inside
+    each 64-deep K block, in the reference tl.dot's.  The rates are this
+    build's measurement, not a parity claim ("parity unpinned"); the
+    64-block alternation of the two products matches the reference's loop
+    and is tested (tests/test_gpu_scales.py)."""
+    from lockstep_amd import dual_gemm as dg
+    from lockstep_amd import fp4
+    torch.manual_seed(0)
+    out = []
+
+    def exact_rate(dt, q, s, ref1, ref2):
+        a1, b1, b2 = q[0].to(dt), q[2].to(dt), q[3].to(dt)
+        a2s = (q[1] * (2.0 ** s)).to(dt)
+        acc = dg.dual_packed(a1, a2s, b1, b2)
+        g1, g2 = dg.unpack_dual(acc, s)
+        return ((g1.double() == ref1) & (g2.double() == ref2)).float().mean().item()
+
+    for k in (16, 32, 64, 128, 512):
+        s = dg.slot_offset(k)
+        need = 2 * (144 * k).bit_length() + 1
+        kp = max(64, (k + 63) // 64 * 64)
+        q = []
+        for sh, axis in (((m, k), 1), ((m, k), 1), ((k, n), 0), ((k, n), 0)):
+            v = fp4.codes_to_q(fp4.random_codes(sh, dev)).float()
+            if kp != k:
+                pad = torch.zeros((m, kp - k) if axis == 1 else (kp - k, n), device=dev)
+                v = torch.cat([v, pad], dim=axis)
+            q.append(v.contiguous())
+        ref1 = q[0].double() @ q[2].double()
+        ref2 = q[1].double() @ q[3].double()
+        bf = exact_rate(torch.bfloat16, q, s, ref1, ref2)
+        a2s = q[1] * (2.0 ** s)
+        rt = a2s.to(torch.float8_e4m3fn).float()
+        enc = bool(torch.isfinite(rt).all().item() and (rt == a2s).all().item())
+        f8 = exact_rate(torch.float8_e4m3fn, q, s, ref1, ref2) if enc else None
+        out.append({"config": f"ref-bench dual numerics: packed accumulator, K={k}, {m}x{n}",
+                    "k": k, "s": s, "bits_needed": need, "bf16_exact": bf, "fp8_encodable": enc,
+                    "fp8_exact": f8, "parity": "unpinned (bits needed > 24: depends on the accumulation "
+                                               "order inside a 64-deep K block)" if need > 24 else "pinned"})
+    return out
 
 
 if __name__ == "__main__":

@@ -1345,14 +1345,20 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
     const int nblk = (int)(g.K / 32);
     const bool dual = g.a1 != nullptr;
 
-    // stage the activation rows: 16 bytes per thread per step
+    // Stage the activation rows, 16 bytes per thread per step.  Lane l reads
+    // the 64 bytes of block l (+ 64 k) as four 16-byte chunks, so 16 lanes
+    // of one ds_read_b128 start 64 bytes apart; chunk q of block b is stored
+    // at position (q + (b >> 2)) & 3 of the block, which puts those 16 lanes
+    // on 16 distinct 16-byte bank groups (without it, 4-way conflicts).
+    auto apos = [](int64_t b, int q) { return b * 64 + 16 * ((q + (int)(b >> 2)) & 3); };
     {
         const int per_row = (int)(g.K / 8);   // 16-byte chunks per row
         for (int i = t; i < VM * per_row; i += NT) {
             const int m = i / per_row, c = i - m * per_row;
             const bool second = dual && m >= (int)g.M;
             const uint8_t *src = (second ? g.a1 : g.a) + (int64_t)(second ? m - g.M : m) * g.lda * 2 + c * 16;
-            *reinterpret_cast<u32x4 *>(sact + ((int64_t)m * g.K * 2 + c * 16)) = *reinterpret_cast<const u32x4 *>(src);
+            *reinterpret_cast<u32x4 *>(sact + ((int64_t)m * g.K * 2 + apos(c >> 2, c & 3))) =
+                *reinterpret_cast<const u32x4 *>(src);
         }
     }
 
@@ -1400,7 +1406,7 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
             for (int m = 0; m < VM; ++m)
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    av[m][q] = *reinterpret_cast<const u32x4 *>(sact + ((int64_t)m * g.K * 2 + (int64_t)b * 64 + q * 16));
+                    av[m][q] = *reinterpret_cast<const u32x4 *>(sact + ((int64_t)m * g.K * 2 + apos(b, q)));
 #pragma unroll
             for (int r = 0; r < RPW; ++r) {
                 const float sc = e8m0_scale_f32(e[u][r]);
