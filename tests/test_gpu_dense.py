@@ -233,10 +233,13 @@ def test_transpose_exact(dev, mods, elem, rows, cols, pad):
 
 @pytest.mark.parametrize("tin", [False, True])
 @pytest.mark.parametrize("misalign", [0, 1])
-def test_scale_to_e8m0_layouts(dev, mods, oracle, tin, misalign):
+@pytest.mark.parametrize("pad", [3, 4])
+def test_scale_to_e8m0_layouts(dev, mods, oracle, tin, misalign, pad):
     """lsmx_scale_to_e8m0 in all four layouts: powers of two 2^-127 .. 2^127 give the oracle's exponent bytes,
     anything else 0xFF; the K-major output (four blocks per thread, whole-dword stores, byte stores at an odd
-    address) holds the row-major output's bytes regrouped, and no byte outside it is written."""
+    address) holds the row-major output's bytes regrouped, and no byte outside it is written.  pad = 4 gives
+    16-byte aligned fp32 rows, which the row-major-in, K-major-out form converts through an LDS tile (64 rows
+    x 16 groups; 300 rows and 10 groups leave both edges partial)."""
     C = mods[3]
     rng = np.random.default_rng(11)
     orows, blocks = 300, 40
@@ -246,7 +249,7 @@ def test_scale_to_e8m0_layouts(dev, mods, oracle, tin, misalign):
     want = oracle.scale_to_e8m0(s)
     want[bad] = 0xFF
     src = np.ascontiguousarray(s.T) if tin else s      # IN_T: element (block, row)
-    lds = src.shape[1] + 3
+    lds = src.shape[1] + pad
     x = torch.zeros((src.shape[0], lds), dtype=torch.float32)
     x[:, :src.shape[1]] = torch.from_numpy(src)
     x = x.to(dev)
