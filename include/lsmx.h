@@ -148,6 +148,28 @@ int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_
                    int scale_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N,
                    int64_t K, void *stream);
 
+/* lsmx_gemm_f4f4 (K-major E8M0 scales) whose epilogue quantizes its output:
+ * C = A . Bt^T rounded to bf16 is written as both MXFP4 forms that
+ * lsmx_quantize_mxfp4_2d(C, LSMX_SCALE_E8M0_KMAJOR) would write from the
+ * stored bf16 C, bit for bit -- the row form (codes_r [M, ld_codes_r] with
+ * scale_r [N/128][ld_scale_r][4]) and the column form laid out for C^T
+ * (codes_c [N, ld_codes_c], scale_c [M/128][ld_scale_c][4]) -- and, when c
+ * is not NULL, as the bf16 C [M, ldc] itself.  It replaces a GEMM followed by
+ * quantize_mxfp4 (fp4.py:57-72) of its output along both axes: between two
+ * linear layers trained in MXFP4, the hidden activation H and its gradient
+ * dH each feed one GEMM along rows and one along columns (the three GEMMs per
+ * linear of train_step.py:3-6), so the bf16 H and dH need never be stored
+ * or read back.  M, N, K multiples of 256; packed A and
+ * Bt rows 16-byte aligned below 2^24 bytes; K-major input scales; row
+ * codes 4-byte, column codes 8-byte aligned rows; scales 4-byte aligned;
+ * c rows 16-byte aligned. */
+int lsmx_gemm_f4f4_quant(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_t ld_sa,
+                         const uint8_t *bt_pk, int64_t ldb, const void *b_scale, int64_t ld_sb,
+                         void *c, int64_t ldc, uint8_t *codes_r, int64_t ld_codes_r,
+                         uint8_t *scale_r, int64_t ld_scale_r, uint8_t *codes_c,
+                         int64_t ld_codes_c, uint8_t *scale_c, int64_t ld_scale_c, int64_t M,
+                         int64_t N, int64_t K, void *stream);
+
 /* Weight-only GEMM, bf16 activations x MXFP4 weight:
  *   C[M, N] = A[M, K] . deq(W)[N, K]^T, fp32 accumulate.
  * Replaces the forward of fp4_linear.py:34-40 for an unquantized activation

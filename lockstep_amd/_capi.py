@@ -40,6 +40,8 @@ SIGNATURES = {
     "lsmx_dequantize_mxfp4": [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp],
     "lsmx_fp4_to_e4m3": [_vp, _vp, _i64, _vp],
     "lsmx_gemm_f4f4": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
+    "lsmx_gemm_f4f4_quant": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
+                             _vp, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_bf16f4": [_vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_bf16f4_workspace": [_i64, _i64, _i64, _int],
     "lsmx_gemm_bf16f4_ws": [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp,

@@ -301,6 +301,47 @@ int lsmx_gemm_f4f4(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_
     return launched(lsmx::launch_gemm_f4f4(g, (hipStream_t)stream), fn);
 }
 
+int lsmx_gemm_f4f4_quant(const uint8_t *a_pk, int64_t lda, const void *a_scale, int64_t ld_sa, const uint8_t *bt_pk,
+                         int64_t ldb, const void *b_scale, int64_t ld_sb, void *c, int64_t ldc, uint8_t *codes_r,
+                         int64_t ld_codes_r, uint8_t *scale_r, int64_t ld_scale_r, uint8_t *codes_c,
+                         int64_t ld_codes_c, uint8_t *scale_c, int64_t ld_scale_c, int64_t M, int64_t N, int64_t K,
+                         void *stream) {
+    const char *fn = "lsmx_gemm_f4f4_quant";
+    if (!a_pk || !a_scale || !bt_pk || !b_scale || !codes_r || !scale_r || !codes_c || !scale_c)
+        return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (M % 256 || N % 256 || K % 256)
+        return fail(LSMX_ERR_SHAPE, "%s: M, N and K must be multiples of 256 (whole output tiles and stages)", fn);
+    if (M > (int64_t)1 << 30 || N > (int64_t)1 << 30) return fail(LSMX_ERR_SHAPE, "%s: M, N must be < 2^30", fn);
+    if (lda < K / 2 || ldb < K / 2 || (c && ldc < N) || ld_codes_r < N / 2 || ld_codes_c < M / 2 ||
+        ld_scale_r < M || ld_scale_c < N)
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (!aligned(a_pk, 16) || !aligned(bt_pk, 16) || lda % 16 || ldb % 16)
+        return fail(LSMX_ERR_ALIGN, "%s: packed rows must be 16-byte aligned", fn);
+    if (int r = check_scale(fn, a_scale, ld_sa, LSMX_SCALE_E8M0_KMAJOR, 4, M, K)) return r;
+    if (int r = check_scale(fn, b_scale, ld_sb, LSMX_SCALE_E8M0_KMAJOR, 4, N, K)) return r;
+    if (lda >= ((int64_t)1 << 24) || ldb >= ((int64_t)1 << 24))
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
+    if (c && (!aligned(c, 16) || (ldc * 2) % 16)) return fail(LSMX_ERR_ALIGN, "%s: c rows must be 16-byte aligned", fn);
+    if (!aligned(codes_r, 4) || ld_codes_r % 4 || !aligned(codes_c, 8) || ld_codes_c % 8)
+        return fail(LSMX_ERR_ALIGN, "%s: row codes need 4-byte, column codes 8-byte aligned rows", fn);
+    if (!aligned(scale_r, 4) || !aligned(scale_c, 4)) return fail(LSMX_ERR_ALIGN, "%s: scales must be 4-byte aligned", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
+    lsmx::GemmArgs g{a_pk, nullptr, lda, a_scale, ld_sa, bt_pk, ldb, b_scale, ld_sb, LSMX_SCALE_E8M0_KMAJOR, c,
+                     nullptr, LSMX_BF16, ldc, M, N, K};
+    g.codes_r = codes_r;
+    g.ld_cr = ld_codes_r;
+    g.scale_r = scale_r;
+    g.ld_sr = ld_scale_r;
+    g.codes_c = codes_c;
+    g.ld_cc = ld_codes_c;
+    g.scale_c = scale_c;
+    g.ld_sc = ld_scale_c;
+    return launched(lsmx::launch_gemm_f4f4_quant(g, (hipStream_t)stream), fn);
+}
+
 static int rows16(const void *p, int64_t ld, int es) { return aligned(p, 16) && (ld * es) % 16 == 0; }
 
 int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0, const void *bt1, int64_t ldb,

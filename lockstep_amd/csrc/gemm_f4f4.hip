@@ -57,6 +57,7 @@
 // lane order, so the swizzle is applied by choosing each lane's source
 // address.
 #include "lsmx_dma.h"
+#include "lsmx_q16.h"
 #include "lsmx_store.h"
 #include "lsmx_internal.h"
 #include "lsmx_sched.h"
@@ -515,7 +516,154 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 __device__ v4f mfma_scale_f4_16(v4i a, v4i b, v4f c, int cbsz, int blgp, int opsel_a, int scale_a, int opsel_b,
                                 int scale_b) __asm("llvm.amdgcn.mfma.scale.f32.16x16x128.f8f6f4.v4i32.v4i32");
 
-template <int JB, int CT>
+// ---- quantizing epilogue: both MXFP4 forms of a wave's 64 x 128 outputs,
+// rounded to bf16 (cb), with the rule and K-major E8M0 layout of
+// lsmx_quantize_mxfp4_2d applied to the stored bf16 C (the column form is
+// the quantization of C^T along its rows).  cb[i][j][h] holds rows
+// 16 i + 4 grp + 2 h (low half) and + 1 (high half) of column 16 j + r16.
+
+// Column maxima of 32-row blocks: cam[ip][jp] = the 16-bit magnitude maxima
+// of rows 32 ip .. + 32 in column 16 (2 jp) + r16 (low half) and 16 (2 jp +
+// 1) + r16 (high half), the same in all four lane groups.  Returns the
+// largest over the wave's columns.
+LSMX_DEV uint32_t qepi_col_maxima(const uint32_t (&cb)[4][8][2], uint32_t (&cam)[2][4]) {
+    uint32_t top = 0;
+#pragma unroll
+    for (int ip = 0; ip < 2; ++ip)
+#pragma unroll
+        for (int jp = 0; jp < 4; ++jp) {
+            uint32_t h[2];
+#pragma unroll
+            for (int o = 0; o < 2; ++o) {
+                const int j = 2 * jp + o;
+                const uint32_t m = pk_max16(pk_max16(cb[2 * ip][j][0] & 0x7FFF7FFFu, cb[2 * ip][j][1] & 0x7FFF7FFFu),
+                                            pk_max16(cb[2 * ip + 1][j][0] & 0x7FFF7FFFu,
+                                                     cb[2 * ip + 1][j][1] & 0x7FFF7FFFu));
+                h[o] = max(m & 0xFFFFu, m >> 16);
+            }
+            uint32_t x = h[0] | (h[1] << 16);
+            // lanes l and l ^ 32, then l and l ^ 16: each swap returns the two
+            // halves of the pair, so their maximum is the pair's in every lane
+            const auto s32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+            x = pk_max16(s32[0], s32[1]);
+            const auto s16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+            x = pk_max16(s16[0], s16[1]);
+            cam[ip][jp] = x;
+            top = pk_max16(top, x);
+        }
+    return max(top & 0xFFFFu, top >> 16);
+}
+
+// The column codes d0 (rows 0..31) and d1 (rows 32..63) of lane r16 + 16 grp
+// -- the low half of d_ip holds code bytes 16 ip + 2 grp .. + 2 of its
+// column, the high half bytes 16 ip + 8 + 2 grp .. + 2 -- regrouped over the
+// four lane groups so that lane group grp holds bytes 8 grp .. + 8.
+LSMX_DEV u32x2 qepi_col_regroup(uint32_t d0, uint32_t d1, int grp) {
+    // groups g and g + 2 trade: group g now holds the words of ip = g >> 1
+    // from groups g & 1 (x) and (g & 1) + 2 (y)
+    const auto xy = __builtin_amdgcn_permlane32_swap(d0, d1, false, false);
+    const uint32_t x = xy[0], y = xy[1];
+    const bool od = (grp & 1) != 0;
+    // even groups collect the low halves (bytes 16 ip ..), odd groups the
+    // high halves (16 ip + 8 ..); v_perm_b32 selector bytes 0-3 pick bytes
+    // of the second operand, 4-7 of the first
+    const uint32_t lo = __builtin_amdgcn_perm(y, x, 0x05040100u), hi = __builtin_amdgcn_perm(y, x, 0x07060302u);
+    const uint32_t keep = od ? hi : lo, send = od ? lo : hi;
+    const auto sw = __builtin_amdgcn_permlane16_swap(send, send, false, false);
+    const uint32_t recv = od ? sw[0] : sw[1];       // the partner group's send
+    const uint32_t first = od ? recv : keep, second = od ? keep : recv;
+    return u32x2{__builtin_amdgcn_perm(second, first, 0x05040100u), __builtin_amdgcn_perm(second, first, 0x07060302u)};
+}
+
+template <bool ANY>
+LSMX_DEV float qepi_nudge(uint32_t b) {
+    if constexpr (ANY) return nudge_keep_nan(b);
+    else return tie_down16(b);
+}
+template <bool ANY>
+LSMX_DEV uint32_t qepi_e8(uint32_t am16) {
+    if constexpr (ANY) return block_e8m0_16x(am16 << 16);
+    else return block_e8m0_16(am16 << 16);
+}
+template <bool ANY>
+LSMX_DEV uint32_t qepi_codes(const float (&f)[8], uint32_t e8) {
+    if constexpr (ANY) return codes8_any(f, e8);
+    else return cvt_fp4_x8(f, u2f(e8 << 23));
+}
+
+// Both forms of the wave's outputs: rows r0 .. + 64, columns c0 .. + 128 of
+// C.  ANY: the wave's outputs hold an Inf or NaN (the rules of
+// block_e8m0_16x and codes8_any).
+template <bool ANY>
+LSMX_DEV void qepi_store(const uint32_t (&cb)[4][8][2], const uint32_t (&cam)[2][4], const GemmArgs &g, int64_t r0,
+                         int64_t c0, int el) {
+    const int q = el & 3, grp = el >> 4, r16 = el & 15;
+    // ---- column form: codes_c [N][M / 2], scale_c [M / 128][N][4]
+    uint32_t sp[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t d[2];
+#pragma unroll
+        for (int ip = 0; ip < 2; ++ip) {
+            const uint32_t e8 = qepi_e8<ANY>((cam[ip][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t w = cb[2 * ip + k][j][h];
+                    f[4 * k + 2 * h] = qepi_nudge<ANY>(w << 16);
+                    f[4 * k + 2 * h + 1] = qepi_nudge<ANY>(w & 0xFFFF0000u);
+                }
+            d[ip] = qepi_codes<ANY>(f, e8);
+            sp[j] = ip == 0 ? e8 : sp[j] | (e8 << 8);
+        }
+        const u32x2 v = qepi_col_regroup(d[0], d[1], grp);
+        *reinterpret_cast<u32x2 *>(g.codes_c + (c0 + 16 * j + r16) * g.ld_cc + r0 / 2 + 8 * grp) = v;
+    }
+    // the two scale bytes of column 16 j + r16 from lane group j & 3
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const uint32_t v = grp == 0 ? sp[4 * jj] : grp == 1 ? sp[4 * jj + 1] : grp == 2 ? sp[4 * jj + 2] : sp[4 * jj + 3];
+        const int64_t col = c0 + 16 * (4 * jj + grp) + r16;
+        *reinterpret_cast<uint16_t *>(g.scale_c + ((r0 >> 7) * g.ld_sc + col) * 4 + 2 * ((r0 >> 6) & 1)) = (uint16_t)v;
+    }
+    // ---- row form: codes_r [M][N / 2], scale_r [N / 128][M][4]; lanes hold
+    // 8 consecutive columns of one row after the in-quad transpose
+    const bool odd = (el & 4) != 0;
+    const int cl = 16 * (odd ? 1 : 0) + 8 * ((el >> 3) & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t row = r0 + 16 * i + 4 * grp + q;
+        uint32_t rs = 0;
+#pragma unroll
+        for (int jp = 0; jp < 4; ++jp) {
+            const u32x4 p = pack16_rows8_of(quad_pack16_bits(cb[i][2 * jp][0], cb[i][2 * jp][1], q),
+                                            quad_pack16_bits(cb[i][2 * jp + 1][0], cb[i][2 * jp + 1][1], q), odd);
+            const int64_t col = c0 + 32 * jp + cl;
+            if (g.c) *reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(g.c) + row * g.ldc + col) = p;
+            const uint32_t m = pk_max16(pk_max16(p[0] & 0x7FFF7FFFu, p[1] & 0x7FFF7FFFu),
+                                        pk_max16(p[2] & 0x7FFF7FFFu, p[3] & 0x7FFF7FFFu));
+            // the block's 32 columns lie in lanes l, l ^ 4, l ^ 8, l ^ 12:
+            // rotations by 4 and 8 within the 16-lane row reach all four
+            uint32_t am = max(m & 0xFFFFu, m >> 16);
+            am = max(am, (uint32_t)__builtin_amdgcn_mov_dpp((int)am, 0x124, 0xF, 0xF, false));
+            am = max(am, (uint32_t)__builtin_amdgcn_mov_dpp((int)am, 0x128, 0xF, 0xF, false));
+            const uint32_t e8 = qepi_e8<ANY>(am);
+            float f[8];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                f[2 * h] = qepi_nudge<ANY>(p[h] << 16);
+                f[2 * h + 1] = qepi_nudge<ANY>(p[h] & 0xFFFF0000u);
+            }
+            *reinterpret_cast<uint32_t *>(g.codes_r + row * g.ld_cr + col / 2) = qepi_codes<ANY>(f, e8);
+            rs |= e8 << (8 * jp);
+        }
+        if ((el & 12) == 0) *reinterpret_cast<uint32_t *>(g.scale_r + ((c0 >> 7) * g.ld_sr + row) * 4) = rs;
+    }
+}
+
+template <int JB, int CT, bool EPI = false>
 __global__ __launch_bounds__(512, 1) void gemm_f4f4_mx16_kernel(GemmArgs g) {
     using namespace f4;
     constexpr int S = 2;                             // ring slots
@@ -794,7 +942,22 @@ __global__ __launch_bounds__(512, 1) void gemm_f4f4_mx16_kernel(GemmArgs g) {
         int el = lane;
         asm volatile("" : "+v"(el));
         const int q = el & 3, egrp = el >> 4, er16 = el & 15;
-        if (vec_c && m0 + BM <= g.M && n0 + BN <= g.N) {
+        if constexpr (EPI) {
+            // whole tiles only (the launcher checks); round to bf16 first
+            uint32_t cb[TM][TN][2];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    cb[i][j][0] = bf16x2(acc[i][j][0], acc[i][j][1]);
+                    cb[i][j][1] = bf16x2(acc[i][j][2], acc[i][j][3]);
+                }
+            uint32_t cam[2][4];
+            const uint32_t top = qepi_col_maxima(cb, cam);
+            const int64_t r0 = m0 + wm * 64, c0 = n0 + wn * 128;
+            if (__builtin_expect(__any(top >= 0x7F80u), 0)) qepi_store<true>(cb, cam, g, r0, c0, el);
+            else qepi_store<false>(cb, cam, g, r0, c0, el);
+        } else if (vec_c && m0 + BM <= g.M && n0 + BN <= g.N) {
             constexpr int EB = CT == LSMX_F32 ? 4 : 2;
             const uint8_t *cw = reinterpret_cast<const uint8_t *>(g.c) + ((m0 + wm * 64) * g.ldc + n0 + wn * 128) * EB;
             if constexpr (CT == LSMX_F32) {
@@ -884,6 +1047,13 @@ hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s) {
     else if (g.scale_fmt == LSMX_SCALE_E8M0_KMAJOR) LSMX_GC(gemm_f4f4_kernel, LSMX_SCALE_E8M0_KMAJOR, 4);
     else LSMX_GC(gemm_f4f4_kernel, LSMX_SCALE_E8M0, 4);
 #undef LSMX_GC
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_f4f4_quant(const GemmArgs &g, hipStream_t s) {
+    const int tiles = (int)((g.M / f4::BM) * (g.N / f4::BN));
+    const int grid = tiles < num_cus() ? tiles : num_cus();
+    hipLaunchKernelGGL((gemm_f4f4_mx16_kernel<4, LSMX_BF16, true>), grid, 512, 0, s, g);
     return hipGetLastError();
 }
 

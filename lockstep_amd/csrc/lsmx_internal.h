@@ -87,6 +87,17 @@ struct GemmArgs {
     float *ws = nullptr;
     // decode-shape weight-only kernel: weight rows per workgroup
     int rows_wg = 0;
+    // f4 x f4 GEMM with a quantizing epilogue: both MXFP4 forms of the
+    // bf16-rounded C with K-major E8M0 scales, as lsmx_quantize_mxfp4_2d
+    // writes them (c optional)
+    uint8_t *codes_r = nullptr;
+    int64_t ld_cr = 0;
+    uint8_t *scale_r = nullptr;
+    int64_t ld_sr = 0;
+    uint8_t *codes_c = nullptr;
+    int64_t ld_cc = 0;
+    uint8_t *scale_c = nullptr;
+    int64_t ld_sc = 0;
 };
 
 struct DenseArgs {
@@ -111,6 +122,7 @@ hipError_t launch_unpack(const uint8_t *packed, uint8_t *codes, int64_t n_bytes,
 hipError_t launch_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n, hipStream_t s);
 hipError_t launch_dequant(const DequantArgs &a, hipStream_t s);
 hipError_t launch_gemm_f4f4(const GemmArgs &g, hipStream_t s);
+hipError_t launch_gemm_f4f4_quant(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s);
 hipError_t launch_gemm_xf4(const GemmArgs &g, int a_dtype, hipStream_t s);
 // split count the weight-only GEMM uses at this shape when given a workspace

@@ -85,11 +85,9 @@ LSMX_DEV uint32_t quad_xor_u(uint32_t v) {
 //   2. halves: lane q keeps row q of both columns and takes row q of columns
 //      q ^ 1 and q ^ 3 from lane q ^ 1;
 //   3. bytes: put the four columns of row q in order.
-template <int CT>
-LSMX_DEV u32x2 quad_pack16(const float (&x)[4], int q) {
-    static_assert(CT == LSMX_BF16 || CT == LSMX_F16, "16-bit outputs");
-    const uint32_t p0 = CT == LSMX_BF16 ? bf16x2(x[0], x[1]) : f16_bits(x[0]) | (f16_bits(x[1]) << 16);
-    const uint32_t p1 = CT == LSMX_BF16 ? bf16x2(x[2], x[3]) : f16_bits(x[2]) | (f16_bits(x[3]) << 16);
+// The transpose of quad_pack16 on values already rounded and packed: p0 =
+// rows 0 and 1, p1 = rows 2 and 3 of lane q's column.
+LSMX_DEV u32x2 quad_pack16_bits(uint32_t p0, uint32_t p1, int q) {
     const bool qh = (q & 2) != 0, ql = (q & 1) != 0;
     const uint32_t t0 = qh ? p1 : p0;
     const uint32_t t1 = quad_xor_u<2>(qh ? p0 : p1);
@@ -99,6 +97,13 @@ LSMX_DEV u32x2 quad_pack16(const float (&x)[4], int q) {
     // keep = (col q, col q^2), recv = (col q^1, col q^3) of row q
     const uint32_t lo = ql ? 0x01000504u : 0x05040100u, hi = lo + 0x02020202u;
     return u32x2{__builtin_amdgcn_perm(recv, keep, qh ? hi : lo), __builtin_amdgcn_perm(recv, keep, qh ? lo : hi)};
+}
+template <int CT>
+LSMX_DEV u32x2 quad_pack16(const float (&x)[4], int q) {
+    static_assert(CT == LSMX_BF16 || CT == LSMX_F16, "16-bit outputs");
+    const uint32_t p0 = CT == LSMX_BF16 ? bf16x2(x[0], x[1]) : f16_bits(x[0]) | (f16_bits(x[1]) << 16);
+    const uint32_t p1 = CT == LSMX_BF16 ? bf16x2(x[2], x[3]) : f16_bits(x[2]) | (f16_bits(x[3]) << 16);
+    return quad_pack16_bits(p0, p1, q);
 }
 
 // Eight consecutive 16-bit columns of one row per lane, from two row groups
@@ -111,9 +116,8 @@ LSMX_DEV u32x2 quad_pack16(const float (&x)[4], int q) {
 // != 0).  One 16-byte store per lane then writes 64 contiguous bytes per
 // row and 16 rows per instruction, half the instructions of 8-byte stores
 // (the output burst at the end of a GEMM tile drains measurably faster).
-template <int CT>
-LSMX_DEV u32x4 pack16_rows8(const float (&x0)[4], const float (&x1)[4], int q, bool odd) {
-    const u32x2 a0 = quad_pack16<CT>(x0, q), a1 = quad_pack16<CT>(x1, q);
+// pack16_rows8_of takes the two quad_pack16 results.
+LSMX_DEV u32x4 pack16_rows8_of(const u32x2 a0, const u32x2 a1, bool odd) {
     const uint32_t s0 = odd ? a0[0] : a1[0], s1 = odd ? a0[1] : a1[1];
     // DPP row_shl:4 reads lane + 4, row_shr:4 lane - 4 (within 16 lanes);
     // each lane uses the one that stays inside its 8-lane group
@@ -122,6 +126,10 @@ LSMX_DEV u32x4 pack16_rows8(const float (&x0)[4], const float (&x1)[4], int q, b
     const uint32_t r0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s0, 0x114, 0xF, 0xF, true);
     const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s1, 0x114, 0xF, 0xF, true);
     return odd ? u32x4{r0, r1, a1[0], a1[1]} : u32x4{a0[0], a0[1], l0, l1};
+}
+template <int CT>
+LSMX_DEV u32x4 pack16_rows8(const float (&x0)[4], const float (&x1)[4], int q, bool odd) {
+    return pack16_rows8_of(quad_pack16<CT>(x0, q), quad_pack16<CT>(x1, q), odd);
 }
 
 // quad_pack16's row stored at idx: lane q writes M[q][0..3].

@@ -96,6 +96,47 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
     return c
 
 
+def mxfp4_gemm_packed_q2d(a_pk, bt_pk, a_scale, b_scale, keep_output: bool = False):
+    """C = mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale) in bf16, returned
+    quantized along both axes:
+
+        (row_packed, row_scale, col_packed, col_scale) ==
+            fp4.quantize_pack_mxfp4_2d(C, scale_layout="kmajor")
+
+    bit for bit, with C itself appended when keep_output.  Scales in and out
+    are K-major E8M0 [K//128, rows, 4] (quantize_pack_mxfp4(...,
+    scale_layout="kmajor")).  With M, N and K multiples of 256 the GEMM's
+    epilogue quantizes its tile in registers (lsmx_gemm_f4f4_quant), so the
+    bf16 C is written only when asked for and never read back; other shapes
+    run the GEMM and then the two-axis quantizer."""
+    M, Kh = a_pk.shape
+    N, Kh2 = bt_pk.shape
+    K = Kh * 2
+    assert Kh == Kh2 and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
+    assert a_scale.dtype == torch.uint8 and a_scale.shape == (K // 128, M, 4) and b_scale.shape == (K // 128, N, 4), \
+        "mxfp4_gemm_packed_q2d takes K-major E8M0 scales [K//128, rows, 4]"
+    if M % 256 or N % 256 or K % 256:
+        c = mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16)
+        from .fp4 import quantize_pack_mxfp4_2d
+        r = quantize_pack_mxfp4_2d(c, scale_layout="kmajor")
+        return (*r, c) if keep_output else r
+    C.require_device(a_pk, bt_pk, a_scale, b_scale)
+    a_pk, bt_pk = _rows16(a_pk), _rows16(bt_pk)
+    a_scale, b_scale = a_scale.contiguous(), b_scale.contiguous()
+    dev = a_pk.device
+    rp = torch.empty((M, N // 2), dtype=torch.uint8, device=dev)
+    rs = torch.empty((N // 128, M, 4), dtype=torch.uint8, device=dev)
+    cp = torch.empty((N, M // 2), dtype=torch.uint8, device=dev)
+    cs = torch.empty((M // 128, N, 4), dtype=torch.uint8, device=dev)
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=dev) if keep_output else None
+    if M and N:
+        C.call("lsmx_gemm_f4f4_quant", a_pk.data_ptr(), a_pk.stride(0) if M > 1 else Kh, a_scale.data_ptr(), M,
+               bt_pk.data_ptr(), bt_pk.stride(0) if N > 1 else Kh, b_scale.data_ptr(), N,
+               c.data_ptr() if c is not None else None, N, rp.data_ptr(), N // 2, rs.data_ptr(), M,
+               cp.data_ptr(), M // 2, cs.data_ptr(), N, M, N, K, C.stream_of(rp))
+    return (rp, rs, cp, cs, c) if keep_output else (rp, rs, cp, cs)
+
+
 _ACT = {torch.bfloat16: C.BF16, torch.float32: C.F32, torch.float16: C.F16}
 
 

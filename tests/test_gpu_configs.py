@@ -195,3 +195,29 @@ def test_cfg5_mlp_block_gemms(dev, oracle, cfg5_run, which):
     rows = np.sort(rng.choice(M, 64, replace=False))
     cols = np.sort(rng.choice(N, 96, replace=False))
     assert _check(oracle, got, aq(), bq(), rows, cols) <= 1e-2
+
+
+def test_cfg5_fused_h_and_dh_quantization(dev, oracle, mods, cfg5_run):
+    """h and dh are only ever quantized, so the fc forward and the out dgrad
+    GEMMs quantize them in their epilogue (mxfp4_gemm_packed_q2d): the four
+    MXFP4 arrays of each equal the two-axis quantizer applied to the bf16 h
+    and dh this chain computed, and sampled rows and columns of them equal
+    the oracle's quantizer (fp4.py:57-72) of those bf16 values."""
+    from lockstep_amd import fp4, mxfp4_gemm as mg
+    r = cfg5_run
+    q = {k: fp4.quantize_pack_mxfp4_2d(r[k], scale_layout="kmajor") for k in ("x", "w1", "w2", "dy")}
+    fused = {"h": mg.mxfp4_gemm_packed_q2d(q["x"][0], q["w1"][0], q["x"][1], q["w1"][1]),
+             "dh": mg.mxfp4_gemm_packed_q2d(q["dy"][0], q["w2"][2], q["dy"][1], q["w2"][3])}
+    rng = np.random.default_rng(55)
+    for name, got in fused.items():
+        want = fp4.quantize_pack_mxfp4_2d(r[name], scale_layout="kmajor")
+        for g_, w_ in zip(got, want):
+            assert torch.equal(g_, w_), name
+        rows = np.sort(rng.choice(T5, 24, replace=False))
+        cols = np.sort(rng.choice(F5, 24, replace=False))
+        rq, rsc = _q_rows(oracle, r[name][torch.from_numpy(rows).to(dev)])
+        assert np.array_equal(got[0].cpu().numpy()[rows], rq)
+        assert np.array_equal(got[1].cpu().numpy()[:, rows, :].transpose(1, 0, 2).reshape(len(rows), -1), rsc)
+        cq, csc = _q_cols(oracle, r[name][:, torch.from_numpy(cols).to(dev)])
+        assert np.array_equal(got[2].cpu().numpy()[cols], cq)
+        assert np.array_equal(got[3].cpu().numpy()[:, cols, :].transpose(1, 0, 2).reshape(len(cols), -1), csc)
