@@ -1316,7 +1316,7 @@ static bool decode_ok(const GemmArgs &g) {
 // W once, and the matrix cores have almost nothing to do.  This kernel reads
 // W with fully contiguous loads and does the arithmetic on the VALU:
 //   - the activation rows are staged once per workgroup in LDS;
-//   - a wave owns GV_RPW weight rows; lane l takes the MX blocks l, l + 64,
+//   - a wave owns RPW weight rows; lane l takes the MX blocks l, l + 64,
 //     l + 128, ... of every row, so each load instruction reads 1 KiB of one
 //     row in one piece, and all of a wave's weight loads are issued before
 //     any arithmetic;
@@ -1327,10 +1327,13 @@ static bool decode_ok(const GemmArgs &g) {
 //     fixed butterfly, so the order depends on K only.
 // VM is the number of virtual activation rows (M, or 2M in dual mode).
 namespace gv {
-constexpr int NT = 512;   // 8 waves
-// weight rows per wave: 2 rows (896 workgroups at N = 14336) stream a
-// 14336 x 4096 weight in 8.6 us against 9.6 us with 4 rows (448, which
-// leaves some CUs one workgroup and others two); 1 row takes 9.1-10.4 us
+// 4 waves of 2 weight rows each (1792 workgroups at N = 14336): a 14336 x
+// 4096 weight streams in 8.4 us against 8.9 us for 8-wave workgroups (896),
+// 9.5 us for 2-wave ones and 9.5-9.8 us with 1 or 4 rows per wave.  Of the
+// 8.4 us, the dequantize-and-dot arithmetic adds ~1.2 us and the activation
+// staging ~0.5 us to the 6.8 us of the loads alone (a plain 31 MB read runs
+// in 6.0 us)
+constexpr int NT = 256;
 constexpr int RPW = 2;
 constexpr int UB = 2;     // groups of 64 blocks per lane in flight
 }  // namespace gv
@@ -1351,8 +1354,29 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
     // at position (q + (b >> 2)) & 3 of the block, which puts those 16 lanes
     // on 16 distinct 16-byte bank groups (without it, 4-way conflicts).
     auto apos = [](int64_t b, int q) { return b * 64 + 16 * ((q + (int)(b >> 2)) & 3); };
-    {
-        const int per_row = (int)(g.K / 8);   // 16-byte chunks per row
+    const int per_row = (int)(g.K / 8);   // 16-byte chunks per row
+    // K % 512 == 0 (whole 64-chunk DMA instructions per row): the rows are
+    // staged by direct-to-LDS loads issued before the weight loads.  A
+    // staging load through registers would have to land before its LDS
+    // store, and with vmcnt counting in issue order the weight stream could
+    // only start after it; a DMA needs no register, so the weight loads go
+    // out behind it at once and the wave waits for the DMA alone (all but
+    // the newest 4 vector-memory operations: the first block group's weight
+    // and scale loads, always issued) before the barrier.  Lane l of a DMA
+    // writes chunk position p = its base + l; the swizzle is applied by
+    // loading into position p the chunk that apos puts there.
+    const bool dma_act = per_row % 64 == 0;
+    if (dma_act) {
+        for (int base = 64 * wave; base < VM * per_row; base += NT) {
+            const int m = base / per_row;
+            const bool second = dual && m >= (int)g.M;
+            const uint8_t *row = (second ? g.a1 : g.a) + (int64_t)(second ? m - g.M : m) * g.lda * 2;
+            const int p = base - m * per_row + lane, bk = p >> 2, slot = p & 3;
+            const uint32_t voff = (uint32_t)((4 * bk + ((slot - (bk >> 2)) & 3)) * 16);
+            dma_x4(voff, buf_rsrc(row, (uint64_t)g.K * 2),
+                   lds_u32(sact) + (uint32_t)((int64_t)m * g.K * 2 + (int64_t)(base - m * per_row) * 16));
+        }
+    } else {
         for (int i = t; i < VM * per_row; i += NT) {
             const int m = i / per_row, c = i - m * per_row;
             const bool second = dual && m >= (int)g.M;
@@ -1395,6 +1419,7 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
         }
     };
     wload(lane);       // the first weight loads are in flight across the barrier
+    if (dma_act) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     __syncthreads();
     for (int b0 = lane; b0 < nblk;) {
 #pragma unroll
