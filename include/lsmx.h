@@ -105,6 +105,30 @@ int lsmx_quantize_mxfp4_2d(const void *x, int x_dtype, int64_t rows, int64_t col
                            int64_t ld_codes_r, uint8_t *scale_r, int64_t ld_scale_r, uint8_t *codes_c,
                            int64_t ld_codes_c, uint8_t *scale_c, int64_t ld_scale_c, int scale_fmt, void *stream);
 
+/* One tensor of lsmx_quantize_mxfp4_2d_batch: the arguments of
+ * lsmx_quantize_mxfp4_2d for it. */
+typedef struct {
+    const void *x;
+    int64_t rows, cols, ldx;
+    uint8_t *codes_r;
+    int64_t ld_codes_r;
+    uint8_t *scale_r;
+    int64_t ld_scale_r;
+    uint8_t *codes_c;
+    int64_t ld_codes_c;
+    uint8_t *scale_c;
+    int64_t ld_scale_c;
+} lsmx_q2d_item;
+
+/* lsmx_quantize_mxfp4_2d of n <= 8 tensors of one dtype and scale format in
+ * one launch, with the same outputs bit for bit.  The tensors a training
+ * step quantizes at its start (the activation and the weights of each
+ * linear, train_step.py:3-6) are a few MB each; one launch keeps the memory
+ * system streaming across them instead of ramping up and draining per
+ * tensor.  items is host memory, read before the call returns. */
+int lsmx_quantize_mxfp4_2d_batch(const lsmx_q2d_item *items, int n, int x_dtype, int scale_fmt,
+                                 void *stream);
+
 /* fp4.py:43-54 _round_to_e2m1: codes[i] = E2M1 code of q[i] (scale 1):
  * nearest, ties toward the smaller magnitude, clip at 6, sign copied, NaN -> 7.
  * q_dtype LSMX_F32 | LSMX_BF16 | LSMX_F16; n elements, one code byte each. */

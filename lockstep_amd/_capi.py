@@ -34,6 +34,7 @@ SIGNATURES = {
     "lsmx_quantize_mxfp4": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
     "lsmx_quantize_mxfp4_t": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
     "lsmx_quantize_mxfp4_2d": [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp],
+    "lsmx_quantize_mxfp4_2d_batch": [_vp, _int, _int, _int, _vp],
     "lsmx_round_e2m1": [_vp, _int, _i64, _vp, _vp],
     "lsmx_pack_fp4": [_vp, _vp, _i64, _vp],
     "lsmx_unpack_fp4": [_vp, _vp, _i64, _vp],
@@ -58,6 +59,13 @@ SIGNATURES = {
 }
 
 RET_I64 = ("lsmx_gemm_bf16f4_workspace",)
+
+
+class Q2dItem(ctypes.Structure):
+    """lsmx_q2d_item of include/lsmx.h."""
+    _fields_ = [("x", _vp), ("rows", _i64), ("cols", _i64), ("ldx", _i64),
+                ("codes_r", _vp), ("ld_codes_r", _i64), ("scale_r", _vp), ("ld_scale_r", _i64),
+                ("codes_c", _vp), ("ld_codes_c", _i64), ("scale_c", _vp), ("ld_scale_c", _i64)]
 
 _lib = None
 _lock = threading.Lock()

@@ -167,10 +167,11 @@ int lsmx_quantize_mxfp4_t(const void *x, int x_dtype, int64_t K, int64_t cols, i
                            ld_scale, stream, true);
 }
 
-int lsmx_quantize_mxfp4_2d(const void *x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, uint8_t *codes_r,
-                           int64_t ld_codes_r, uint8_t *scale_r, int64_t ld_scale_r, uint8_t *codes_c,
-                           int64_t ld_codes_c, uint8_t *scale_c, int64_t ld_scale_c, int scale_fmt, void *stream) {
-    const char *fn = "lsmx_quantize_mxfp4_2d";
+// The argument checks of one tensor of lsmx_quantize_mxfp4_2d(_batch).
+static int check_q2d(const char *fn, const void *x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
+                     const uint8_t *codes_r, int64_t ld_codes_r, const uint8_t *scale_r, int64_t ld_scale_r,
+                     const uint8_t *codes_c, int64_t ld_codes_c, const uint8_t *scale_c, int64_t ld_scale_c,
+                     int scale_fmt) {
     if (!x || !codes_r || !scale_r || !codes_c || !scale_c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
     if (x_dtype != LSMX_BF16 && x_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: x_dtype must be bf16 or fp16", fn);
     if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_E8M0_KMAJOR)
@@ -187,11 +188,46 @@ int lsmx_quantize_mxfp4_2d(const void *x, int x_dtype, int64_t rows, int64_t col
     if (!aligned(scale_r, 4) || !aligned(scale_c, 4) || (!km && (ld_scale_r % 4 || ld_scale_c % 4)))
         return fail(LSMX_ERR_ALIGN, "%s: scales must be 4-byte aligned", fn);
     if ((rows / 128) * (cols / 128) > 0x7FFFFFFF) return fail(LSMX_ERR_SHAPE, "%s: too many tiles", fn);
+    return LSMX_OK;
+}
+
+int lsmx_quantize_mxfp4_2d(const void *x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, uint8_t *codes_r,
+                           int64_t ld_codes_r, uint8_t *scale_r, int64_t ld_scale_r, uint8_t *codes_c,
+                           int64_t ld_codes_c, uint8_t *scale_c, int64_t ld_scale_c, int scale_fmt, void *stream) {
+    const char *fn = "lsmx_quantize_mxfp4_2d";
+    if (int r = check_q2d(fn, x, x_dtype, rows, cols, ldx, codes_r, ld_codes_r, scale_r, ld_scale_r, codes_c,
+                          ld_codes_c, scale_c, ld_scale_c, scale_fmt))
+        return r;
     if (int r = device_guard()) return r;
     if (rows == 0 || cols == 0) return LSMX_OK;
     lsmx::Quant2dArgs a{x, x_dtype, rows, cols, ldx, codes_r, ld_codes_r, scale_r, ld_scale_r,
                         codes_c, ld_codes_c, scale_c, ld_scale_c, scale_fmt};
     return launched(lsmx::launch_quantize_2d(a, (hipStream_t)stream), fn);
+}
+
+int lsmx_quantize_mxfp4_2d_batch(const lsmx_q2d_item *items, int n, int x_dtype, int scale_fmt, void *stream) {
+    const char *fn = "lsmx_quantize_mxfp4_2d_batch";
+    if (!items) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (n < 0 || n > lsmx::kQ2Batch) return fail(LSMX_ERR_SHAPE, "%s: n must be 0 .. %d", fn, lsmx::kQ2Batch);
+    lsmx::Quant2dBatch b{};
+    int64_t tiles = 0;
+    for (int k = 0; k < n; ++k) {
+        const lsmx_q2d_item &it = items[k];
+        if (int r = check_q2d(fn, it.x, x_dtype, it.rows, it.cols, it.ldx, it.codes_r, it.ld_codes_r, it.scale_r,
+                              it.ld_scale_r, it.codes_c, it.ld_codes_c, it.scale_c, it.ld_scale_c, scale_fmt))
+            return r;
+        const int64_t t = (it.rows / 128) * (it.cols / 128);
+        if (t == 0) continue;                      // empty tensors take no workgroup
+        if (tiles + t > 0x7FFFFFFF) return fail(LSMX_ERR_SHAPE, "%s: too many tiles", fn);
+        b.a[b.n] = lsmx::Quant2dArgs{it.x, x_dtype, it.rows, it.cols, it.ldx, it.codes_r, it.ld_codes_r,
+                                     it.scale_r, it.ld_scale_r, it.codes_c, it.ld_codes_c, it.scale_c,
+                                     it.ld_scale_c, scale_fmt};
+        tiles += t;
+        b.end[b.n++] = tiles;
+    }
+    if (int r = device_guard()) return r;
+    if (b.n == 0) return LSMX_OK;
+    return launched(lsmx::launch_quantize_2d_batch(b, (hipStream_t)stream), fn);
 }
 
 int lsmx_round_e2m1(const void *q, int q_dtype, int64_t n, uint8_t *codes, void *stream) {

@@ -50,6 +50,15 @@ struct Quant2dArgs {
     int scale_fmt;
 };
 
+// Up to kQ2Batch tensors of one dtype and scale format quantized by one
+// launch; end[k] = tiles of tensors 0 .. k.
+constexpr int kQ2Batch = 8;
+struct Quant2dBatch {
+    Quant2dArgs a[kQ2Batch];
+    int64_t end[kQ2Batch];
+    int n;
+};
+
 struct DequantArgs {
     const void *codes;
     int codes_fmt;
@@ -116,6 +125,7 @@ struct DenseArgs {
 
 hipError_t launch_quantize(const QuantArgs &a, bool cols, hipStream_t s);
 hipError_t launch_quantize_2d(const Quant2dArgs &a, hipStream_t s);
+hipError_t launch_quantize_2d_batch(const Quant2dBatch &b, hipStream_t s);
 hipError_t launch_round(const void *q, int q_dtype, int64_t n, uint8_t *codes, hipStream_t s);
 hipError_t launch_pack(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, hipStream_t s);
 hipError_t launch_unpack(const uint8_t *packed, uint8_t *codes, int64_t n_bytes, hipStream_t s);

@@ -466,19 +466,20 @@ LSMX_DEV uint32_t q2_maxima(const u32x4 (&raw)[8], uint32_t (&am)[8], uint32_t (
     return top;
 }
 
-// ROWS = false: the column form only (lsmx_quantize_mxfp4_t of a 16-bit x).
-template <typename T, int SFMT, bool ROWS = true>
-__global__ __launch_bounds__(q2::NT, 5) void quantize_2d_kernel(
-    const T *__restrict__ x, int64_t R, int64_t C, int64_t ldx, uint8_t *__restrict__ codes_r, int64_t ld_cr,
-    uint8_t *__restrict__ scale_r, int64_t ld_sr, uint8_t *__restrict__ codes_c, int64_t ld_cc,
-    uint8_t *__restrict__ scale_c, int64_t ld_sc) {
+// One 128 x 128 tile of x (tile index `tile`, row-major over the tiles),
+// by one workgroup of q2::NT threads.  ROWS = false: the column form only
+// (lsmx_quantize_mxfp4_t of a 16-bit x).
+template <typename T, int SFMT, bool ROWS>
+LSMX_DEV void q2_tile(const T *__restrict__ x, int64_t R, int64_t C, int64_t ldx, uint8_t *__restrict__ codes_r,
+                      int64_t ld_cr, uint8_t *__restrict__ scale_r, int64_t ld_sr, uint8_t *__restrict__ codes_c,
+                      int64_t ld_cc, uint8_t *__restrict__ scale_c, int64_t ld_sc, int64_t tile) {
     static_assert(sizeof(T) == 2, "16-bit inputs");
     // [column][dword]: dword 4w + g holds the codes of tile rows 32w + 8g .. +8
     __shared__ __attribute__((aligned(16))) uint32_t ccode[q2::T][17];
     __shared__ uint32_t cscale[q2::T];
 
-    const int tiles_c = (int)(C / q2::T);
-    const int64_t r0 = (int64_t)(blockIdx.x / tiles_c) * q2::T, c0 = (int64_t)(blockIdx.x % tiles_c) * q2::T;
+    const int64_t tiles_c = C / q2::T;
+    const int64_t r0 = (tile / tiles_c) * q2::T, c0 = (tile % tiles_c) * q2::T;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int v = lane & 15, g = lane >> 4;
     const int rl = 32 * w + 8 * g;                       // first tile row of this lane
@@ -527,6 +528,39 @@ __global__ __launch_bounds__(q2::NT, 5) void quantize_2d_kernel(
                 *reinterpret_cast<uint32_t *>(scale_c + (c0 + t) * ld_sc + r0 / 32) = e4;
         }
     }
+}
+
+template <typename T, int SFMT, bool ROWS = true>
+__global__ __launch_bounds__(q2::NT, 5) void quantize_2d_kernel(
+    const T *__restrict__ x, int64_t R, int64_t C, int64_t ldx, uint8_t *__restrict__ codes_r, int64_t ld_cr,
+    uint8_t *__restrict__ scale_r, int64_t ld_sr, uint8_t *__restrict__ codes_c, int64_t ld_cc,
+    uint8_t *__restrict__ scale_c, int64_t ld_sc) {
+    q2_tile<T, SFMT, ROWS>(x, R, C, ldx, codes_r, ld_cr, scale_r, ld_sr, codes_c, ld_cc, scale_c, ld_sc,
+                           (int64_t)blockIdx.x);
+}
+
+// Several tensors in one launch: workgroup b takes tile b - end[k - 1] of
+// tensor k, the first k with b < end[k] (end: running tile counts).  One
+// launch keeps the memory system busy across the tensors' boundaries, where
+// separate launches of a few-MB tensor each pay a ramp-up and a drain.
+template <typename T, int SFMT>
+__global__ __launch_bounds__(q2::NT, 5) void quantize_2d_batch_kernel(Quant2dBatch b) {
+    const int64_t blk = (int64_t)blockIdx.x;
+    int k = 0;
+    while (k + 1 < b.n && blk >= b.end[k]) ++k;
+    const Quant2dArgs &a = b.a[k];
+    q2_tile<T, SFMT, true>(reinterpret_cast<const T *>(a.x), a.R, a.C, a.ldx, a.codes_r, a.ld_cr, a.scale_r, a.ld_sr,
+                           a.codes_c, a.ld_cc, a.scale_c, a.ld_sc, blk - (k ? b.end[k - 1] : 0));
+}
+
+hipError_t launch_quantize_2d_batch(const Quant2dBatch &b, hipStream_t s) {
+    const dim3 grid((unsigned)b.end[b.n - 1]), blk(q2::NT);
+    const bool bf = b.a[0].x_dtype == LSMX_BF16, km = b.a[0].scale_fmt == LSMX_SCALE_E8M0_KMAJOR;
+    if (bf && km) hipLaunchKernelGGL((quantize_2d_batch_kernel<bf16_t, LSMX_SCALE_E8M0_KMAJOR>), grid, blk, 0, s, b);
+    else if (bf) hipLaunchKernelGGL((quantize_2d_batch_kernel<bf16_t, LSMX_SCALE_E8M0>), grid, blk, 0, s, b);
+    else if (km) hipLaunchKernelGGL((quantize_2d_batch_kernel<f16_t, LSMX_SCALE_E8M0_KMAJOR>), grid, blk, 0, s, b);
+    else hipLaunchKernelGGL((quantize_2d_batch_kernel<f16_t, LSMX_SCALE_E8M0>), grid, blk, 0, s, b);
+    return hipGetLastError();
 }
 
 template <typename T>

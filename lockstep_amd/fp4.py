@@ -21,6 +21,8 @@ along the other axis), and the E8M0 <-> fp32 scale conversions.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _capi as C
@@ -209,6 +211,53 @@ def quantize_pack_mxfp4_2d(x: torch.Tensor, scale_layout: str = "kmajor"):
                rp.data_ptr(), Cn // 2, rs.data_ptr(), lsr, cp.data_ptr(), R // 2, cs.data_ptr(), lsc, fmt,
                C.stream_of(x))
     return rp, rs, cp, cs
+
+
+def quantize_pack_mxfp4_2d_many(xs, scale_layout: str = "kmajor"):
+    """[quantize_pack_mxfp4_2d(x, scale_layout) for x in xs], bit for bit.
+    bf16 / fp16 tensors of one dtype with both sizes multiples of 128 go to
+    the device in one launch per group of up to 8 (lsmx_quantize_mxfp4_2d_batch);
+    any other tensor takes quantize_pack_mxfp4_2d on its own."""
+    if scale_layout not in ("rows", "kmajor"):
+        raise ValueError(f"scale_layout must be 'rows' or 'kmajor', got {scale_layout!r}")
+    out = [None] * len(xs)
+    groups = {}
+    for i, x in enumerate(xs):
+        C.require_device(x)
+        assert x.dim() == 2, "quantize_pack_mxfp4_2d takes 2-D tensors"
+        R, Cn = x.shape
+        if x.dtype in (torch.bfloat16, torch.float16) and R % 128 == 0 and Cn % 128 == 0:
+            groups.setdefault((x.dtype, x.device), []).append(i)
+        else:
+            out[i] = quantize_pack_mxfp4_2d(x, scale_layout=scale_layout)
+    km = scale_layout == "kmajor"
+    for (dt, dev), idx in groups.items():
+        for g0 in range(0, len(idx), 8):
+            part = idx[g0:g0 + 8]
+            items = (C.Q2dItem * len(part))()
+            keep = []
+            for slot, i in enumerate(part):
+                x = xs[i]
+                R, Cn = x.shape
+                if x.stride(1) != 1 or (R > 1 and x.stride(0) < Cn) or x.data_ptr() % 16 or (x.stride(0) * 2) % 16:
+                    x = x.contiguous()
+                rp = torch.empty((R, Cn // 2), dtype=torch.uint8, device=dev)
+                cp = torch.empty((Cn, R // 2), dtype=torch.uint8, device=dev)
+                if km:
+                    rs = torch.empty((Cn // 128, R, 4), dtype=torch.uint8, device=dev)
+                    cs = torch.empty((R // 128, Cn, 4), dtype=torch.uint8, device=dev)
+                    lsr, lsc = R, Cn
+                else:
+                    rs = torch.empty((R, Cn // 32), dtype=torch.uint8, device=dev)
+                    cs = torch.empty((Cn, R // 32), dtype=torch.uint8, device=dev)
+                    lsr, lsc = Cn // 32, R // 32
+                items[slot] = C.Q2dItem(x.data_ptr(), R, Cn, x.stride(0) if R > 1 else Cn, rp.data_ptr(), Cn // 2,
+                                        rs.data_ptr(), lsr, cp.data_ptr(), R // 2, cs.data_ptr(), lsc)
+                keep.append(x)
+                out[i] = (rp, rs, cp, cs)
+            C.call("lsmx_quantize_mxfp4_2d_batch", ctypes.addressof(items), len(part), C.dtype_code(dt),
+                   C.SCALE_E8M0_KMAJOR if km else C.SCALE_E8M0, C.stream_of(keep[0]))
+    return out
 
 
 def e8m0_to_scale(e8m0: torch.Tensor) -> torch.Tensor:

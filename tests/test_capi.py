@@ -76,6 +76,30 @@ def test_bad_dtype_and_alignment_are_rejected():
     assert rc == C.ERR_DTYPE
 
 
+def test_batched_quantizer_and_quantizing_gemm_validate_before_launch():
+    """lsmx_quantize_mxfp4_2d_batch checks every item as lsmx_quantize_mxfp4_2d
+    does, and at most 8 items; lsmx_gemm_f4f4_quant takes whole 256 x 256
+    tiles and 256-deep K only."""
+    assert _rc("lsmx_quantize_mxfp4_2d_batch", None, 1, C.BF16, C.SCALE_E8M0_KMAJOR, None) == C.ERR_ARG
+    items = (C.Q2dItem * 9)()
+    assert _rc("lsmx_quantize_mxfp4_2d_batch", ctypes.addressof(items), 9, C.BF16, C.SCALE_E8M0_KMAJOR,
+               None) == C.ERR_SHAPE
+    f = 0x1000
+    items[0] = C.Q2dItem(f, 100, 128, 128, f, 64, f, 100, f, 64, f, 128)
+    assert _rc("lsmx_quantize_mxfp4_2d_batch", ctypes.addressof(items), 1, C.BF16, C.SCALE_E8M0_KMAJOR,
+               None) == C.ERR_SHAPE
+    assert "multiples of 128" in C.last_error()
+    items[0] = C.Q2dItem(f, 128, 128, 128, f, 64, f, 128, f, 64, f, 128)
+    assert _rc("lsmx_quantize_mxfp4_2d_batch", ctypes.addressof(items), 1, C.F32, C.SCALE_E8M0_KMAJOR,
+               None) == C.ERR_DTYPE
+    q = lambda M, N, K: _rc("lsmx_gemm_f4f4_quant", FAKE, K // 2, FAKE, M, FAKE, K // 2, FAKE, N, None, N,  # noqa: E731
+                            FAKE, N // 2, FAKE, M, FAKE, M // 2, FAKE, N, M, N, K, None)
+    assert q(384, 256, 256) == C.ERR_SHAPE and "multiples of 256" in C.last_error()
+    assert q(256, 256, 128) == C.ERR_SHAPE
+    assert _rc("lsmx_gemm_f4f4_quant", None, 128, FAKE, 256, FAKE, 128, FAKE, 256, None, 256, FAKE, 128, FAKE,
+               256, FAKE, 128, FAKE, 256, 256, 256, 256, None) == C.ERR_ARG
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="a GPU is present")
 def test_device_guard_without_gpu():
     assert _rc("lsmx_device_check") == C.ERR_DEVICE

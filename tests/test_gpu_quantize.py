@@ -398,3 +398,27 @@ def test_quantize_both_axes_falls_back_for_other_inputs(dev, fp4mod, oracle):
         x = gen.normal(R * C, (R, C))
         xh = x if dtype == "f32" else gen.to_bf16_bits(x)
         _check_2d(fp4mod, oracle, xh, None if dtype == "f32" else dtype, dev, layouts=("rows",))
+
+
+def test_quantize_both_axes_batch(dev, fp4mod):
+    """quantize_pack_mxfp4_2d_many: tensors of one dtype with sizes multiples
+    of 128 share one launch (lsmx_quantize_mxfp4_2d_batch, up to 8 per
+    launch), the rest run alone; every output equals the one-tensor call's
+    bytes.  Includes an fp16 group beside a bf16 one, a transposed view, a
+    zero tensor, a shape off the 128 grid and two launches for 11 tensors."""
+    g = torch.Generator(device=dev).manual_seed(21)
+    rn = lambda *s: torch.randn(s, device=dev, generator=g)   # noqa: E731
+    xs = [rn(256, 384).to(torch.bfloat16), rn(1024, 128).to(torch.float16), rn(384, 256).to(torch.bfloat16).t(),
+          (rn(2048, 8192) * 0.05).to(torch.bfloat16), torch.zeros((128, 128), device=dev, dtype=torch.bfloat16),
+          rn(128, 256).to(torch.float16)]
+    many = [(rn(128, 256) * (k + 1)).to(torch.bfloat16) for k in range(11)]
+    # off the 128 grid (row-major scales only): the one-tensor path
+    mixed = [rn(96, 256).to(torch.bfloat16), rn(128, 128).to(torch.bfloat16)]
+    for group, lays in ((xs, ("kmajor", "rows")), (many, ("kmajor", "rows")), (mixed, ("rows",))):
+        for lay in lays:
+            got = fp4mod.quantize_pack_mxfp4_2d_many(group, scale_layout=lay)
+            assert len(got) == len(group)
+            for x, gt in zip(group, got):
+                want = fp4mod.quantize_pack_mxfp4_2d(x, scale_layout=lay)
+                for a, b in zip(gt, want):
+                    assert a.shape == b.shape and torch.equal(a, b), (tuple(x.shape), lay)
