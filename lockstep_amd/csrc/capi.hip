@@ -358,6 +358,10 @@ int lsmx_gemm_f4f4_quant(const uint8_t *a_pk, int64_t lda, const void *a_scale, 
     if (int r = check_scale(fn, b_scale, ld_sb, LSMX_SCALE_E8M0_KMAJOR, 4, N, K)) return r;
     if (lda >= ((int64_t)1 << 24) || ldb >= ((int64_t)1 << 24))
         return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
+    // the epilogue's per-lane store offsets are 32-bit: 16 rows of codes
+    // (and of C) past a wave-uniform base
+    if (ld_codes_r >= ((int64_t)1 << 27) || ld_codes_c >= ((int64_t)1 << 27) || (c && ldc >= ((int64_t)1 << 26)))
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit store offsets", fn);
     if (c && (!aligned(c, 16) || (ldc * 2) % 16)) return fail(LSMX_ERR_ALIGN, "%s: c rows must be 16-byte aligned", fn);
     if (!aligned(codes_r, 4) || ld_codes_r % 4 || !aligned(codes_c, 8) || ld_codes_c % 8)
         return fail(LSMX_ERR_ALIGN, "%s: row codes need 4-byte, column codes 8-byte aligned rows", fn);

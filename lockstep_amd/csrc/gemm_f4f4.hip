@@ -598,6 +598,21 @@ template <bool ANY>
 LSMX_DEV void qepi_store(const uint32_t (&cb)[4][8][2], const uint32_t (&cam)[2][4], const GemmArgs &g, int64_t r0,
                          int64_t c0, int el) {
     const int q = el & 3, grp = el >> 4, r16 = el & 15;
+    const bool odd = (el & 4) != 0;
+    const int cl = 16 * (odd ? 1 : 0) + 8 * ((el >> 3) & 1);
+    // Store addresses: a wave-uniform base per array (scalar registers) plus
+    // a 32-bit lane offset (the launcher bounds the strides), so that each
+    // store costs no 64-bit address arithmetic.
+    uint8_t *const ccb = g.codes_c + c0 * g.ld_cc + r0 / 2;
+    const uint32_t ccl = (uint32_t)(r16 * g.ld_cc + 8 * grp);
+    uint8_t *const scb = g.scale_c + ((r0 >> 7) * g.ld_sc + c0) * 4 + 2 * ((r0 >> 6) & 1);
+    const uint32_t scl = (uint32_t)((16 * grp + r16) * 4);
+    uint8_t *const rcb = g.codes_r + r0 * g.ld_cr + c0 / 2;
+    const uint32_t rcl = (uint32_t)((4 * grp + q) * g.ld_cr + cl / 2);
+    uint8_t *const rsb = g.scale_r + ((c0 >> 7) * g.ld_sr + r0) * 4;
+    const uint32_t rsl = (uint32_t)((4 * grp + q) * 4);
+    uint8_t *const cwb = reinterpret_cast<uint8_t *>(g.c) + (r0 * g.ldc + c0) * 2;
+    const uint32_t cwl = (uint32_t)(((4 * grp + q) * g.ldc + cl) * 2);
     // ---- column form: codes_c [N][M / 2], scale_c [M / 128][N][4]
     uint32_t sp[8];
 #pragma unroll
@@ -619,29 +634,24 @@ LSMX_DEV void qepi_store(const uint32_t (&cb)[4][8][2], const uint32_t (&cam)[2]
             sp[j] = ip == 0 ? e8 : sp[j] | (e8 << 8);
         }
         const u32x2 v = qepi_col_regroup(d[0], d[1], grp);
-        *reinterpret_cast<u32x2 *>(g.codes_c + (c0 + 16 * j + r16) * g.ld_cc + r0 / 2 + 8 * grp) = v;
+        *reinterpret_cast<u32x2 *>(ccb + j * (16 * g.ld_cc) + ccl) = v;
     }
     // the two scale bytes of column 16 j + r16 from lane group j & 3
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
         const uint32_t v = grp == 0 ? sp[4 * jj] : grp == 1 ? sp[4 * jj + 1] : grp == 2 ? sp[4 * jj + 2] : sp[4 * jj + 3];
-        const int64_t col = c0 + 16 * (4 * jj + grp) + r16;
-        *reinterpret_cast<uint16_t *>(g.scale_c + ((r0 >> 7) * g.ld_sc + col) * 4 + 2 * ((r0 >> 6) & 1)) = (uint16_t)v;
+        *reinterpret_cast<uint16_t *>(scb + 256 * jj + scl) = (uint16_t)v;
     }
     // ---- row form: codes_r [M][N / 2], scale_r [N / 128][M][4]; lanes hold
     // 8 consecutive columns of one row after the in-quad transpose
-    const bool odd = (el & 4) != 0;
-    const int cl = 16 * (odd ? 1 : 0) + 8 * ((el >> 3) & 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int64_t row = r0 + 16 * i + 4 * grp + q;
         uint32_t rs = 0;
 #pragma unroll
         for (int jp = 0; jp < 4; ++jp) {
             const u32x4 p = pack16_rows8_of(quad_pack16_bits(cb[i][2 * jp][0], cb[i][2 * jp][1], q),
                                             quad_pack16_bits(cb[i][2 * jp + 1][0], cb[i][2 * jp + 1][1], q), odd);
-            const int64_t col = c0 + 32 * jp + cl;
-            if (g.c) *reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(g.c) + row * g.ldc + col) = p;
+            if (g.c) *reinterpret_cast<u32x4 *>(cwb + i * (32 * g.ldc) + 64 * jp + cwl) = p;
             const uint32_t m = pk_max16(pk_max16(p[0] & 0x7FFF7FFFu, p[1] & 0x7FFF7FFFu),
                                         pk_max16(p[2] & 0x7FFF7FFFu, p[3] & 0x7FFF7FFFu));
             // the block's 32 columns lie in lanes l, l ^ 4, l ^ 8, l ^ 12:
@@ -656,10 +666,10 @@ LSMX_DEV void qepi_store(const uint32_t (&cb)[4][8][2], const uint32_t (&cam)[2]
                 f[2 * h] = qepi_nudge<ANY>(p[h] << 16);
                 f[2 * h + 1] = qepi_nudge<ANY>(p[h] & 0xFFFF0000u);
             }
-            *reinterpret_cast<uint32_t *>(g.codes_r + row * g.ld_cr + col / 2) = qepi_codes<ANY>(f, e8);
+            *reinterpret_cast<uint32_t *>(rcb + i * (16 * g.ld_cr) + 16 * jp + rcl) = qepi_codes<ANY>(f, e8);
             rs |= e8 << (8 * jp);
         }
-        if ((el & 12) == 0) *reinterpret_cast<uint32_t *>(g.scale_r + ((c0 >> 7) * g.ld_sr + row) * 4) = rs;
+        if ((el & 12) == 0) *reinterpret_cast<uint32_t *>(rsb + 64 * i + rsl) = rs;
     }
 }
 
