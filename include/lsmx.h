@@ -161,9 +161,11 @@ int lsmx_fp4_to_e4m3(const uint32_t *in, uint32_t *out, int64_t n_words, void *s
  *   row-major scale rows (in bytes) below 2^24.
  * fp32 scales are the powers of two fp4.py produces.  A scale with no E8M0
  * form (not a positive power of two in [2^-127, 2^127]) is taken as E8M0
- * NaN: the outputs that use it are NaN, where the reference's fp32
- * multiply (mxfp4_gemm.py:148-150) would scale by it.  E8M0 byte 0 is
- * 2^-127.  K-major E8M0 scales with K % 256 == 0 run the fastest kernel
+ * NaN here: the outputs that use it are NaN, where the reference's fp32
+ * multiply (mxfp4_gemm.py:148-150) would scale by it; for any fp32 scale,
+ * convert with lsmx_scale_to_e8m0_batch (flag, epoch), call this with the
+ * K-major bytes and follow with lsmx_gemm_mx_promote (flag, epoch), as
+ * mxfp4_gemm.mxfp4_gemm_packed does.  E8M0 byte 0 is 2^-127.  K-major E8M0 scales with K % 256 == 0 run the fastest kernel
  * (16 x 16 x 128 scaled MFMA on 256-code stages); the other formats and K
  * % 256 != 0 run a 32 x 32 x 64 kernel on 128-code stages.  Every format of
  * the same scales gives the same bits. */
@@ -303,7 +305,9 @@ int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0
  *   [K/128, ld_sa, 4] and [K/128, ld_sb, 4] with ld_sa >= M, ld_sb >= N
  *   (lsmx_scale_to_e8m0 of fp4.py's fp32 power-of-two scales);
  *   c [M, ldc] of c_dtype (LSMX_F32 | LSMX_BF16 | LSMX_F16).  K % 128 == 0
- *   (mxfp4_gemm.py:78). */
+ *   (mxfp4_gemm.py:78).  fp32 scales that are not powers of two take the
+ *   lsmx_scale_to_e8m0_batch + lsmx_gemm_mx_promote sequence described at
+ *   lsmx_gemm_f4f4 (op_fmt LSMX_E4M3). */
 int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *bt,
                    int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, int scale_fmt, void *c, int c_dtype,
                    int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
@@ -327,6 +331,49 @@ int lsmx_transpose(const void *x, int elem_bytes, int64_t rows, int64_t cols, in
 #define LSMX_E8M0_OUT_KMAJOR 2
 int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, int layout, uint8_t *out,
                        int64_t ldo, void *stream);
+
+/* lsmx_scale_to_e8m0 with K-major output for up to 4 fp32 scale tensors in
+ * one launch (the A and B scales of one GEMM call: mxfp4_gemm.py:161-174's
+ * and :74-87's fp32 scales, regrouped for the fast kernels), and a test for
+ * the scales the fast kernels cannot apply: when any scale has no E8M0 form
+ * (not a power of two in [2^-127, 2^127]: 1.5, 0, -2, inf, NaN ...) and
+ * flag is not NULL, the launch writes epoch to *flag (8-byte aligned device
+ * memory); otherwise it leaves *flag as it was.  A caller picks an epoch it
+ * has never used with that flag, so no earlier content can equal it, and
+ * passes flag and epoch to lsmx_gemm_mx_promote after the fast GEMM. */
+typedef struct {
+    const float *s;   /* [rows, cols], row stride lds (elements)           */
+    int64_t rows, cols, lds;
+    int layout;       /* 0 or LSMX_E8M0_IN_T; the output is always K-major */
+    uint8_t *out;     /* [blocks/4][ldo][4], 4-byte aligned, ldo >= out rows */
+    int64_t ldo;
+} lsmx_e8m0_item;
+int lsmx_scale_to_e8m0_batch(const lsmx_e8m0_item *items, int n, uint64_t *flag, uint64_t epoch,
+                             void *stream);
+
+/* The reference's own arithmetic for fp32 block scales of any value:
+ *   acc = 0;  for kb in 0 .. K/32-1:  acc = fma(p_kb, a_scale[m,kb] * b_scale[n,kb], acc)
+ *   p_kb = the 32-block product of A[m, :] and Bt[n, :] (fp32; exact on the E2M1 grid)
+ *   C[m, n] = acc rounded to c_dtype
+ * Replaces the promotion step of mxfp4_gemm.py:141-150 (_mxfp4_gemm_packed_
+ * kernel, op_fmt LSMX_CODES_PACKED: a [M, lda] and bt [N, ldb] packed FP4
+ * bytes) and mxfp4_gemm.py:52-63 (_mxfp4_gemm_fp8_kernel, op_fmt
+ * LSMX_E4M3: E4M3 bytes, bt = the reference's b_fp8 [K, N] transposed), with
+ * Triton's fma contraction of `acc += p * (sa * sb)`.  Scale (row r, block
+ * kb) of A is a_scale[r * sa_row + kb * sa_blk], likewise b_scale (the
+ * reference's b_scale [K/32, N] of mxfp4_gemm_fp8 has sb_row = 1, sb_blk =
+ * N).  K % 128 == 0; operand rows 16-byte aligned; c [M, ldc] of c_dtype
+ * (LSMX_F32 | LSMX_BF16 | LSMX_F16).  With flag NULL it always computes.
+ * Otherwise the launch does nothing unless *flag == epoch: call
+ * lsmx_scale_to_e8m0_batch(flag, epoch), then lsmx_gemm_f4f4 / lsmx_gemm_f8f8
+ * on its E8M0 bytes, then this on the same C, and a call whose scales are all
+ * powers of two costs one early-exit launch while the others get every
+ * output recomputed by this kernel.  Vector-ALU bound (2 fp32 operations per
+ * output per 32-block): a fallback, not a fast path. */
+int lsmx_gemm_mx_promote(const uint8_t *a, int64_t lda, const float *a_scale, int64_t sa_row, int64_t sa_blk,
+                         const uint8_t *bt, int64_t ldb, const float *b_scale, int64_t sb_row, int64_t sb_blk,
+                         int op_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                         const uint64_t *flag, uint64_t epoch, void *stream);
 
 #ifdef __cplusplus
 }

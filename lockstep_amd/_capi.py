@@ -8,6 +8,8 @@ op that needs it -- there is no CPU or torch fallback for the kernels.
 from __future__ import annotations
 
 import ctypes
+import itertools
+import os
 import threading
 from pathlib import Path
 
@@ -23,6 +25,7 @@ CODES_PACKED, CODES_UNPACKED = 0, 1
 SCALE_E8M0, SCALE_F32, SCALE_E8M0_KMAJOR = 0, 1, 2
 
 _i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
 _int = ctypes.c_int
 _vp = ctypes.c_void_p
 
@@ -56,6 +59,9 @@ SIGNATURES = {
     "lsmx_gemm_f8f8": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_transpose": [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp],
     "lsmx_scale_to_e8m0": [_vp, _i64, _i64, _i64, _int, _vp, _i64, _vp],
+    "lsmx_scale_to_e8m0_batch": [_vp, _int, _vp, _u64, _vp],
+    "lsmx_gemm_mx_promote": [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _int, _vp, _int, _i64, _i64,
+                             _i64, _i64, _vp, _u64, _vp],
 }
 
 RET_I64 = ("lsmx_gemm_bf16f4_workspace",)
@@ -66,6 +72,22 @@ class Q2dItem(ctypes.Structure):
     _fields_ = [("x", _vp), ("rows", _i64), ("cols", _i64), ("ldx", _i64),
                 ("codes_r", _vp), ("ld_codes_r", _i64), ("scale_r", _vp), ("ld_scale_r", _i64),
                 ("codes_c", _vp), ("ld_codes_c", _i64), ("scale_c", _vp), ("ld_scale_c", _i64)]
+
+
+class E8m0Item(ctypes.Structure):
+    """lsmx_e8m0_item of include/lsmx.h."""
+    _fields_ = [("s", _vp), ("rows", _i64), ("cols", _i64), ("lds", _i64), ("layout", _int), ("out", _vp),
+                ("ldo", _i64)]
+
+
+# Epochs for lsmx_scale_to_e8m0_batch's flag: unique within the process and
+# starting at a random value, so no earlier content of a flag equals a new one.
+_epochs = itertools.count((int.from_bytes(os.urandom(6), "little") << 16) | 1)
+
+
+def next_epoch() -> int:
+    return next(_epochs) & 0xFFFFFFFFFFFFFFFF
+
 
 _lib = None
 _lock = threading.Lock()

@@ -18,7 +18,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "liblsmx.so"
-SOURCES = ["capi.hip", "quantize.hip", "gemm_f4f4.hip", "gemm_bf16f4.hip", "gemm_dense.hip", "gemm_dense_ring.hip", "gemm_f8f8.hip"]
+SOURCES = ["capi.hip", "quantize.hip", "gemm_f4f4.hip", "gemm_bf16f4.hip", "gemm_dense.hip", "gemm_dense_ring.hip", "gemm_f8f8.hip", "gemm_promote.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere in the device code.

@@ -474,6 +474,75 @@ int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, 
     return launched(lsmx::launch_scale_to_e8m0(s, rows, cols, lds, layout, out, ldo, (hipStream_t)stream), fn);
 }
 
+int lsmx_scale_to_e8m0_batch(const lsmx_e8m0_item *items, int n, uint64_t *flag, uint64_t epoch, void *stream) {
+    const char *fn = "lsmx_scale_to_e8m0_batch";
+    if (!items && n) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (n < 0 || n > lsmx::kE8Batch) return fail(LSMX_ERR_SHAPE, "%s: n must be 0 .. %d", fn, lsmx::kE8Batch);
+    if (flag && !aligned(flag, 8)) return fail(LSMX_ERR_ALIGN, "%s: flag must be 8-byte aligned", fn);
+    lsmx::E8m0Batch b{};
+    int64_t wgs = 0;
+    for (int k = 0; k < n; ++k) {
+        const lsmx_e8m0_item &it = items[k];
+        if ((!it.s || !it.out) && it.rows && it.cols) return fail(LSMX_ERR_ARG, "%s: null pointer in item %d", fn, k);
+        if (it.layout & ~LSMX_E8M0_IN_T)
+            return fail(LSMX_ERR_ARG, "%s: item %d layout must be 0 or LSMX_E8M0_IN_T (the output is K-major)", fn, k);
+        const bool tin = it.layout & LSMX_E8M0_IN_T;
+        const int64_t orows = tin ? it.cols : it.rows, blocks = tin ? it.rows : it.cols;
+        if (it.rows < 0 || it.cols < 0 || it.lds < it.cols || it.ldo < orows)
+            return fail(LSMX_ERR_SHAPE, "%s: item %d: bad shape", fn, k);
+        if (blocks % 4) return fail(LSMX_ERR_SHAPE, "%s: item %d: K-major output needs a multiple of 4 blocks", fn, k);
+        if (!aligned(it.s, 4) || !aligned(it.out, 4)) return fail(LSMX_ERR_ALIGN, "%s: item %d misaligned", fn, k);
+        if (it.rows > 0 && it.cols > ((int64_t)1 << 38) / it.rows) return fail(LSMX_ERR_SHAPE, "%s: item %d too large", fn, k);
+        const int64_t w = ((orows + 63) / 64) * ((blocks / 4 + 15) / 16);
+        if (w == 0) continue;  // empty tensors take no workgroup
+        if (wgs + w > 0x7FFFFFFF) return fail(LSMX_ERR_SHAPE, "%s: too many workgroups", fn);
+        b.it[b.n] = lsmx::E8m0Item{it.s, orows, blocks / 4, it.lds, (int)tin, it.out, it.ldo};
+        wgs += w;
+        b.end[b.n++] = wgs;
+    }
+    b.flag = flag;
+    b.epoch = epoch;
+    if (int r = device_guard()) return r;
+    if (b.n == 0) return LSMX_OK;
+    return launched(lsmx::launch_scale_to_e8m0_batch(b, (hipStream_t)stream), fn);
+}
+
+int lsmx_gemm_mx_promote(const uint8_t *a, int64_t lda, const float *a_scale, int64_t sa_row, int64_t sa_blk,
+                         const uint8_t *bt, int64_t ldb, const float *b_scale, int64_t sb_row, int64_t sb_blk,
+                         int op_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                         const uint64_t *flag, uint64_t epoch, void *stream) {
+    const char *fn = "lsmx_gemm_mx_promote";
+    if (!a || !a_scale || !bt || !b_scale || !c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (op_fmt != LSMX_CODES_PACKED && op_fmt != LSMX_E4M3)
+        return fail(LSMX_ERR_DTYPE, "%s: op_fmt must be LSMX_CODES_PACKED or LSMX_E4M3", fn);
+    if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % 128) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
+    const int64_t kbytes = op_fmt == LSMX_CODES_PACKED ? K / 2 : K;
+    if (lda < kbytes || ldb < kbytes || ldc < N) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (sa_row < 0 || sa_blk < 0 || sb_row < 0 || sb_blk < 0) return fail(LSMX_ERR_SHAPE, "%s: negative scale stride", fn);
+    if (!aligned(a, 16) || !aligned(bt, 16) || lda % 16 || ldb % 16)
+        return fail(LSMX_ERR_ALIGN, "%s: operand rows must be 16-byte aligned", fn);
+    if (!aligned(a_scale, 4) || !aligned(b_scale, 4) || !aligned(c, elem_size(c_dtype)) || (flag && !aligned(flag, 8)))
+        return fail(LSMX_ERR_ALIGN, "%s: misaligned scale, output or flag", fn);
+    // the kernel forms every load offset in 32 bits, over rows up to a
+    // tile past M or N and blocks up to a chunk past K
+    const int64_t lim = (int64_t)1 << 31, nkb = K / 32;
+    if (128 * lda + kbytes + 256 >= lim || 128 * ldb + kbytes + 256 >= lim)
+        return fail(LSMX_ERR_SHAPE, "%s: operand rows of %lld / %lld bytes are too long", fn, (long long)lda,
+                    (long long)ldb);
+    if (M + 128 > lim / 4 || N + 128 > lim / 4 || 4 * ((M + 128) * sa_row + (nkb + 8) * sa_blk) >= lim ||
+        4 * ((N + 128) * sb_row + (nkb + 8) * sb_blk) >= lim)
+        return fail(LSMX_ERR_SHAPE, "%s: scale tensors span 2^31 bytes or more", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    const int sa_bytes = nkb ? (int)(4 * ((M - 1) * sa_row + (nkb - 1) * sa_blk + 1)) : 0;
+    const int sb_bytes = nkb ? (int)(4 * ((N - 1) * sb_row + (nkb - 1) * sb_blk + 1)) : 0;
+    lsmx::PromoteArgs g{a, lda, bt, ldb, a_scale, sa_row, sa_blk, b_scale, sb_row, sb_blk, sa_bytes, sb_bytes,
+                        c, c_dtype, ldc, M, N, K, flag, epoch};
+    return launched(lsmx::launch_gemm_promote(g, op_fmt == LSMX_CODES_PACKED, (hipStream_t)stream), fn);
+}
+
 static int w4_common(const char *fn, const void *a0, const void *a1, int a_dtype, int64_t lda, const uint8_t *w_pk,
                      int64_t ldw, const void *w_scale, int64_t ld_sw, int scale_fmt, void *c0, void *c1, int c_dtype,
                      int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream, void *ws = nullptr,

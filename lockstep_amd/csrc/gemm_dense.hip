@@ -398,6 +398,55 @@ __global__ __launch_bounds__(256) void scale_to_e8m0_km4_tiled_kernel(const floa
     }
 }
 
+// Up to four fp32 scale tensors -> K-major E8M0 dwords in one launch (the A
+// and B scales of one GEMM call).  A workgroup converts 64 output rows x 16
+// four-block groups of one tensor through a byte tile in LDS: its loads walk
+// the contiguous axis of s (the blocks of a row, or with tin the rows of a
+// block), its stores 64 consecutive dwords of a group.  A scale with no E8M0
+// form becomes 0xFF as above and, with a flag, makes the wave that met it
+// write the caller's epoch there (one store per wave), which the promotion
+// GEMM that follows checks.
+__global__ __launch_bounds__(256) void scale_to_e8m0_batch_kernel(E8m0Batch b) {
+    __shared__ uint32_t tile[16][64];
+    const int64_t blk = (int64_t)blockIdx.x;
+    int k = 0;
+    while (k + 1 < b.n && blk >= b.end[k]) ++k;
+    const E8m0Item &it = b.it[k];
+    const int64_t local = blk - (k ? b.end[k - 1] : 0);
+    const int64_t tiles_o = (it.orows + 63) / 64;
+    const int64_t o0 = (local % tiles_o) * 64, g0 = (local / tiles_o) * 16;
+    const int t = threadIdx.x;
+    uint8_t *tb = reinterpret_cast<uint8_t *>(tile);
+    bool bad = false;
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+        const int q = i * 256 + t;
+        const int r = it.tin ? (q & 63) : (q >> 6), c = it.tin ? (q >> 6) : (q & 63);  // out row, block in tile
+        const int64_t o = o0 + r, bk = 4 * g0 + c;
+        if (o < it.orows && bk < 4 * it.groups) {
+            const uint32_t e = f32_scale_e8m0(f2u(it.tin ? it.s[bk * it.lds + o] : it.s[o * it.lds + bk]));
+            bad |= e == 0xFFu;
+            tb[((c >> 2) * 64 + r) * 4 + (c & 3)] = (uint8_t)e;
+        }
+    }
+    if (b.flag) {
+        const uint64_t m = __ballot(bad);
+        if (m && (t & 63) == __builtin_ctzll(m)) *b.flag = b.epoch;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = i * 256 + t, gi = q >> 6, r = q & 63;
+        const int64_t o = o0 + r, gr = g0 + gi;
+        if (o < it.orows && gr < it.groups) *reinterpret_cast<uint32_t *>(it.out + (gr * it.ldo + o) * 4) = tile[gi][r];
+    }
+}
+
+hipError_t launch_scale_to_e8m0_batch(const E8m0Batch &b, hipStream_t s) {
+    hipLaunchKernelGGL(scale_to_e8m0_batch_kernel, dim3((unsigned)b.end[b.n - 1]), dim3(256), 0, s, b);
+    return hipGetLastError();
+}
+
 template <int DT, int MODE, bool SHB, bool SCALED, int CT, bool ATOMIC>
 static void launch_d(const DenseArgs &g, hipStream_t s) {
     const int tiles = (int)(((g.M + dn::BM - 1) / dn::BM) * ((g.N + dn::BN - 1) / dn::BN));

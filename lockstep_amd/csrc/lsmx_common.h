@@ -83,6 +83,14 @@ LSMX_HD uint32_t f32_scale_e8m0(uint32_t b) {
     return pow2 ? (b == 0x00400000u ? 0u : ex) : 0xFFu;
 }
 
+// 4 nibbles (low 16 bits of p) -> 4 E4M3 bytes: magnitude by a byte permute
+// against the 8-entry table {00 30 38 3C 40 44 48 4C}, sign bit 3 -> bit 7.
+LSMX_DEV uint32_t fp4x4_to_e4m3x4(uint32_t p) {
+    const uint32_t spread = (p & 0xF) | ((p & 0xF0) << 4) | ((p & 0xF00) << 8) | ((p & 0xF000) << 12);
+    const uint32_t mag = __builtin_amdgcn_perm(0x4C484440u, 0x3C383000u, spread & 0x07070707u);
+    return mag | ((spread & 0x08080808u) << 4);
+}
+
 // E2M1 code -> value (fp4.py:24).
 LSMX_HD float e2m1_value(uint32_t code) {
     const float m[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};

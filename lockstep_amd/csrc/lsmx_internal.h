@@ -123,6 +123,47 @@ struct DenseArgs {
     int64_t k_split;         // K per split (== K without split-K)
 };
 
+// The reference's promotion arithmetic for fp32 block scales of any value
+// (gemm_promote.hip): A [M, lda] and Bt [N, ldb] as packed FP4 codes or E4M3
+// bytes, scale (r, kb) of A at sa[r * sa_r + kb * sa_k] (likewise sb).  With
+// a flag the launch does nothing unless *flag == epoch.
+struct PromoteArgs {
+    const uint8_t *a;
+    int64_t lda;
+    const uint8_t *b;
+    int64_t ldb;
+    const float *sa;
+    int64_t sa_r, sa_k;
+    const float *sb;
+    int64_t sb_r, sb_k;
+    int sa_bytes, sb_bytes;  // extents of the scale tensors (loads past them read 0)
+    void *c;
+    int c_dtype;
+    int64_t ldc;
+    int64_t M, N, K;
+    const uint64_t *flag;
+    uint64_t epoch;
+};
+
+// Up to kE8Batch fp32 scale tensors converted to K-major E8M0 in one launch;
+// end[k] = workgroups of tensors 0 .. k.  When a scale has no E8M0 form the
+// launch writes epoch to *flag (if flag is not null).
+constexpr int kE8Batch = 4;
+struct E8m0Item {
+    const float *s;
+    int64_t orows, groups, lds;  // out rows, 4-block groups, stride of s
+    int tin;                     // s is [blocks, out rows] (else [out rows, blocks])
+    uint8_t *out;
+    int64_t ldo;
+};
+struct E8m0Batch {
+    E8m0Item it[kE8Batch];
+    int64_t end[kE8Batch];
+    int n;
+    uint64_t *flag;
+    uint64_t epoch;
+};
+
 hipError_t launch_quantize(const QuantArgs &a, bool cols, hipStream_t s);
 hipError_t launch_quantize_2d(const Quant2dArgs &a, hipStream_t s);
 hipError_t launch_quantize_2d_batch(const Quant2dBatch &b, hipStream_t s);
@@ -148,5 +189,7 @@ hipError_t launch_transpose(const void *x, int elem_bytes, int64_t rows, int64_t
                             int64_t ldy, hipStream_t s);
 hipError_t launch_scale_to_e8m0(const float *sc, int64_t rows, int64_t cols, int64_t lds, int layout, uint8_t *out,
                                 int64_t ldo, hipStream_t s);
+hipError_t launch_scale_to_e8m0_batch(const E8m0Batch &b, hipStream_t s);
+hipError_t launch_gemm_promote(const PromoteArgs &g, bool fp4, hipStream_t s);
 
 }  // namespace lsmx

@@ -701,14 +701,6 @@ __global__ void unpack_kernel(const uint2 *__restrict__ packed, uint4 *__restric
     }
 }
 
-// 4 nibbles (low 16 bits of p) -> 4 E4M3 bytes: magnitude by a byte permute
-// against the 8-entry table {00 30 38 3C 40 44 48 4C}, sign bit 3 -> bit 7.
-LSMX_DEV uint32_t fp4x4_to_e4m3x4(uint32_t p) {
-    const uint32_t spread = (p & 0xF) | ((p & 0xF0) << 4) | ((p & 0xF00) << 8) | ((p & 0xF000) << 12);
-    const uint32_t mag = __builtin_amdgcn_perm(0x4C484440u, 0x3C383000u, spread & 0x07070707u);
-    return mag | ((spread & 0x08080808u) << 4);
-}
-
 __global__ void fp4_to_e4m3_kernel(const uint32_t *__restrict__ in, uint2 *__restrict__ out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {

@@ -53,14 +53,18 @@ def _scales(s: torch.Tensor, rows: int, nkb: int) -> torch.Tensor:
 def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
     """a_pk [M,K//2] uint8, bt_pk [N,K//2] uint8, a_scale [M,K//32], b_scale [N,K//32].
 
-    Scales are fp32 powers of two (as fp4.quantize_mxfp4 returns) or E8M0
-    bytes (as fp4.quantize_pack_mxfp4 returns), row-major [rows, K//32] or
-    K-major [K//128, rows, 4] (quantize_pack_mxfp4(..., scale_layout="kmajor"));
-    both operands must use the same format.  Row-major scales are regrouped
-    to K-major E8M0 on the device first (fp32 through lsmx_scale_to_e8m0, a
-    scale that is not a power of two becoming E8M0 NaN; E8M0 bytes through a
-    dword transpose), so every format runs the same kernel and gives the same
-    bits.  Returns C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
+    Scales are fp32 (as fp4.quantize_mxfp4 returns) or E8M0 bytes (as
+    fp4.quantize_pack_mxfp4 returns), row-major [rows, K//32] or K-major
+    [K//128, rows, 4] (quantize_pack_mxfp4(..., scale_layout="kmajor")); both
+    operands must use the same format.  Row-major scales are regrouped to
+    K-major E8M0 on the device first (fp32 through lsmx_scale_to_e8m0_batch,
+    E8M0 bytes through a dword transpose), so every format runs the same
+    kernel and gives the same bits.  fp32 scales that are not all powers of
+    two (1.5, 0, -2, inf ...; the quantizer never makes them) have no E8M0
+    form: the conversion flags them and lsmx_gemm_mx_promote then recomputes
+    C with the reference's own promotion arithmetic (mxfp4_gemm.py:141-150),
+    a vector-ALU-bound fallback; with power-of-two scales that launch exits
+    at once.  Returns C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
     M, Kh = a_pk.shape
     N, Kh2 = bt_pk.shape
     K = Kh * 2
@@ -82,17 +86,25 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
             "K-major scales must be [K//128, rows, 4]"
         a_scale, b_scale = a_scale.contiguous(), b_scale.contiguous()
         fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
-    else:
-        # the reference's spelling (fp32 scales from quantize_mxfp4) and
+        promote = None
+    elif a_scale.dtype == torch.uint8:
         # row-major E8M0 bytes: regroup to the K-major layout the GEMM
         # streams fastest (one dword per row per 128 codes, rows contiguous)
         a_scale = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
         b_scale = _e8m0_kmajor(b_scale, N, K // 32, transposed=False)
         fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
-    C.call("lsmx_gemm_f4f4", a_pk.data_ptr(), a_pk.stride(0) if M > 1 else Kh,
-           a_scale.data_ptr(), lsa, bt_pk.data_ptr(), bt_pk.stride(0) if N > 1 else Kh,
-           b_scale.data_ptr(), lsb, fmt, c.data_ptr(), _out_code(out_dtype), N, M, N, K,
-           C.stream_of(c))
+        promote = None
+    else:
+        # the reference's spelling (fp32 scales from quantize_mxfp4)
+        sa32, sb32 = _f32_rows(a_scale), _f32_rows(b_scale)
+        (a_scale, b_scale), flag, epoch = _e8m0_kmajor_flagged([(sa32, M, False), (sb32, N, False)], K // 32)
+        fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
+        promote = (sa32, False, sb32, False, flag, epoch)
+    lda, ldb = a_pk.stride(0) if M > 1 else Kh, bt_pk.stride(0) if N > 1 else Kh
+    C.call("lsmx_gemm_f4f4", a_pk.data_ptr(), lda, a_scale.data_ptr(), lsa, bt_pk.data_ptr(), ldb,
+           b_scale.data_ptr(), lsb, fmt, c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
+    if promote is not None:
+        _promote(a_pk, lda, bt_pk, ldb, C.CODES_PACKED, c, K, *promote)
     return c
 
 
@@ -255,6 +267,54 @@ def _e8m0_kmajor(s: torch.Tensor, rows: int, nkb: int, transposed: bool) -> torc
     return out
 
 
+def _f32_rows(s: torch.Tensor) -> torch.Tensor:
+    """fp32 scales with unit stride along the last axis."""
+    if s.dtype != torch.float32:
+        s = s.float()
+    return s if s.stride(-1) == 1 or s.shape[-1] <= 1 else s.contiguous()
+
+
+def _ld(s: torch.Tensor) -> int:
+    return s.stride(0) if s.shape[0] > 1 else s.shape[1]
+
+
+def _e8m0_kmajor_flagged(scales, nkb: int):
+    """fp32 block scales -> K-major E8M0 bytes [nkb//4, rows, 4] for the fast
+    kernels, all tensors in one launch (lsmx_scale_to_e8m0_batch).  scales:
+    (s, rows, transposed) with s [rows, nkb], or [nkb, rows] when transposed.
+    Returns (outputs, flag, epoch): the launch writes epoch to the device word
+    flag when some scale has no E8M0 form, which lsmx_gemm_mx_promote checks."""
+    dev = scales[0][0].device
+    flag = torch.empty(1, dtype=torch.int64, device=dev)
+    epoch = C.next_epoch()
+    items = (C.E8m0Item * len(scales))()
+    outs = []
+    for k, (s, rows, tr) in enumerate(scales):
+        out = torch.empty((nkb // 4, rows, 4), device=dev, dtype=torch.uint8)
+        items[k] = C.E8m0Item(s.data_ptr(), s.shape[0], s.shape[1], _ld(s), C.E8M0_IN_T if tr else 0,
+                              out.data_ptr(), rows)
+        outs.append(out)
+    C.call("lsmx_scale_to_e8m0_batch", items, len(scales), flag.data_ptr(), epoch, C.stream_of(flag))
+    return outs, flag, epoch
+
+
+def _promote(a, lda, bt, ldb, op_fmt, c, K, sa, sa_tr, sb, sb_tr, flag, epoch):
+    """lsmx_gemm_mx_promote over c when flag == epoch: the reference's fp32
+    promotion for scales the fast kernels cannot apply.  sa [M, K//32] (or
+    [K//32, M] when sa_tr), likewise sb."""
+    M, N = c.shape
+
+    def strides(s, tr):  # (row stride, block stride); a size-1 axis gets its dense stride
+        rows, nkb = (s.shape[1], s.shape[0]) if tr else s.shape
+        r, k = (s.stride(1), s.stride(0)) if tr else (s.stride(0), s.stride(1))
+        return (r if rows > 1 else (1 if tr else nkb)), (k if nkb > 1 else (rows if tr else 1))
+
+    (sa_r, sa_k), (sb_r, sb_k) = strides(sa, sa_tr), strides(sb, sb_tr)
+    C.call("lsmx_gemm_mx_promote", a.data_ptr(), lda, sa.data_ptr(), sa_r, sa_k, bt.data_ptr(), ldb,
+           sb.data_ptr(), sb_r, sb_k, op_fmt, c.data_ptr(), _out_code(c.dtype), N, M, N, K, flag.data_ptr(),
+           epoch, C.stream_of(c))
+
+
 def kmajor_operand(b: torch.Tensor) -> torch.Tensor:
     """B [K, N] -> the K-contiguous [N, K] operand the kernels read: B.T itself
     when it already is K-contiguous with 16-byte aligned rows, else a
@@ -277,14 +337,16 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
     """a_fp8 [M,K] K-contig, b_fp8 [K,N] N-contig, a_scale [M,K//32], b_scale [K//32,N].
 
     Operands are E4M3 bytes (float8_e4m3fn or uint8 views of them), normally
-    holding E2M1 values (fp4.codes_to_e4m3).  Scales are fp32 powers of two as
+    holding E2M1 values (fp4.codes_to_e4m3).  Scales are fp32 as
     fp4.quantize_mxfp4 returns, or E8M0 bytes of the same shapes.  Returns
     C[m, n] = sum_kb a_scale[m, kb] b_scale[kb, n] (A_kb . B_kb) in out_dtype:
     the E4M3 products run on the scaled MFMA (v_mfma_scale_f32_32x32x64_
     f8f6f4, E4M3 mode) with the block scales applied by the instruction and
-    fp32 accumulation (reference: mxfp4_gemm.py:29-87).  B is transposed to
-    K-contiguous rows on the device first unless b_fp8 is a transposed view
-    of such rows."""
+    fp32 accumulation (reference: mxfp4_gemm.py:29-87).  fp32 scales that are
+    not all powers of two are flagged by their conversion and C is then
+    recomputed with the reference's promotion (lsmx_gemm_mx_promote,
+    mxfp4_gemm.py:52-63).  B is transposed to K-contiguous rows on the device
+    first unless b_fp8 is a transposed view of such rows."""
     M, K = a_fp8.shape
     K2, N = b_fp8.shape
     assert K == K2 and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
@@ -302,10 +364,18 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
     bt = kmajor_operand(b_fp8.view(torch.uint8))
     # fp32 scales (the reference's form) or E8M0 bytes, either way as K-major
     # E8M0 for the persistent 256 x 256-tile kernel (csrc/gemm_f8f8.hip)
-    sa = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
-    sb = _e8m0_kmajor(b_scale, N, K // 32, transposed=True)
+    promote = None
+    if a_scale.dtype == torch.uint8 or b_scale.dtype == torch.uint8:
+        sa = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
+        sb = _e8m0_kmajor(b_scale, N, K // 32, transposed=True)
+    else:
+        sa32, sb32 = _f32_rows(a_scale), _f32_rows(b_scale)
+        (sa, sb), flag, epoch = _e8m0_kmajor_flagged([(sa32, M, False), (sb32, N, True)], K // 32)
+        promote = (sa32, False, sb32, True, flag, epoch)
     fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
-    C.call("lsmx_gemm_f8f8", a.data_ptr(), a.stride(0) if M > 1 else K, sa.data_ptr(), lsa,
-           bt.data_ptr(), bt.stride(0) if N > 1 else K, sb.data_ptr(), lsb, fmt, c.data_ptr(),
-           _out_code(out_dtype), N, M, N, K, C.stream_of(c))
+    lda, ldb = a.stride(0) if M > 1 else K, bt.stride(0) if N > 1 else K
+    C.call("lsmx_gemm_f8f8", a.data_ptr(), lda, sa.data_ptr(), lsa, bt.data_ptr(), ldb, sb.data_ptr(), lsb, fmt,
+           c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
+    if promote is not None:
+        _promote(a, lda, bt, ldb, C.E4M3, c, K, *promote)
     return c

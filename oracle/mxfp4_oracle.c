@@ -19,6 +19,7 @@
  *   fp4.py:75-78   dequantize_mxfp4    -> orc_dequantize
  *   fp4.py:91-99   pack_fp4/unpack_fp4 -> orc_pack_fp4 / orc_unpack_fp4
  *   cuda/fp4_unpack.cuh:45-61  FP4->E4M3 expansion -> orc_fp4x8_to_e4m3x8
+ *   mxfp4_gemm.py:52-63, 141-150  fp32 promotion per 32-block -> orc_gemm_promote
  *
  * Parity pins (what each function is checked against) are listed in
  * tests/test_oracle.py.
@@ -237,6 +238,34 @@ void orc_fp4x8_to_e4m3x8(const uint32_t *in, int64_t n, uint32_t *out_lo, uint32
         out_lo[i] = lo;
         out_hi[i] = hi;
     }
+}
+
+/* mxfp4_gemm.py:52-63 (_mxfp4_gemm_fp8_kernel) and :141-150
+ * (_mxfp4_gemm_packed_kernel): the K loop promotes every 32-block product to
+ * the fp32 accumulator and multiplies the two fp32 scales there,
+ *     p = dot(a_block, b_block);  acc += p * (sa * sb)
+ * with Triton's default fp contraction making the update one fma.  The block
+ * product p is exact on the E2M1 grid (|p| <= 1152 in steps of 1/4); here it
+ * is summed in double and rounded to float once.  Operands are values
+ * (E2M1 or E4M3, already expanded to float): A [M, K], Bt [N, K]; scale
+ * (row r, block kb) of A at sa[r * sa_r + kb * sa_k], likewise sb. */
+void orc_gemm_promote(const float *A, const float *Bt, const float *sa, int64_t sa_r, int64_t sa_k,
+                      const float *sb, int64_t sb_r, int64_t sb_k, int64_t M, int64_t N, int64_t K,
+                      float *C) {
+    const int64_t nkb = K / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            float acc = 0.0f;
+            for (int64_t kb = 0; kb < nkb; ++kb) {
+                double d = 0.0;
+                for (int64_t k = 32 * kb; k < 32 * kb + 32; ++k) d += (double)A[m * K + k] * (double)Bt[n * K + k];
+                const float p = (float)d;
+                const float s = sa[m * sa_r + kb * sa_k] * sb[n * sb_r + kb * sb_k];
+                acc = fmaf(p, s, acc);
+            }
+            C[m * N + n] = acc;
+        }
 }
 
 /* Number of OpenMP threads this library will use. */

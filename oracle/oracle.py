@@ -24,6 +24,13 @@ Parity pins, per function (all in tests/test_oracle.py unless noted):
                   plus the 0xFEDCBA98 known answer of cuda/test_unpack.c:94
   reference_gemm  integer-grid exact products (bench.py:44-57) and brute
                   force over K on tiny shapes
+  gemm_promote    power-of-two scales on the integer grid against the exact
+                  fp64 product; one and two blocks with any scales against
+                  numpy's float32 products and a single rounding of the exact
+                  fp64 sum (which pins the fma of the update: the unfused
+                  form is shown to differ); IEEE special scales (0, -2, inf,
+                  NaN) on one block; random scales against fp64 within the
+                  summation bound
 """
 
 from __future__ import annotations
@@ -85,6 +92,9 @@ def lib():
         L.orc_fp4x8_to_e4m3x8.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_int64,
                                           ctypes.POINTER(ctypes.c_uint32),
                                           ctypes.POINTER(ctypes.c_uint32)]
+        c_fp = ctypes.POINTER(ctypes.c_float)
+        L.orc_gemm_promote.argtypes = [c_fp, c_fp, c_fp, ctypes.c_int64, ctypes.c_int64, c_fp, ctypes.c_int64,
+                                       ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, c_fp]
         L.orc_num_threads.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -238,6 +248,33 @@ def reference_gemm_wonly(a: np.ndarray, w_pk, w_e8m0, rows=None, cols=None) -> n
         w_pk, w_e8m0 = w_pk[cols], w_e8m0[cols]
     W = dequantize_packed(w_pk, w_e8m0)
     return np.asarray(a, dtype=np.float64) @ W.T
+
+
+def gemm_promote(a_vals: np.ndarray, bt_vals: np.ndarray, sa: np.ndarray, sb: np.ndarray,
+                 sb_transposed: bool = False) -> np.ndarray:
+    """mxfp4_gemm.py:52-63 / 141-150 for fp32 scales of any value:
+    acc = fma(p_kb, sa[m,kb] * sb[n,kb], acc) over the 32-blocks in order
+    (orc_gemm_promote).  a_vals [M, K] and bt_vals [N, K] are operand values
+    (E2M1 or E4M3, as float); sa [M, K/32]; sb [N, K/32], or [K/32, N] when
+    sb_transposed (mxfp4_gemm_fp8's b_scale).  Returns fp32 [M, N]."""
+    A = np.ascontiguousarray(a_vals, dtype=np.float32)
+    B = np.ascontiguousarray(bt_vals, dtype=np.float32)
+    sa = np.ascontiguousarray(sa, dtype=np.float32)
+    sb = np.ascontiguousarray(sb, dtype=np.float32)
+    M, K = A.shape
+    N = B.shape[0]
+    assert B.shape[1] == K and K % 32 == 0 and sa.shape == (M, K // 32)
+    assert sb.shape == ((K // 32, N) if sb_transposed else (N, K // 32))
+    sb_r, sb_k = (1, N) if sb_transposed else (K // 32, 1)
+    out = np.empty((M, N), dtype=np.float32)
+    lib().orc_gemm_promote(_p(A, ctypes.c_float), _p(B, ctypes.c_float), _p(sa, ctypes.c_float), K // 32, 1,
+                           _p(sb, ctypes.c_float), sb_r, sb_k, M, N, K, _p(out, ctypes.c_float))
+    return out
+
+
+def fp4_values(packed: np.ndarray) -> np.ndarray:
+    """Packed E2M1 bytes [rows, K/2] -> float values [rows, K] (fp4.py:20-24)."""
+    return E2M1_VALUES[unpack_fp4(packed)]
 
 
 def max_rel(got: np.ndarray, ref: np.ndarray) -> float:

@@ -100,6 +100,39 @@ def test_batched_quantizer_and_quantizing_gemm_validate_before_launch():
                256, FAKE, 128, FAKE, 256, 256, 256, 256, None) == C.ERR_ARG
 
 
+def test_promotion_entry_points_validate_before_launch():
+    """lsmx_scale_to_e8m0_batch takes 0 .. 4 items with K-major output and an
+    8-byte aligned flag; lsmx_gemm_mx_promote takes packed FP4 or E4M3
+    operands with 16-byte aligned rows and keeps every load offset in 32
+    bits."""
+    items = (C.E8m0Item * 5)()
+    assert _rc("lsmx_scale_to_e8m0_batch", ctypes.addressof(items), 5, None, 0, None) == C.ERR_SHAPE
+    assert _rc("lsmx_scale_to_e8m0_batch", None, 1, None, 0, None) == C.ERR_ARG
+    f = 0x1000
+    items[0] = C.E8m0Item(f, 64, 8, 8, C.E8M0_OUT_KMAJOR, f, 64)
+    assert _rc("lsmx_scale_to_e8m0_batch", ctypes.addressof(items), 1, None, 0, None) == C.ERR_ARG
+    items[0] = C.E8m0Item(f, 64, 6, 6, 0, f, 64)
+    assert _rc("lsmx_scale_to_e8m0_batch", ctypes.addressof(items), 1, None, 0, None) == C.ERR_SHAPE
+    items[0] = C.E8m0Item(f, 64, 8, 8, 0, f + 2, 64)
+    assert _rc("lsmx_scale_to_e8m0_batch", ctypes.addressof(items), 1, None, 0, None) == C.ERR_ALIGN
+    items[0] = C.E8m0Item(f, 64, 8, 8, 0, f, 64)
+    assert _rc("lsmx_scale_to_e8m0_batch", ctypes.addressof(items), 1, f + 4, 0, None) == C.ERR_ALIGN
+
+    def pm(op=C.CODES_PACKED, a=FAKE, lda=128, M=64, N=64, K=256, sa_r=8, c_dtype=C.F32):
+        return _rc("lsmx_gemm_mx_promote", a, lda, FAKE, sa_r, 1, FAKE, 128, FAKE, 8, 1, op, FAKE, c_dtype, N, M, N,
+                   K, None, 0, None)
+    assert pm(op=C.BF16) == C.ERR_DTYPE
+    assert pm(c_dtype=C.E4M3) == C.ERR_DTYPE
+    assert pm(K=192) == C.ERR_SHAPE and "multiple of 128" in C.last_error()
+    assert pm(lda=64) == C.ERR_SHAPE
+    assert pm(op=C.E4M3) == C.ERR_SHAPE       # E4M3 rows are K bytes long
+    assert pm(a=ctypes.c_void_p(0x1008)) == C.ERR_ALIGN
+    assert pm(lda=1 << 24, K=256) == C.ERR_SHAPE and "too long" in C.last_error()
+    assert pm(sa_r=1 << 24) == C.ERR_SHAPE and "2^31" in C.last_error()
+    assert _rc("lsmx_gemm_mx_promote", None, 128, FAKE, 8, 1, FAKE, 128, FAKE, 8, 1, C.CODES_PACKED, FAKE, C.F32,
+               64, 64, 64, 256, None, 0, None) == C.ERR_ARG
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="a GPU is present")
 def test_device_guard_without_gpu():
     assert _rc("lsmx_device_check") == C.ERR_DEVICE

@@ -340,3 +340,100 @@ def test_generator_is_deterministic():
     z = gen.normal(9, (100000,)).astype(np.float64)
     assert abs(z.mean()) < 0.02 and abs(z.std() - 1) < 0.02
     assert sha(gen.normal(1002, (2, 4), std=0.02)) == sha(gen.normal(1002, (2, 4), std=0.02))
+
+
+# ----------------------------------------------------- fp32 promotion GEMM
+def _codes(rng, shape):
+    return rng.integers(0, 16, size=shape, dtype=np.uint8)
+
+
+def test_promote_pow2_scales_integer_grid_is_exact(oracle):
+    # power-of-two scales 2^-1 .. 2^1 on the E2M1 grid: every partial sum is
+    # a multiple of 2^-4 below 2^16, exact in fp32, so the promotion loop
+    # equals the exact fp64 product of the dequantized operands
+    rng = np.random.default_rng(5)
+    M, N, K = 12, 10, 256
+    ca, cb = _codes(rng, (M, K)), _codes(rng, (N, K))
+    ea = rng.integers(126, 129, size=(M, K // 32)).astype(np.uint8)
+    eb = rng.integers(126, 129, size=(N, K // 32)).astype(np.uint8)
+    got = oracle.gemm_promote(oracle.E2M1_VALUES[ca], oracle.E2M1_VALUES[cb], oracle.e8m0_to_scale(ea),
+                              oracle.e8m0_to_scale(eb))
+    want = oracle.reference_gemm_packed(oracle.pack_fp4(ca), ea, oracle.pack_fp4(cb), eb)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+def _one_block_expected(p, sa, sb):
+    # fl(p * fl(sa * sb)) with numpy's float32 multiply for the scale product
+    # and one rounding of the exact fp64 product (p has <= 13 bits, the scale
+    # 24, so the fp64 product is exact)
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = (sa.astype(np.float32)[:, None] * sb.astype(np.float32)[None, :]).astype(np.float32)
+        return (p.astype(np.float64) * s.astype(np.float64)).astype(np.float32)
+
+
+def test_promote_one_block_any_scale(oracle):
+    rng = np.random.default_rng(6)
+    M, N = 9, 7
+    ca, cb = _codes(rng, (M, 32)), _codes(rng, (N, 32))
+    A, B = oracle.E2M1_VALUES[ca], oracle.E2M1_VALUES[cb]
+    sa = (rng.uniform(0.3, 3.0, size=(M, 1))).astype(np.float32)
+    sb = (rng.uniform(0.3, 3.0, size=(N, 1))).astype(np.float32)
+    got = oracle.gemm_promote(A, B, sa, sb)
+    p = A.astype(np.float64) @ B.astype(np.float64).T
+    assert np.array_equal(got, _one_block_expected(p, sa[:, 0], sb[:, 0]))
+
+
+def test_promote_special_scales_follow_ieee(oracle):
+    # scales the E8M0 kernels cannot represent: zero, negative, inf, NaN,
+    # subnormal, non-powers of two
+    rng = np.random.default_rng(7)
+    specials = np.array([0.0, -2.0, np.inf, -np.inf, np.nan, 1e-40, 1.5, 3.0e38], dtype=np.float32)
+    M = N = len(specials)
+    ca, cb = _codes(rng, (M, 32)), _codes(rng, (N, 32))
+    ca[0] = 0  # an all-zero row meets inf and NaN scales
+    A, B = oracle.E2M1_VALUES[ca], oracle.E2M1_VALUES[cb]
+    got = oracle.gemm_promote(A, B, specials[:, None], specials[::-1].copy()[:, None])
+    p = A.astype(np.float64) @ B.astype(np.float64).T
+    want = _one_block_expected(p, specials, specials[::-1].copy())
+    np.testing.assert_array_equal(got, want)  # NaN positions included
+    assert np.isnan(got).any() and np.isinf(got).any() and (got == 0).any()
+
+
+def test_promote_two_blocks_pin_the_fused_update(oracle):
+    # two blocks: acc = fma(p2, s2, fl(p1 * s1)).  With scales in [0.5, 2)
+    # the fp64 sum p2 * s2 + acc1 is exact, so one rounding of it is the fma.
+    # The unfused form fl(fl(p2 * s2) + acc1) differs on some outputs, which
+    # shows the comparison can tell the two apart.
+    rng = np.random.default_rng(8)
+    M, N = 64, 64
+    ca, cb = _codes(rng, (M, 64)), _codes(rng, (N, 64))
+    A, B = oracle.E2M1_VALUES[ca], oracle.E2M1_VALUES[cb]
+    sa = rng.uniform(0.5, 2.0, size=(M, 2)).astype(np.float32)
+    sb = rng.uniform(0.5, 2.0, size=(N, 2)).astype(np.float32)
+    got = oracle.gemm_promote(A, B, sa, sb)
+    A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    p1, p2 = A64[:, :32] @ B64[:, :32].T, A64[:, 32:] @ B64[:, 32:].T
+    acc1 = _one_block_expected(p1, sa[:, 0], sb[:, 0])
+    s2 = (sa[:, 1][:, None] * sb[:, 1][None, :]).astype(np.float32)
+    fused = (p2 * s2.astype(np.float64) + acc1.astype(np.float64)).astype(np.float32)
+    unfused = ((p2 * s2.astype(np.float64)).astype(np.float32) + acc1).astype(np.float32)
+    assert np.array_equal(got, fused)
+    assert not np.array_equal(fused, unfused)
+
+
+def test_promote_random_scales_near_fp64(oracle):
+    rng = np.random.default_rng(9)
+    M, N, K = 16, 12, 512
+    ca, cb = _codes(rng, (M, K)), _codes(rng, (N, K))
+    A, B = oracle.E2M1_VALUES[ca].astype(np.float64), oracle.E2M1_VALUES[cb].astype(np.float64)
+    sa = rng.uniform(-3.0, 3.0, size=(M, K // 32)).astype(np.float32)
+    sb = rng.uniform(-3.0, 3.0, size=(N, K // 32)).astype(np.float32)
+    got = oracle.gemm_promote(A, B, sa, sb)
+    Ad = A * np.repeat(sa.astype(np.float64), 32, axis=1)
+    Bd = B * np.repeat(sb.astype(np.float64), 32, axis=1)
+    want = Ad @ Bd.T
+    bound = (np.abs(Ad) @ np.abs(Bd).T) * (K // 32 + 2) * 2.0 ** -24
+    assert np.all(np.abs(got - want) <= bound)
+    # the transposed layout of mxfp4_gemm_fp8's b_scale gives the same values
+    got_t = oracle.gemm_promote(A, B, sa, np.ascontiguousarray(sb.T), sb_transposed=True)
+    assert np.array_equal(got, got_t)
