@@ -47,6 +47,9 @@ PEAK_FP4_TFLOPS = 10100.0     # MI355X dense MXFP4 MFMA (2.4 GHz)
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+# vector-ALU fp32 operations issued without packed math (this build disables
+# it): 256 CUs x 4 SIMDs x 16 lanes per clock x 2.4 GHz
+PEAK_VALU_GOPS = 39321.6
 NOMINAL_GHZ = 2.4
 
 
@@ -418,8 +421,11 @@ def bench_cfg4_reference_spelling(torch, A, B, apk, bpk, ae8, be8):
             "gemm_call_ratio": round(gemm_ref / gemm_km, 4),
             "roofline": roofline("mfma", "gemm_f4f4_mx16_kernel after the scale regroup", flop / gemm_ref / 1e9,
                                  PEAK_FP4_TFLOPS, "TFLOP/s"),
-            "note": "the GEMM call includes the two fp32 -> K-major E8M0 scale conversions (lsmx_scale_to_e8m0); "
-                    "the step adds the unpacked-code quantizer and pack_fp4 of both operands"}
+            "note": "the GEMM call includes the fp32 -> K-major E8M0 conversion of both scale tensors in one "
+                    "launch (lsmx_scale_to_e8m0_batch, which also flags scales that are not powers of two) and the "
+                    "promotion launch that follows the GEMM and exits at once for the quantizer's power-of-two "
+                    "scales (lsmx_gemm_mx_promote); the step adds the unpacked-code quantizer and pack_fp4 of both "
+                    "operands"}
 
 
 def cpu_cfg4(n):
@@ -661,6 +667,16 @@ def bench_reference_rows(torch, dev, n=4096):
         _time_events(lambda: mg.mxfp4_gemm_fp8(a_f8, bt_f8.t(), a_e8, bt_e8.t())), fl1, PEAK_FP8_TFLOPS)
     row("mxfp4_gemm_packed (f4 x f4)", _time_events(lambda: mg.mxfp4_gemm_packed(a_pk, bt_pk, a_e8, bt_e8)),
         fl1, PEAK_FP4_TFLOPS)
+    # fp32 scales that are not powers of two (the quantizer's times 1.5): the
+    # conversion flags them, and after the fast kernel the promotion kernel
+    # recomputes C with the reference's per-block fp32 arithmetic
+    # (mxfp4_gemm.py:141-150), 2 vector-ALU operations per output per block
+    a_s15, bt_s15 = a_s * 1.5, bt_s * 1.5
+    ms = _time_events(lambda: mg.mxfp4_gemm_packed(a_pk, bt_pk, a_s15, bt_s15), reps=5)
+    ops = 2.0 * n * n * (n // 32)
+    rows.append({"config": f"ref-bench mxfp4_gemm_packed, fp32 scales that are not powers of two (flagged "
+                           f"conversion + fast kernel + promotion kernel), {n}^3", "ms": ms, "tflops": fl1 / ms / 1e9,
+                 "valu_gops": ops / ms / 1e6, "frac_valu": ops / ms / 1e6 / PEAK_VALU_GOPS})
     a1 = torch.randn((n, n), device=dev, generator=g).to(torch.bfloat16)
     a2 = torch.randn((n, n), device=dev, generator=g).to(torch.bfloat16)
     b1 = torch.randn((n, n), device=dev, generator=g).to(torch.bfloat16)

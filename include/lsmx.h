@@ -335,10 +335,11 @@ int lsmx_scale_to_e8m0(const float *s, int64_t rows, int64_t cols, int64_t lds, 
 /* lsmx_scale_to_e8m0 with K-major output for up to 4 fp32 scale tensors in
  * one launch (the A and B scales of one GEMM call: mxfp4_gemm.py:161-174's
  * and :74-87's fp32 scales, regrouped for the fast kernels), and a test for
- * the scales the fast kernels cannot apply: when any scale has no E8M0 form
- * (not a power of two in [2^-127, 2^127]: 1.5, 0, -2, inf, NaN ...) and
- * flag is not NULL, the launch writes epoch to *flag (8-byte aligned device
- * memory); otherwise it leaves *flag as it was.  A caller picks an epoch it
+ * the scales the fast kernels cannot apply: when any scale is neither a
+ * power of two in [2^-127, 2^127] nor a NaN (1.5, 0, -2, inf ...; a NaN
+ * scale is E8M0 0xFF, NaN in every output that uses it, as the reference's
+ * multiply makes it) and flag is not NULL, the launch writes epoch to *flag
+ * (8-byte aligned device memory); otherwise it leaves *flag as it was.  A caller picks an epoch it
  * has never used with that flag, so no earlier content can equal it, and
  * passes flag and epoch to lsmx_gemm_mx_promote after the fast GEMM. */
 typedef struct {

@@ -496,7 +496,8 @@ int lsmx_scale_to_e8m0_batch(const lsmx_e8m0_item *items, int n, uint64_t *flag,
         const int64_t w = ((orows + 63) / 64) * ((blocks / 4 + 15) / 16);
         if (w == 0) continue;  // empty tensors take no workgroup
         if (wgs + w > 0x7FFFFFFF) return fail(LSMX_ERR_SHAPE, "%s: too many workgroups", fn);
-        b.it[b.n] = lsmx::E8m0Item{it.s, orows, blocks / 4, it.lds, (int)tin, it.out, it.ldo};
+        const int vec4 = !tin && aligned(it.s, 16) && it.lds % 4 == 0;
+        b.it[b.n] = lsmx::E8m0Item{it.s, orows, blocks / 4, it.lds, (int)tin, vec4, it.out, it.ldo};
         wgs += w;
         b.end[b.n++] = wgs;
     }

@@ -400,14 +400,18 @@ __global__ __launch_bounds__(256) void scale_to_e8m0_km4_tiled_kernel(const floa
 
 // Up to four fp32 scale tensors -> K-major E8M0 dwords in one launch (the A
 // and B scales of one GEMM call).  A workgroup converts 64 output rows x 16
-// four-block groups of one tensor through a byte tile in LDS: its loads walk
-// the contiguous axis of s (the blocks of a row, or with tin the rows of a
-// block), its stores 64 consecutive dwords of a group.  A scale with no E8M0
-// form becomes 0xFF as above and, with a flag, makes the wave that met it
-// write the caller's epoch there (one store per wave), which the promotion
-// GEMM that follows checks.
+// four-block groups of one tensor through a dword tile in LDS (one padding
+// dword per group row): row-major input with 16-byte rows is read as in
+// scale_to_e8m0_km4_tiled_kernel (four blocks per float4, 256 contiguous
+// bytes per 16 threads); [blocks, rows] input (tin) one float per thread, 64
+// consecutive rows of a block per wave, each lane writing a byte of its own
+// dword.  The stores are 64 consecutive dwords of a group.  A scale with no
+// E8M0 form becomes 0xFF as above and, unless it is a NaN (which E8M0 has,
+// with the same effect on every output that uses it), makes the wave that
+// met it write the caller's epoch to the flag (one store per wave), which
+// the promotion GEMM that follows checks.
 __global__ __launch_bounds__(256) void scale_to_e8m0_batch_kernel(E8m0Batch b) {
-    __shared__ uint32_t tile[16][64];
+    __shared__ uint32_t tile[16][65];
     const int64_t blk = (int64_t)blockIdx.x;
     int k = 0;
     while (k + 1 < b.n && blk >= b.end[k]) ++k;
@@ -416,17 +420,42 @@ __global__ __launch_bounds__(256) void scale_to_e8m0_batch_kernel(E8m0Batch b) {
     const int64_t tiles_o = (it.orows + 63) / 64;
     const int64_t o0 = (local % tiles_o) * 64, g0 = (local / tiles_o) * 16;
     const int t = threadIdx.x;
-    uint8_t *tb = reinterpret_cast<uint8_t *>(tile);
     bool bad = false;
+    if (it.tin) {
+        uint8_t *tb = reinterpret_cast<uint8_t *>(tile);
 #pragma unroll 4
-    for (int i = 0; i < 16; ++i) {
-        const int q = i * 256 + t;
-        const int r = it.tin ? (q & 63) : (q >> 6), c = it.tin ? (q >> 6) : (q & 63);  // out row, block in tile
-        const int64_t o = o0 + r, bk = 4 * g0 + c;
-        if (o < it.orows && bk < 4 * it.groups) {
-            const uint32_t e = f32_scale_e8m0(f2u(it.tin ? it.s[bk * it.lds + o] : it.s[o * it.lds + bk]));
-            bad |= e == 0xFFu;
-            tb[((c >> 2) * 64 + r) * 4 + (c & 3)] = (uint8_t)e;
+        for (int i = 0; i < 16; ++i) {
+            const int q = i * 256 + t, r = q & 63, c = q >> 6;  // out row, block in tile
+            const int64_t o = o0 + r, bk = 4 * g0 + c;
+            if (o < it.orows && bk < 4 * it.groups) {
+                const uint32_t x = f2u(it.s[bk * it.lds + o]), e = f32_scale_e8m0(x);
+                bad |= e == 0xFFu && (x & 0x7FFFFFFFu) <= 0x7F800000u;
+                tb[((c >> 2) * 65 + r) * 4 + (c & 3)] = (uint8_t)e;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = i * 256 + t, r = q >> 4, gi = q & 15;
+            const int64_t o = o0 + r, gr = g0 + gi;
+            if (o < it.orows && gr < it.groups) {
+                uint32_t x[4];
+                if (it.vec4) {
+                    const float4 v = *reinterpret_cast<const float4 *>(it.s + o * it.lds + 4 * gr);
+                    x[0] = f2u(v.x), x[1] = f2u(v.y), x[2] = f2u(v.z), x[3] = f2u(v.w);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[j] = f2u(it.s[o * it.lds + 4 * gr + j]);
+                }
+                uint32_t w = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t e = f32_scale_e8m0(x[j]);
+                    bad |= e == 0xFFu && (x[j] & 0x7FFFFFFFu) <= 0x7F800000u;
+                    w |= e << (8 * j);
+                }
+                tile[gi][r] = w;
+            }
         }
     }
     if (b.flag) {

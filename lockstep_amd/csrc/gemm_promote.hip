@@ -224,7 +224,7 @@ __global__ __launch_bounds__(pm::NT, 2) void gemm_promote_kernel(PromoteArgs g) 
 
 hipError_t launch_gemm_promote(const PromoteArgs &g, bool fp4, hipStream_t s) {
     const int64_t tiles = ((g.M + pm::BM - 1) / pm::BM) * ((g.N + pm::BN - 1) / pm::BN);
-    const dim3 grid((unsigned)min(tiles, (int64_t)512)), blk(pm::NT);
+    const dim3 grid((unsigned)min(tiles, (int64_t)1024)), blk(pm::NT);
 #define LSMX_PM(F, CT) hipLaunchKernelGGL((gemm_promote_kernel<F, CT>), grid, blk, 0, s, g)
     if (fp4) {
         if (g.c_dtype == LSMX_F32) LSMX_PM(true, LSMX_F32);

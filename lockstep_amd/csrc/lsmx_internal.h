@@ -153,6 +153,7 @@ struct E8m0Item {
     const float *s;
     int64_t orows, groups, lds;  // out rows, 4-block groups, stride of s
     int tin;                     // s is [blocks, out rows] (else [out rows, blocks])
+    int vec4;                    // row-major with 16-byte rows: float4 loads
     uint8_t *out;
     int64_t ldo;
 };

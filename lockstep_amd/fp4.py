@@ -22,10 +22,32 @@ along the other axis), and the E8M0 <-> fp32 scale conversions.
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
 from . import _capi as C
+
+# fp32 scale tensors this module returned -- powers of two in [2^-127, 2^127]
+# or NaN by construction -- by id, with the version counter and address they
+# had then.  mxfp4_gemm_packed and mxfp4_gemm_fp8 skip the promotion launch
+# for scales still in that state (an in-place write to the tensor or to any
+# view of it bumps the shared version counter); any other fp32 scales are
+# checked on the device.
+_E8M0_EXACT: dict = {}
+
+
+def _mark_e8m0_exact(s: torch.Tensor) -> torch.Tensor:
+    key = id(s)
+    _E8M0_EXACT[key] = (s._version, s.data_ptr())
+    weakref.finalize(s, _E8M0_EXACT.pop, key, None)
+    return s
+
+
+def e8m0_exact(*scales: torch.Tensor) -> bool:
+    """True when every tensor is an fp32 scale tensor returned by
+    quantize_mxfp4 or e8m0_to_scale and not written since."""
+    return all(_E8M0_EXACT.get(id(s)) == (s._version, s.data_ptr()) for s in scales)
 
 # ---------------------------------------------------------------- E2M1 tables
 # fp4.py:20-34
@@ -99,7 +121,7 @@ def quantize_mxfp4(x: torch.Tensor, block: int = 32):
     C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
            x2.stride(0) if rows > 1 else K, block, codes.data_ptr(), C.CODES_UNPACKED, K,
            scale.data_ptr(), C.SCALE_F32, K // block, C.stream_of(x2))
-    return codes.reshape(*lead, K), scale.reshape(*lead, K // block)
+    return codes.reshape(*lead, K), _mark_e8m0_exact(scale.reshape(*lead, K // block))
 
 
 def quantize_pack_mxfp4(x: torch.Tensor, block: int = 32, scale_layout: str = "rows"):
@@ -265,7 +287,7 @@ def e8m0_to_scale(e8m0: torch.Tensor) -> torch.Tensor:
     2^-127, the fp32 subnormal 0x00400000).  Exact."""
     e = e8m0.to(torch.int32)
     s = torch.where(e == 0, torch.full_like(e, 0x00400000), e << 23).view(torch.float32)
-    return torch.where(e8m0 == 255, torch.full_like(s, float("nan")), s)
+    return _mark_e8m0_exact(torch.where(e8m0 == 255, torch.full_like(s, float("nan")), s))
 
 
 def scale_to_e8m0(scale: torch.Tensor) -> torch.Tensor:

@@ -60,11 +60,13 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
     K-major E8M0 on the device first (fp32 through lsmx_scale_to_e8m0_batch,
     E8M0 bytes through a dword transpose), so every format runs the same
     kernel and gives the same bits.  fp32 scales that are not all powers of
-    two (1.5, 0, -2, inf ...; the quantizer never makes them) have no E8M0
-    form: the conversion flags them and lsmx_gemm_mx_promote then recomputes
-    C with the reference's own promotion arithmetic (mxfp4_gemm.py:141-150),
-    a vector-ALU-bound fallback; with power-of-two scales that launch exits
-    at once.  Returns C = A @ B_T.T [M, N] in out_dtype, fp32 accumulate."""
+    two or NaN (1.5, 0, -2, inf ...; the quantizer never makes them) have no
+    E8M0 form: the conversion flags them and lsmx_gemm_mx_promote then
+    recomputes C with the reference's own promotion arithmetic
+    (mxfp4_gemm.py:141-150), a vector-ALU-bound fallback; with powers of two
+    that launch exits at once, and for scales fp4.quantize_mxfp4 returned
+    (and nobody wrote since) it is not made.  Returns C = A @ B_T.T [M, N]
+    in out_dtype, fp32 accumulate."""
     M, Kh = a_pk.shape
     N, Kh2 = bt_pk.shape
     K = Kh * 2
@@ -96,10 +98,12 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
         promote = None
     else:
         # the reference's spelling (fp32 scales from quantize_mxfp4)
+        exact = _fp4.e8m0_exact(a_scale, b_scale)
         sa32, sb32 = _f32_rows(a_scale), _f32_rows(b_scale)
-        (a_scale, b_scale), flag, epoch = _e8m0_kmajor_flagged([(sa32, M, False), (sb32, N, False)], K // 32)
+        (a_scale, b_scale), flag, epoch = _e8m0_kmajor_flagged([(sa32, M, False), (sb32, N, False)], K // 32,
+                                                               flagged=not exact)
         fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
-        promote = (sa32, False, sb32, False, flag, epoch)
+        promote = None if exact else (sa32, False, sb32, False, flag, epoch)
     lda, ldb = a_pk.stride(0) if M > 1 else Kh, bt_pk.stride(0) if N > 1 else Kh
     C.call("lsmx_gemm_f4f4", a_pk.data_ptr(), lda, a_scale.data_ptr(), lsa, bt_pk.data_ptr(), ldb,
            b_scale.data_ptr(), lsb, fmt, c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
@@ -278,15 +282,16 @@ def _ld(s: torch.Tensor) -> int:
     return s.stride(0) if s.shape[0] > 1 else s.shape[1]
 
 
-def _e8m0_kmajor_flagged(scales, nkb: int):
+def _e8m0_kmajor_flagged(scales, nkb: int, flagged: bool = True):
     """fp32 block scales -> K-major E8M0 bytes [nkb//4, rows, 4] for the fast
     kernels, all tensors in one launch (lsmx_scale_to_e8m0_batch).  scales:
     (s, rows, transposed) with s [rows, nkb], or [nkb, rows] when transposed.
-    Returns (outputs, flag, epoch): the launch writes epoch to the device word
-    flag when some scale has no E8M0 form, which lsmx_gemm_mx_promote checks."""
+    Returns (outputs, flag, epoch): when flagged, the launch writes epoch to
+    the device word flag if some scale is neither a power of two nor a NaN,
+    which lsmx_gemm_mx_promote checks (flag None otherwise)."""
     dev = scales[0][0].device
-    flag = torch.empty(1, dtype=torch.int64, device=dev)
-    epoch = C.next_epoch()
+    flag = torch.empty(1, dtype=torch.int64, device=dev) if flagged else None
+    epoch = C.next_epoch() if flagged else 0
     items = (C.E8m0Item * len(scales))()
     outs = []
     for k, (s, rows, tr) in enumerate(scales):
@@ -294,7 +299,8 @@ def _e8m0_kmajor_flagged(scales, nkb: int):
         items[k] = C.E8m0Item(s.data_ptr(), s.shape[0], s.shape[1], _ld(s), C.E8M0_IN_T if tr else 0,
                               out.data_ptr(), rows)
         outs.append(out)
-    C.call("lsmx_scale_to_e8m0_batch", items, len(scales), flag.data_ptr(), epoch, C.stream_of(flag))
+    C.call("lsmx_scale_to_e8m0_batch", items, len(scales), flag.data_ptr() if flagged else None, epoch,
+           C.stream_of(outs[0]))
     return outs, flag, epoch
 
 
@@ -369,9 +375,11 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
         sa = _e8m0_kmajor(a_scale, M, K // 32, transposed=False)
         sb = _e8m0_kmajor(b_scale, N, K // 32, transposed=True)
     else:
+        exact = _fp4.e8m0_exact(a_scale, b_scale)
         sa32, sb32 = _f32_rows(a_scale), _f32_rows(b_scale)
-        (sa, sb), flag, epoch = _e8m0_kmajor_flagged([(sa32, M, False), (sb32, N, True)], K // 32)
-        promote = (sa32, False, sb32, True, flag, epoch)
+        (sa, sb), flag, epoch = _e8m0_kmajor_flagged([(sa32, M, False), (sb32, N, True)], K // 32,
+                                                     flagged=not exact)
+        promote = None if exact else (sa32, False, sb32, True, flag, epoch)
     fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
     lda, ldb = a.stride(0) if M > 1 else K, bt.stride(0) if N > 1 else K
     C.call("lsmx_gemm_f8f8", a.data_ptr(), lda, sa.data_ptr(), lsa, bt.data_ptr(), ldb, sb.data_ptr(), lsb, fmt,

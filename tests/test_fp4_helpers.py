@@ -111,3 +111,22 @@ def test_dual_slot_split():
         c2 = torch.tensor([-144.0 * k, 144.0 * k, -7.0], dtype=torch.float64)
         g1, g2 = dual_gemm.unpack_dual(c1 + c2 * 2.0 ** s, s)
         assert torch.equal(g1, c1) and torch.equal(g2, c2)
+
+
+def test_e8m0_exact_tracks_the_module_s_own_scales():
+    """fp4.e8m0_exact: true for fp32 scales e8m0_to_scale returned, false for
+    copies, views and after an in-place write (which bumps the version
+    counter views share), so mxfp4_gemm_packed skips its promotion launch
+    only for scales that are powers of two or NaN by construction."""
+    import torch
+    from lockstep_amd import fp4
+    s = fp4.e8m0_to_scale(torch.tensor([[127, 0, 255, 130]], dtype=torch.uint8))
+    assert fp4.e8m0_exact(s)
+    assert not fp4.e8m0_exact(s.clone()) and not fp4.e8m0_exact(s.view(1, 4)) and not fp4.e8m0_exact(torch.ones(1, 4))
+    v = s.view(4)
+    v[1] = 1.5
+    assert not fp4.e8m0_exact(s)
+    t = fp4.e8m0_to_scale(torch.tensor([[127]], dtype=torch.uint8))
+    key = id(t)
+    del t
+    assert key not in fp4._E8M0_EXACT

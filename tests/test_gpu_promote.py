@@ -89,11 +89,43 @@ def test_power_of_two_scales_keep_the_fast_kernel_bits(dev, mods, oracle):
     w = torch.from_numpy(gen.normal(44, (N, K), std=0.02)).to(dev)
     xc, xs = fp4.quantize_mxfp4(x)
     wc, ws = fp4.quantize_mxfp4(w)
+    assert fp4.e8m0_exact(xs, ws)   # the quantizer's own scales: no promotion launch at all
     ref_spelling = mg.mxfp4_gemm_packed(fp4.pack_fp4(xc), fp4.pack_fp4(wc), xs, ws)
     xk = fp4.quantize_pack_mxfp4(x, scale_layout="kmajor")
     wk = fp4.quantize_pack_mxfp4(w, scale_layout="kmajor")
     fast = mg.mxfp4_gemm_packed(xk[0], wk[0], xk[1], wk[1])
     assert torch.equal(ref_spelling, fast)
+    # copies of them are checked on the device: the flag stays clear and the
+    # promotion launch exits
+    xs2, ws2 = xs.clone(), ws.clone()
+    assert not fp4.e8m0_exact(xs2, ws2)
+    assert torch.equal(mg.mxfp4_gemm_packed(fp4.pack_fp4(xc), fp4.pack_fp4(wc), xs2, ws2), fast)
+    # an in-place write to the quantizer's tensor takes it off the fast list
+    xs[5, 2] = 1.5
+    assert not fp4.e8m0_exact(xs)
+    got = mg.mxfp4_gemm_packed(fp4.pack_fp4(xc), fp4.pack_fp4(wc), xs, ws, out_dtype=torch.float32)
+    _same(got, oracle.gemm_promote(oracle.E2M1_VALUES[xc.cpu().numpy()], oracle.E2M1_VALUES[wc.cpu().numpy()],
+                                   xs.cpu().numpy(), ws.cpu().numpy()))
+
+
+def test_nan_scales_stay_on_the_fast_kernel(dev, mods, oracle):
+    """A NaN fp32 scale is E8M0 NaN: it does not set the flag, and the output
+    is the E8M0 call's (NaN in every output that uses the scale, as the
+    reference's multiply makes it; the others unchanged)."""
+    C, fp4, mg = mods
+    M, N, K = 256, 256, 512
+    x = torch.from_numpy(gen.normal(45, (M, K))).to(dev)
+    w = torch.from_numpy(gen.normal(46, (N, K), std=0.02)).to(dev)
+    xk = fp4.quantize_pack_mxfp4(x)
+    wk = fp4.quantize_pack_mxfp4(w)
+    ea, eb = xk[1].clone(), wk[1].clone()
+    ea[3, 1] = 255
+    eb[9, 4] = 255
+    want = mg.mxfp4_gemm_packed(xk[0], wk[0], ea, eb, out_dtype=torch.float32)
+    sa, sb = fp4.e8m0_to_scale(ea).clone(), fp4.e8m0_to_scale(eb).clone()   # untagged copies
+    got = mg.mxfp4_gemm_packed(xk[0], wk[0], sa, sb, out_dtype=torch.float32)
+    assert bool(got[3].isnan().all()) and bool(got[:, 9].isnan().all())
+    np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy())
 
 
 def test_special_scales_follow_ieee(dev, mods, oracle):
@@ -194,7 +226,7 @@ def test_scale_batch_matches_single_conversions_and_flags(dev, mods, oracle, bad
     """lsmx_scale_to_e8m0_batch over three tensors (row-major and [blocks,
     rows] inputs, partial 64 x 16 tiles, one empty) writes the bytes
     lsmx_scale_to_e8m0 writes, and writes its epoch to the flag exactly when
-    a scale has no E8M0 form."""
+    a scale is neither a power of two nor a NaN."""
     C, fp4, mg = mods
     rng = np.random.default_rng(21 + bad)
     shapes = [(300, 40, False), (72, 300, True), (0, 8, False)]
@@ -202,6 +234,8 @@ def test_scale_batch_matches_single_conversions_and_flags(dev, mods, oracle, bad
     keep, outs, refs = [], [], []
     for k, (r, cl, tin) in enumerate(shapes):
         s = np.ldexp(np.ones((r, cl)), rng.integers(-127, 128, size=(r, cl))).astype(np.float32)
+        if r and cl:
+            s[2, 3] = np.nan          # E8M0 has NaN: never flagged
         if bad and k == 1:
             s[17, 5] = 1.5
         x = torch.from_numpy(s).to(dev)
