@@ -1311,6 +1311,272 @@ static bool decode_ok(const GemmArgs &g) {
     return g.K % dk::SLICE_K == 0 && (reinterpret_cast<uintptr_t>(g.sb) & 15) == 0 && g.ld_sb % 16 == 0;
 }
 
+// ------------------------------------------------------------------ mid M
+// 17 to 64 activation rows per batch: the decode kernel's weight layout, with
+// the activations streamed instead of held.
+//   - a workgroup owns the weight rows the decode kernel would give it (the
+//     weight spread evenly over the CUs, at most 64 rows, four 16-row MFMA
+//     tiles) and the whole K: its 8 waves split each 4096-deep pass into
+//     512-deep slices, each wave's slice of every row loaded once into LDS
+//     (the decode kernel's 4-row, 256-byte direct-to-LDS loads and chunk
+//     swizzle) together with its 16 E8M0 scale bytes per row;
+//   - the activation rows are processed in groups of 64 (4 MFMA tiles; the
+//     dual form's 2M virtual rows can make two): for each 32-deep K-step of
+//     its slice a wave loads the group's fragments row-contiguous (lane l:
+//     16-byte piece l%4 of row l/4, so a quarter-wave touches 4 rows, not
+//     16) in pairs of steps (both halves of each 128-byte line together), a
+//     pair or two ahead, moves them to the MFMA layout with ds_bpermute and
+//     reads the step's weight code words one step ahead of its 16
+//     independent v_mfma_f32_16x16x32_bf16, dequantizing them just before
+//     (v_cvt_scalef32_pk_bf16_fp4, exact); with one pass (K <= 4096) the
+//     weight slice stays in LDS for every group;
+//   - the 8 waves' partial sums of a group meet in a separate 32 KiB LDS
+//     buffer, one activation tile at a time, and are added in wave order.
+// No partial tiles go to memory and there is no second launch (the split-K
+// ring's cost at these shapes).  The summation order of an output element
+// depends on K only, so single and dual launches of the same M give
+// identical bits.
+namespace mk {
+constexpr int NW = 8, NT = 64 * NW;
+constexpr int SLICE_K = 512, PASS_K = NW * SLICE_K, ROW_B = SLICE_K / 2, STEPS = SLICE_K / 32;
+constexpr int R = 64, TN = R / 16, XW = R / 4;   // weight rows (at most), 16-row tiles, 4-row loads
+constexpr int MT = 4, GROUP = 16 * MT;           // activation tiles per group, rows per group
+}  // namespace mk
+
+template <int CT>
+__global__ __launch_bounds__(mk::NT, 1) void gemm_bf16f4_midm_kernel(GemmArgs g) {
+    using namespace mk;
+    __shared__ __attribute__((aligned(16))) uint8_t sW[NW][R * ROW_B];   // 128 KiB
+    __shared__ __attribute__((aligned(16))) float red[NW][TN * 256];      // 32 KiB
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n16 = lane & 15, q = lane >> 4;
+    const bool dual = g.a1 != nullptr;
+    const int64_t VM = dual ? 2 * g.M : g.M;
+    const int64_t n0 = (int64_t)blockIdx.x * g.rows_wg;
+    const int64_t nend = min(n0 + g.rows_wg, g.N);   // rows past nend read zeros
+    const bool one_pass = g.K <= PASS_K;
+
+    // scale rows of this lane's weight rows (rows past nend repeat the last one)
+    const uint8_t *srow[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+        srow[t] = reinterpret_cast<const uint8_t *>(g.sb) + min(n0 + 16 * t + n16, nend - 1) * g.ld_sb;
+    // weight load j covers rows 4j .. 4j + 3: lane l -> row 4j + l/16, LDS
+    // chunk l%16 holding source chunk (l%16) ^ (row & 15)
+    uint32_t w_off[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + (lane >> 4);
+        w_off[j] = (uint32_t)((lane >> 4) * g.ldb + 16 * ((lane & 15) ^ (r & 15)));
+    }
+    u32x4 sv[TN];
+    // Workgroup b walks the steps of its slices starting at 4 (b mod 4): the
+    // activation rows are 8 KiB apart, so at any moment the bytes all the
+    // workgroups read of them would otherwise fall in the same few L2
+    // channels.  Step s reads K-step (s + rot) mod 16 of the slice; the
+    // E8M0 dword of a step is then dword (s/4 + rq) mod 4 of its vector.
+    const int rq = (int)(blockIdx.x & 3), rot = 4 * rq;
+    // byte address of the lane that loaded this lane's MFMA piece
+    const int src4 = 4 * (4 * n16 + q);
+
+#pragma nounroll
+    for (int64_t vg = 0; vg < VM; vg += GROUP) {
+        // Activation fragments are loaded row-contiguous -- lane l reads the
+        // 16-byte piece l%4 of row l/4 of the tile's 64-byte step segment, so
+        // a quarter-wave touches 4 rows instead of 16 -- and moved to the MFMA
+        // layout (lane (n16, q): row n16, piece q) with ds_bpermute.  Rows
+        // past VM repeat the last one; their outputs are not stored.
+        const uint8_t *arow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int64_t v = min(vg + 16 * mt + (lane >> 2), VM - 1);
+            const bool second = dual && v >= g.M;
+            arow[mt] = (second ? g.a1 : g.a) + (second ? v - g.M : v) * g.lda * 2 + (lane & 3) * 16;
+        }
+        v4f acc[MT][TN];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < TN; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#pragma nounroll
+        for (int64_t kp = 0; kp < g.K; kp += PASS_K) {
+            const int64_t k0 = kp + (int64_t)wave * SLICE_K;   // this wave's slice
+            const bool live = k0 < g.K;                         // K % 512 == 0: whole slices
+            const bool load_w = vg == 0 || !one_pass;
+            // every wave is done with the LDS slice it is about to overwrite
+            if (load_w && kp > 0) __syncthreads();
+            if (!live) continue;
+            // The scales and the weight slice (when not already in LDS),
+            // then the first two steps' activation fragments: asm loads, all
+            // counted by the explicit waits below, in issue order, so the
+            // wait for step 0's fragments also covers the weights.
+            if (load_w) {
+#pragma unroll
+                for (int t = 0; t < TN; ++t) sv[t] = gload_x4(srow[t] + k0 / 32);
+#pragma unroll
+                for (int j = 0; j < XW; ++j) {
+                    const int64_t r0 = n0 + 4 * j, left = nend - r0;
+                    const uint64_t bytes = left > 0 ? (uint64_t)((left - 1) * g.ldb + (g.K - k0) / 2) : 0;
+                    dma_x4(w_off[j & 3], buf_rsrc(g.b + r0 * g.ldb + k0 / 2, bytes), lds_u32(&sW[wave][0]) + j * 1024);
+                }
+            }
+            // Fragments of steps s and s + 1 (s even) are loaded back to back
+            // per tile, so the two 64-byte halves of each 128-byte line are
+            // requested together (one line fill); the next pair is issued at
+            // the start of an even step, a pair ahead.
+            u32x4 af[4][MT];
+            auto fetch2 = [&](int s) __attribute__((always_inline)) {
+                const uint32_t off0 = (uint32_t)(k0 * 2) + 64u * (uint32_t)((s + rot) & (STEPS - 1));
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    af[s % 4][mt] = gload_x4(arow[mt] + off0);
+                    af[(s + 1) % 4][mt] = gload_x4(arow[mt] + off0 + 64);
+                }
+            };
+            fetch2(0);
+            // A step's operands (the permuted activation fragments ab and
+            // the dequantized weight fragments wf) are prepared one step
+            // ahead, so their LDS latencies overlap the previous step's
+            // MFMAs.  wait_for(s): step s's fragments have landed; what may
+            // still be in flight is what was issued after step s's last one
+            // (issued = pairs fetched up to and including step cur).
+            auto wait_for = [&](int s, int cur) __attribute__((always_inline)) {
+                // first step of the newest pair issued: two pairs in the
+                // prologue, then pair s + 3 at each odd step s
+                const int last = min(cur % 2 ? cur + 3 : cur + 2, STEPS - 2);
+                const int ahead = (s % 2 == 0) ? 1 + (last - s) / 2 * 2 * MT : (last - (s - 1)) / 2 * 2 * MT;
+                __builtin_amdgcn_sched_barrier(0);
+                if (ahead == 4 * MT + 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * MT + 1) : "memory");
+                else if (ahead == 2 * MT + 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * MT + 1) : "memory");
+                else if (ahead == 4 * MT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * MT) : "memory");
+                else if (ahead == 2 * MT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * MT) : "memory");
+                else if (ahead == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            auto prep = [&](int s, u32x4 (&ab)[MT], uint32_t (&pc)[TN]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    asm volatile("" : "+v"(af[s % 4][mt]));
+                    const u32x4 v = af[s % 4][mt];
+                    ab[mt] = u32x4{(uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.x),
+                                   (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.y),
+                                   (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.z),
+                                   (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.w)};
+                }
+                const int se = (s + rot) & (STEPS - 1);
+                // the step's four weight code words (8 codes per lane each)
+#pragma unroll
+                for (int t = 0; t < TN; ++t)
+                    pc[t] = *reinterpret_cast<const uint32_t *>(&sW[wave][(16 * t + n16) * ROW_B + 16 * (se ^ n16) + 4 * q]);
+            };
+            // step 0: its pair and the next one in flight
+            fetch2(2);
+            wait_for(0, 0);
+            if (load_w) {
+#pragma unroll
+                for (int t = 0; t < TN; ++t) {
+                    asm volatile("" : "+v"(sv[t]));
+                    // rotate the dwords so that dword s/4 holds step s's scales
+                    const u32x4 v = sv[t];
+                    sv[t] = rq == 0 ? v : rq == 1 ? u32x4{v.y, v.z, v.w, v.x}
+                                        : rq == 2 ? u32x4{v.z, v.w, v.x, v.y} : u32x4{v.w, v.x, v.y, v.z};
+                }
+            }
+            u32x4 ab[2][MT];
+            uint32_t pc[2][TN];
+            prep(0, ab[0], pc[0]);
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                // the pair after next, issued at the start of an odd step
+                if (s % 2 == 1 && s + 3 < STEPS) fetch2(s + 3);
+                if (s + 1 < STEPS) {
+                    wait_for(s + 1, s);
+                    prep(s + 1, ab[(s + 1) % 2], pc[(s + 1) % 2]);
+                }
+                // dequantize the step's weight fragments (exact, block scale applied)
+                v8bf wf[TN];
+#pragma unroll
+                for (int t = 0; t < TN; ++t) {
+                    const uint32_t p = pc[s % 2][t];
+                    const float sc = e8m0_scale_nb((sv[t][s >> 2] >> (8 * (s & 3))) & 0xFFu);
+                    const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 0);
+                    const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 1);
+                    const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 2);
+                    const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 3);
+                    wf[t] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int t = 0; t < TN; ++t)
+                        acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(v8bf, ab[s % 2][mt]), wf[t], acc[mt][t], 0, 0, 0);
+            }
+        }
+
+        // acc[mt][t][r] = D[4q + r][n16] of the 16 x 16 tile (rows: activation
+        // rows vg + 16 mt .., columns: weight rows 16 t ..); one activation
+        // tile at a time, the 8 waves' partial sums are added in wave order
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[wave][t * 256 + r * 64 + lane] = acc[mt][t][r];
+            __syncthreads();
+            for (int o = threadIdx.x; o < TN * 256; o += NT) {
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) v += red[w][o];
+                const int t = o >> 8, e = o & 255, r = e >> 6, l = e & 63;
+                const int64_t vr = vg + 16 * mt + 4 * (l >> 4) + r, n = n0 + 16 * t + (l & 15);
+                if (vr < VM && n < nend) {
+                    const bool second = dual && vr >= g.M;
+                    store_cw<CT>(second ? g.c1 : g.c, (second ? vr - g.M : vr) * g.ldc + n, v);
+                }
+            }
+        }
+    }
+}
+
+template <int CT>
+static void launch_midm_ct(GemmArgs g, hipStream_t s) {
+    const int64_t cus = num_cus_w(), per = (g.N + cus - 1) / cus, rows = (per + 3) / 4 * 4;
+    g.rows_wg = (int)(rows > mk::R ? mk::R : rows < 16 ? 16 : rows);
+    const dim3 grid((unsigned)((g.N + g.rows_wg - 1) / g.rows_wg)), blk(mk::NT);
+    hipLaunchKernelGGL((gemm_bf16f4_midm_kernel<CT>), grid, blk, 0, s, g);
+}
+
+static hipError_t launch_midm(const GemmArgs &g, hipStream_t s) {
+    if (g.c_dtype == LSMX_F32) launch_midm_ct<LSMX_F32>(g, s);
+    else if (g.c_dtype == LSMX_BF16) launch_midm_ct<LSMX_BF16>(g, s);
+    else launch_midm_ct<LSMX_F16>(g, s);
+    return hipGetLastError();
+}
+
+// Per-batch rows the mid-M kernel takes (above the decode kernel's).  Up to
+// 64 it beats the skinny and split-K kernels at cfg3's weight (M = 32: 20.3
+// against 26.3 us, M = 64: 21.0 against 27.1, the dual form of M = 64: 33.5
+// against 38.9); at M = 128 the activation stream through each CU's vector
+// memory path makes it slower than split-K (33.5 against 29.5).
+constexpr int64_t kMidMaxM = 64;
+// The shape test (M, N, K only, so that the split-K workspace query agrees):
+// whole 512-deep K slices, the weight spread as the decode kernel spreads it
+// (at most 64 rows per workgroup) over at least one workgroup per CU.
+static bool midm_shape(int64_t M, int64_t N, int64_t K) {
+    const int64_t cus = num_cus_w();
+    return M > kDecodeMaxM && M <= kMidMaxM && K % mk::SLICE_K == 0 && N >= 16 * cus && (N + cus - 1) / cus <= mk::R;
+}
+// and E8M0 byte scales in 16-byte aligned rows (the decode kernel's scale loads)
+static bool midm_ok(const GemmArgs &g) {
+    return g.scale_fmt == LSMX_SCALE_E8M0 && decode_ok(g) && midm_shape(g.M, g.N, g.K);
+}
+
 // ------------------------------------------------------------------ GEMV
 // For one or two activation rows per batch (decode) the whole cost is reading
 // W once, and the matrix cores have almost nothing to do.  This kernel reads
@@ -1613,7 +1879,7 @@ struct SplitPlan {
 };
 static SplitPlan splitk_plan(int64_t M, int64_t N, int64_t K) {
     SplitPlan best{1, 256};
-    if (M <= kSkinnyMaxM) return best;  // the GEMV and skinny kernels own these
+    if (M <= kSkinnyMaxM || midm_shape(M, N, K)) return best;  // the GEMV, decode, mid-M and skinny kernels own these
     const int64_t mt = (M + 127) / 128, cus = num_cus_w();
     if (2 * mt * ((N + 255) / 256) > cus) return best;  // whole-K tiles fill half of the CUs
     int64_t best_wg = 0, best_bytes = 0;
@@ -1715,6 +1981,7 @@ hipError_t launch_gemm_bf16f4(const GemmArgs &g, hipStream_t s) {
     // test depends on M and K only, so single and dual launches agree)
     if (g.M <= kGemvMaxM && 2 * g.M * g.K * 2 <= kGemvMaxLds) return launch_gemv(g, s);
     if (g.M <= kDecodeMaxM && decode_ok(g)) return launch_decode(g, s);
+    if (midm_ok(g)) return launch_midm(g, s);
     if (g.M <= kSkinnyMaxM && (g.a1 ? 2 * g.M : g.M) <= 128) return launch_skinny(g, s);
     if (g.ws && ring_ok(g)) {
         const SplitPlan p = splitk_plan(g.M, g.N, g.K);

@@ -170,6 +170,59 @@ def test_weight_only_decode_shapes(dev, mods, oracle, M, N, K):
     assert torch.equal(c1, mg.mxfp4_gemm_bf16(a1, wpk, we8, out_dtype=torch.float32))
 
 
+@pytest.mark.parametrize("M,N,K", [(17, 4096, 512), (32, 5000, 4608), (48, 14336, 8192), (64, 14336, 4096),
+                                   (40, 16384, 1024)])
+def test_weight_only_mid_m_shapes(dev, mods, oracle, M, N, K):
+    """17 <= M <= 64 against 16 .. 64 weight rows per CU with K % 512 == 0
+    runs the mid-M kernel (no split-K workspace is asked for): activation
+    groups of 64 rows (the dual forms of M = 48 and 64 have two; with
+    K = 8192 each group reloads its weight slices), a second pass with one
+    live slice (K = 4608), two live waves (K = 1024), ragged weight rows.
+    fp32 output vs the fp64 oracle; E8M0 bytes and fp32 powers of two give
+    the same bits; the dual form gives the single form's bits for both
+    batches; bf16 and fp16 outputs are the fp32 result rounded."""
+    from lockstep_amd import _capi as C
+    fp4, mg, dg, _ = mods
+    assert C.load().lsmx_gemm_bf16f4_workspace(M, N, K, 0) == 0
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N + K)
+    a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    a1 = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    codes, s32 = fp4.quantize_mxfp4(w)
+    wpk = fp4.pack_fp4(codes)
+    we8 = fp4.scale_to_e8m0(s32)
+    c = mg.mxfp4_gemm_bf16(a, wpk, we8, out_dtype=torch.float32)
+    ref = oracle.reference_gemm_wonly(a.float().cpu().numpy(), wpk.cpu().numpy(), we8.cpu().numpy())
+    assert oracle.max_rel(c.cpu().numpy(), ref) <= 1e-5
+    assert torch.equal(mg.mxfp4_gemm_bf16(a, wpk, s32, out_dtype=torch.float32), c)
+    c0, c1 = dg.dual_mxfp4(a, a1, wpk, we8, out_dtype=torch.float32)
+    assert torch.equal(c0, c)
+    assert torch.equal(c1, mg.mxfp4_gemm_bf16(a1, wpk, we8, out_dtype=torch.float32))
+    for dt in (torch.bfloat16, torch.float16):
+        assert torch.equal(mg.mxfp4_gemm_bf16(a, wpk, we8, out_dtype=dt), c.to(dt))
+
+
+def test_weight_only_mid_m_special_scale_bytes(dev, mods, oracle):
+    """E8M0 bytes 0 (2^-127) and 255 (NaN) in the mid-M kernel: the NaN
+    byte's column is NaN, the others match the oracle."""
+    fp4, mg, _, _ = mods
+    M, N, K = 40, 14336, 4096
+    g = torch.Generator(device=dev).manual_seed(78)
+    a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev, generator=g) * 0.02
+    wpk, we8 = fp4.quantize_pack_mxfp4(w)
+    bad = we8.clone()
+    bad[7, 5] = 255
+    bad[9000, 31] = 0
+    c = mg.mxfp4_gemm_bf16(a, wpk, bad, out_dtype=torch.float32).cpu().numpy()
+    assert np.isnan(c[:, 7]).all()
+    keep = np.ones(N, dtype=bool)
+    keep[7] = False
+    ref = oracle.reference_gemm_wonly(a.float().cpu().numpy(), wpk.cpu().numpy(), bad.cpu().numpy())
+    assert not np.isnan(c[:, keep]).any()
+    assert oracle.max_rel(c[:, keep], ref[:, keep]) <= 1e-5
+
+
 def test_weight_only_decode_nan_scale_byte(dev, mods, oracle):
     """An E8M0 byte 255 (NaN) in one block of a weight row makes that output
     column NaN and leaves the others as the oracle computes them (the decode
