@@ -484,14 +484,10 @@ LSMX_DEV void q2_tile(const T *__restrict__ x, int64_t R, int64_t C, int64_t ldx
     const int v = lane & 15, g = lane >> 4;
     const int rl = 32 * w + 8 * g;                       // first tile row of this lane
 
-    // plain loads: with non-temporal ones this kernel's mix of 2 bytes read
-    // and 1.06 written per element streamed at 4.6 against 5.5 TB/s (cfg5's
-    // batched x, w1, w2: 33.5 against 28.1 us; a bare streaming kernel with
-    // the same bytes measures 4.8 against 5.5 TB/s the same way)
     u32x4 raw[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        raw[i] = *reinterpret_cast<const u32x4 *>(x + (r0 + rl + i) * ldx + c0 + 8 * v);
+        raw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x + (r0 + rl + i) * ldx + c0 + 8 * v));
 
     uint32_t am[8], cmx[4];
     const uint32_t top = q2_maxima<T>(raw, am, cmx);
