@@ -46,8 +46,12 @@ def _mark_e8m0_exact(s: torch.Tensor) -> torch.Tensor:
 
 def e8m0_exact(*scales: torch.Tensor) -> bool:
     """True when every tensor is an fp32 scale tensor returned by
-    quantize_mxfp4 or e8m0_to_scale and not written since."""
-    return all(_E8M0_EXACT.get(id(s)) == (s._version, s.data_ptr()) for s in scales)
+    quantize_mxfp4 or e8m0_to_scale, or a view of one, and neither has been
+    written since (views share the version counter of their base)."""
+    def known(s):
+        b = s._base if s._base is not None else s
+        return _E8M0_EXACT.get(id(b)) == (b._version, b.data_ptr())
+    return all(known(s) for s in scales)
 
 # ---------------------------------------------------------------- E2M1 tables
 # fp4.py:20-34

@@ -114,18 +114,19 @@ def test_dual_slot_split():
 
 
 def test_e8m0_exact_tracks_the_module_s_own_scales():
-    """fp4.e8m0_exact: true for fp32 scales e8m0_to_scale returned, false for
-    copies, views and after an in-place write (which bumps the version
-    counter views share), so mxfp4_gemm_packed skips its promotion launch
-    only for scales that are powers of two or NaN by construction."""
+    """fp4.e8m0_exact: true for fp32 scales e8m0_to_scale returned and views
+    of them, false for copies and after an in-place write through any view
+    (which bumps the version counter views share), so mxfp4_gemm_packed skips
+    its promotion launch only for scales that are powers of two or NaN by
+    construction."""
     import torch
     from lockstep_amd import fp4
-    s = fp4.e8m0_to_scale(torch.tensor([[127, 0, 255, 130]], dtype=torch.uint8))
-    assert fp4.e8m0_exact(s)
-    assert not fp4.e8m0_exact(s.clone()) and not fp4.e8m0_exact(s.view(1, 4)) and not fp4.e8m0_exact(torch.ones(1, 4))
-    v = s.view(4)
+    s = fp4.e8m0_to_scale(torch.tensor([[127, 0, 255, 130], [1, 2, 3, 4]], dtype=torch.uint8))
+    assert fp4.e8m0_exact(s) and fp4.e8m0_exact(s.t()) and fp4.e8m0_exact(s.view(8)[1:])
+    assert not fp4.e8m0_exact(s.clone()) and not fp4.e8m0_exact(s.t().contiguous()) and not fp4.e8m0_exact(torch.ones(2, 4))
+    v = s.view(8)
     v[1] = 1.5
-    assert not fp4.e8m0_exact(s)
+    assert not fp4.e8m0_exact(s) and not fp4.e8m0_exact(v)
     t = fp4.e8m0_to_scale(torch.tensor([[127]], dtype=torch.uint8))
     key = id(t)
     del t
