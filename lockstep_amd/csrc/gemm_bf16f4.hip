@@ -1337,17 +1337,36 @@ static bool decode_ok(const GemmArgs &g) {
 // depends on K only, so single and dual launches of the same M give
 // identical bits.
 namespace mk {
-constexpr int NW = 8, NT = 64 * NW;
-constexpr int SLICE_K = 512, PASS_K = NW * SLICE_K, ROW_B = SLICE_K / 2, STEPS = SLICE_K / 32;
-constexpr int R = 64, TN = R / 16, XW = R / 4;   // weight rows (at most), 16-row tiles, 4-row loads
+constexpr int PASS_K = 4096;                     // K per pass (all waves' slices)
+constexpr int R = 64, TN = R / 16;               // weight rows (at most), 16-row MFMA tiles
 constexpr int MT = 4, GROUP = 16 * MT;           // activation tiles per group, rows per group
 }  // namespace mk
 
-template <int CT>
-__global__ __launch_bounds__(mk::NT, 1) void gemm_bf16f4_midm_kernel(GemmArgs g) {
+template <int I, int N, typename F>
+LSMX_DEV void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(SlotC<I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+template <int N>
+LSMX_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// NW waves (each a PASS_K / NW deep slice of K), activation step pairs
+// loaded PD pairs ahead of the pair in use.
+template <int NW, int PD, int CT>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_bf16f4_midm_kernel(GemmArgs g) {
     using namespace mk;
-    __shared__ __attribute__((aligned(16))) uint8_t sW[NW][R * ROW_B];   // 128 KiB
-    __shared__ __attribute__((aligned(16))) float red[NW][TN * 256];      // 32 KiB
+    constexpr int NT = 64 * NW, SLICE_K = PASS_K / NW, STEPS = SLICE_K / 32, NPAIR = STEPS / 2;
+    constexpr int H = SLICE_K / 512;                // 256-byte halves of a row's slice
+    constexpr int XW = (R / 4) * H;                 // weight loads per wave per pass (4 rows x 256 bytes)
+    constexpr int SV = SLICE_K / 512;               // 16-byte E8M0 vectors per row per slice
+    constexpr int NSLOT = 2 * (PD + 1);             // activation fragment slots (steps)
+    __shared__ __attribute__((aligned(16))) uint8_t sW[NW][H][R * 256];   // 128 KiB
+    __shared__ __attribute__((aligned(16))) float red[NW][TN * 256];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1363,21 +1382,16 @@ __global__ __launch_bounds__(mk::NT, 1) void gemm_bf16f4_midm_kernel(GemmArgs g)
 #pragma unroll
     for (int t = 0; t < TN; ++t)
         srow[t] = reinterpret_cast<const uint8_t *>(g.sb) + min(n0 + 16 * t + n16, nend - 1) * g.ld_sb;
-    // weight load j covers rows 4j .. 4j + 3: lane l -> row 4j + l/16, LDS
-    // chunk l%16 holding source chunk (l%16) ^ (row & 15)
+    // weight load (j, h) covers rows 4j .. 4j + 3, bytes 256h .. 256h + 255 of
+    // their slices: lane l -> row 4j + l/16, LDS chunk l%16 holding source
+    // chunk (l%16) ^ (row & 15)
     uint32_t w_off[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int r = 4 * j + (lane >> 4);
         w_off[j] = (uint32_t)((lane >> 4) * g.ldb + 16 * ((lane & 15) ^ (r & 15)));
     }
-    u32x4 sv[TN];
-    // Workgroup b walks the steps of its slices starting at 4 (b mod 4): the
-    // activation rows are 8 KiB apart, so at any moment the bytes all the
-    // workgroups read of them would otherwise fall in the same few L2
-    // channels.  Step s reads K-step (s + rot) mod 16 of the slice; the
-    // E8M0 dword of a step is then dword (s/4 + rq) mod 4 of its vector.
-    const int rq = (int)(blockIdx.x & 3), rot = 4 * rq;
+    u32x4 sv[TN][SV];
     // byte address of the lane that loaded this lane's MFMA piece
     const int src4 = 4 * (4 * n16 + q);
 
@@ -1404,109 +1418,103 @@ __global__ __launch_bounds__(mk::NT, 1) void gemm_bf16f4_midm_kernel(GemmArgs g)
 #pragma nounroll
         for (int64_t kp = 0; kp < g.K; kp += PASS_K) {
             const int64_t k0 = kp + (int64_t)wave * SLICE_K;   // this wave's slice
-            const bool live = k0 < g.K;                         // K % 512 == 0: whole slices
+            const bool live = k0 < g.K;                         // K % SLICE_K == 0: whole slices
             const bool load_w = vg == 0 || !one_pass;
             // every wave is done with the LDS slice it is about to overwrite
             if (load_w && kp > 0) __syncthreads();
             if (!live) continue;
-            // The scales and the weight slice (when not already in LDS),
-            // then the first two steps' activation fragments: asm loads, all
-            // counted by the explicit waits below, in issue order, so the
-            // wait for step 0's fragments also covers the weights.
+            // The scales and the weight slice (when not already in LDS), then
+            // the first PD + 1 pairs of steps' activation fragments: asm
+            // loads, all counted by the explicit waits below, in issue order,
+            // so the wait for step 0's fragments also covers the weights.
             if (load_w) {
 #pragma unroll
-                for (int t = 0; t < TN; ++t) sv[t] = gload_x4(srow[t] + k0 / 32);
+                for (int t = 0; t < TN; ++t)
 #pragma unroll
-                for (int j = 0; j < XW; ++j) {
+                    for (int v = 0; v < SV; ++v) sv[t][v] = gload_x4(srow[t] + k0 / 32 + 16 * v);
+#pragma unroll
+                for (int j = 0; j < R / 4; ++j) {
                     const int64_t r0 = n0 + 4 * j, left = nend - r0;
                     const uint64_t bytes = left > 0 ? (uint64_t)((left - 1) * g.ldb + (g.K - k0) / 2) : 0;
-                    dma_x4(w_off[j & 3], buf_rsrc(g.b + r0 * g.ldb + k0 / 2, bytes), lds_u32(&sW[wave][0]) + j * 1024);
+#pragma unroll
+                    for (int h = 0; h < H; ++h)
+                        dma_x4(w_off[j & 3], buf_rsrc(g.b + r0 * g.ldb + k0 / 2 + 256 * h, bytes > 256u * h ? bytes - 256u * h : 0),
+                               lds_u32(&sW[wave][h][0]) + j * 1024);
                 }
             }
-            // Fragments of steps s and s + 1 (s even) are loaded back to back
-            // per tile, so the two 64-byte halves of each 128-byte line are
-            // requested together (one line fill); the next pair is issued at
-            // the start of an even step, a pair ahead.
-            u32x4 af[4][MT];
+            // Steps s and s + 1 (s even) are loaded back to back per tile, so
+            // the two 64-byte halves of each 128-byte line are requested
+            // together (one line fill).
+            u32x4 af[NSLOT][MT];
             auto fetch2 = [&](int s) __attribute__((always_inline)) {
-                const uint32_t off0 = (uint32_t)(k0 * 2) + 64u * (uint32_t)((s + rot) & (STEPS - 1));
+                const uint32_t off0 = (uint32_t)(k0 * 2) + 64u * (uint32_t)s;
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    af[s % 4][mt] = gload_x4(arow[mt] + off0);
-                    af[(s + 1) % 4][mt] = gload_x4(arow[mt] + off0 + 64);
+                    af[s % NSLOT][mt] = gload_x4(arow[mt] + off0);
+                    af[(s + 1) % NSLOT][mt] = gload_x4(arow[mt] + off0 + 64);
                 }
             };
-            fetch2(0);
-            // A step's operands (the permuted activation fragments ab and
-            // the dequantized weight fragments wf) are prepared one step
-            // ahead, so their LDS latencies overlap the previous step's
-            // MFMAs.  wait_for(s): step s's fragments have landed; what may
-            // still be in flight is what was issued after step s's last one
-            // (issued = pairs fetched up to and including step cur).
-            auto wait_for = [&](int s, int cur) __attribute__((always_inline)) {
-                // first step of the newest pair issued: two pairs in the
-                // prologue, then pair s + 3 at each odd step s
-                const int last = min(cur % 2 ? cur + 3 : cur + 2, STEPS - 2);
-                const int ahead = (s % 2 == 0) ? 1 + (last - s) / 2 * 2 * MT : (last - (s - 1)) / 2 * 2 * MT;
-                __builtin_amdgcn_sched_barrier(0);
-                if (ahead == 4 * MT + 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * MT + 1) : "memory");
-                else if (ahead == 2 * MT + 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * MT + 1) : "memory");
-                else if (ahead == 4 * MT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * MT) : "memory");
-                else if (ahead == 2 * MT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * MT) : "memory");
-                else if (ahead == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-                else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __builtin_amdgcn_sched_barrier(0);
-            };
+            // A step's operands (the permuted activation fragments ab and the
+            // weight code words pc) are prepared one step ahead, so their LDS
+            // latencies overlap the previous step's MFMAs.
             auto prep = [&](int s, u32x4 (&ab)[MT], uint32_t (&pc)[TN]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    asm volatile("" : "+v"(af[s % 4][mt]));
-                    const u32x4 v = af[s % 4][mt];
+                    asm volatile("" : "+v"(af[s % NSLOT][mt]));
+                    const u32x4 v = af[s % NSLOT][mt];
                     ab[mt] = u32x4{(uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.x),
                                    (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.y),
                                    (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.z),
                                    (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)v.w)};
                 }
-                const int se = (s + rot) & (STEPS - 1);
-                // the step's four weight code words (8 codes per lane each)
+                const int h = s >> 4, c = s & 15;
 #pragma unroll
                 for (int t = 0; t < TN; ++t)
-                    pc[t] = *reinterpret_cast<const uint32_t *>(&sW[wave][(16 * t + n16) * ROW_B + 16 * (se ^ n16) + 4 * q]);
+                    pc[t] = *reinterpret_cast<const uint32_t *>(&sW[wave][h][(16 * t + n16) * 256 + 16 * (c ^ n16) + 4 * q]);
             };
-            // step 0: its pair and the next one in flight
-            fetch2(2);
-            wait_for(0, 0);
+            // Pair p (steps 2p, 2p + 1) is issued in the prologue for p <= PD,
+            // else at the end of step 2(p - PD) - 1.  wait_for<s, cur>: step
+            // s's fragments have landed, given the pairs issued by step cur;
+            // what may stay in flight is what was issued after step s's last
+            // fragment (that of tile MT - 1).
+            auto wait_for = [&](auto sc, auto cc) __attribute__((always_inline)) {
+                constexpr int st = decltype(sc)::value, cur = decltype(cc)::value;
+                constexpr int newest = (PD + (cur + 1) / 2) < NPAIR - 1 ? PD + (cur + 1) / 2 : NPAIR - 1;
+                constexpr int ahead = st % 2 == 0 ? 1 + (newest - st / 2) * 2 * MT : (newest - (st - 1) / 2) * 2 * MT;
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vmcnt<ahead>();
+                __builtin_amdgcn_sched_barrier(0);
+            };
+#pragma unroll
+            for (int p = 0; p <= PD; ++p) fetch2(2 * p);
+            wait_for(SlotC<0>{}, SlotC<-1>{});
             if (load_w) {
 #pragma unroll
-                for (int t = 0; t < TN; ++t) {
-                    asm volatile("" : "+v"(sv[t]));
-                    // rotate the dwords so that dword s/4 holds step s's scales
-                    const u32x4 v = sv[t];
-                    sv[t] = rq == 0 ? v : rq == 1 ? u32x4{v.y, v.z, v.w, v.x}
-                                        : rq == 2 ? u32x4{v.z, v.w, v.x, v.y} : u32x4{v.w, v.x, v.y, v.z};
-                }
+                for (int t = 0; t < TN; ++t)
+#pragma unroll
+                    for (int v = 0; v < SV; ++v) asm volatile("" : "+v"(sv[t][v]));
             }
             u32x4 ab[2][MT];
             uint32_t pc[2][TN];
             prep(0, ab[0], pc[0]);
-#pragma unroll
-            for (int s = 0; s < STEPS; ++s) {
-                // the pair after next, issued at the start of an odd step
-                if (s % 2 == 1 && s + 3 < STEPS) fetch2(s + 3);
-                if (s + 1 < STEPS) {
-                    wait_for(s + 1, s);
-                    prep(s + 1, ab[(s + 1) % 2], pc[(s + 1) % 2]);
+            static_for<0, STEPS>([&](auto sc) __attribute__((always_inline)) {
+                constexpr int st = decltype(sc)::value;
+                // the pair PD + 1 ahead of the one ending here
+                if constexpr (st % 2 == 1 && (st + 1) / 2 + PD < NPAIR) fetch2(2 * ((st + 1) / 2 + PD));
+                if constexpr (st + 1 < STEPS) {
+                    wait_for(SlotC<st + 1>{}, SlotC<st>{});
+                    prep(st + 1, ab[(st + 1) % 2], pc[(st + 1) % 2]);
                 }
                 // dequantize the step's weight fragments (exact, block scale applied)
                 v8bf wf[TN];
 #pragma unroll
                 for (int t = 0; t < TN; ++t) {
-                    const uint32_t p = pc[s % 2][t];
-                    const float sc = e8m0_scale_nb((sv[t][s >> 2] >> (8 * (s & 3))) & 0xFFu);
-                    const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 0);
-                    const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 1);
-                    const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 2);
-                    const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 3);
+                    const uint32_t pw = pc[st % 2][t];
+                    const float sc8 = e8m0_scale_nb((sv[t][st >> 4][(st >> 2) & 3] >> (8 * (st & 3))) & 0xFFu);
+                    const v2bf d0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw, sc8, 0);
+                    const v2bf d1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw, sc8, 1);
+                    const v2bf d2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw, sc8, 2);
+                    const v2bf d3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(pw, sc8, 3);
                     wf[t] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
                 }
 #pragma unroll
@@ -1514,13 +1522,13 @@ __global__ __launch_bounds__(mk::NT, 1) void gemm_bf16f4_midm_kernel(GemmArgs g)
 #pragma unroll
                     for (int t = 0; t < TN; ++t)
                         acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(v8bf, ab[s % 2][mt]), wf[t], acc[mt][t], 0, 0, 0);
-            }
+                            __builtin_bit_cast(v8bf, ab[st % 2][mt]), wf[t], acc[mt][t], 0, 0, 0);
+            });
         }
 
         // acc[mt][t][r] = D[4q + r][n16] of the 16 x 16 tile (rows: activation
         // rows vg + 16 mt .., columns: weight rows 16 t ..); one activation
-        // tile at a time, the 8 waves' partial sums are added in wave order
+        // tile at a time, the waves' partial sums are added in wave order
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             __syncthreads();
@@ -1544,12 +1552,16 @@ __global__ __launch_bounds__(mk::NT, 1) void gemm_bf16f4_midm_kernel(GemmArgs g)
     }
 }
 
+// 8 waves with the next pair in flight: 4 waves (one per SIMD, 512
+// registers) with 2 or 3 pairs in flight measured 11-16% slower at M = 32,
+// 64 and 128 (cfg3's weight, one box)
+constexpr int kMidNW = 8, kMidPD = 1;
 template <int CT>
 static void launch_midm_ct(GemmArgs g, hipStream_t s) {
     const int64_t cus = num_cus_w(), per = (g.N + cus - 1) / cus, rows = (per + 3) / 4 * 4;
     g.rows_wg = (int)(rows > mk::R ? mk::R : rows < 16 ? 16 : rows);
-    const dim3 grid((unsigned)((g.N + g.rows_wg - 1) / g.rows_wg)), blk(mk::NT);
-    hipLaunchKernelGGL((gemm_bf16f4_midm_kernel<CT>), grid, blk, 0, s, g);
+    const dim3 grid((unsigned)((g.N + g.rows_wg - 1) / g.rows_wg)), blk(64 * kMidNW);
+    hipLaunchKernelGGL((gemm_bf16f4_midm_kernel<kMidNW, kMidPD, CT>), grid, blk, 0, s, g);
 }
 
 static hipError_t launch_midm(const GemmArgs &g, hipStream_t s) {
@@ -1570,7 +1582,7 @@ constexpr int64_t kMidMaxM = 64;
 // (at most 64 rows per workgroup) over at least one workgroup per CU.
 static bool midm_shape(int64_t M, int64_t N, int64_t K) {
     const int64_t cus = num_cus_w();
-    return M > kDecodeMaxM && M <= kMidMaxM && K % mk::SLICE_K == 0 && N >= 16 * cus && (N + cus - 1) / cus <= mk::R;
+    return M > kDecodeMaxM && M <= kMidMaxM && K % (mk::PASS_K / kMidNW) == 0 && N >= 16 * cus && (N + cus - 1) / cus <= mk::R;
 }
 // and E8M0 byte scales in 16-byte aligned rows (the decode kernel's scale loads)
 static bool midm_ok(const GemmArgs &g) {
