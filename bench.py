@@ -422,9 +422,8 @@ def bench_cfg4_reference_spelling(torch, A, B, apk, bpk, ae8, be8):
             "roofline": roofline("mfma", "gemm_f4f4_mx16_kernel after the scale regroup", flop / gemm_ref / 1e9,
                                  PEAK_FP4_TFLOPS, "TFLOP/s"),
             "note": "the GEMM call includes the fp32 -> K-major E8M0 conversion of both scale tensors in one "
-                    "launch (lsmx_scale_to_e8m0_batch, which also flags scales that are not powers of two) and the "
-                    "promotion launch that follows the GEMM and exits at once for the quantizer's power-of-two "
-                    "scales (lsmx_gemm_mx_promote); the step adds the unpacked-code quantizer and pack_fp4 of both "
+                    "launch (lsmx_scale_to_e8m0_batch); the promotion launch (lsmx_gemm_mx_promote) is skipped because "
+                    "fp4.py tracks the quantizer's own scales as powers of two; the step adds the unpacked-code quantizer and pack_fp4 of both "
                     "operands"}
 
 

@@ -38,9 +38,12 @@ _E8M0_EXACT: dict = {}
 
 
 def _mark_e8m0_exact(s: torch.Tensor) -> torch.Tensor:
-    key = id(s)
-    _E8M0_EXACT[key] = (s._version, s.data_ptr())
-    weakref.finalize(s, _E8M0_EXACT.pop, key, None)
+    # Views (reshape of a fresh tensor returns one) are tracked through the
+    # tensor that owns the storage: every view of it points to that one.
+    b = s._base if s._base is not None else s
+    key = id(b)
+    _E8M0_EXACT[key] = (b._version, b.data_ptr())
+    weakref.finalize(b, _E8M0_EXACT.pop, key, None)
     return s
 
 

@@ -127,6 +127,9 @@ def test_e8m0_exact_tracks_the_module_s_own_scales():
     v = s.view(8)
     v[1] = 1.5
     assert not fp4.e8m0_exact(s) and not fp4.e8m0_exact(v)
+    # quantize_mxfp4 marks a reshape of its output, which is a view
+    r = fp4._mark_e8m0_exact(torch.ones(2, 4).reshape(2, 4))
+    assert r._base is not None and fp4.e8m0_exact(r) and fp4.e8m0_exact(r[1:])
     t = fp4.e8m0_to_scale(torch.tensor([[127]], dtype=torch.uint8))
     key = id(t)
     del t
