@@ -82,6 +82,26 @@ int lsmx_quantize_mxfp4(const void *x, int x_dtype, int64_t rows, int64_t K, int
                         int block, void *codes, int codes_fmt, int64_t ld_codes, void *scale,
                         int scale_fmt, int64_t ld_scale, void *stream);
 
+/* One tensor of lsmx_quantize_mxfp4_batch: the arguments of
+ * lsmx_quantize_mxfp4 for it (block 32, packed codes). */
+typedef struct {
+    const void *x;
+    int64_t rows, K, ldx;
+    void *codes;
+    int64_t ld_codes;
+    void *scale;
+    int64_t ld_scale;
+} lsmx_q_item;
+
+/* lsmx_quantize_mxfp4 (block 32, LSMX_CODES_PACKED, E8M0 scales row-major
+ * or K-major) of n <= 8 tensors of one dtype and scale format in one launch,
+ * with the same outputs bit for bit.  The fully-FP4 GEMM step quantizes both
+ * of its operands before the product (fp4_linear.py:36-39: X and W); one
+ * launch streams both without a drain and a ramp-up between them.  items is
+ * host memory, read before the call returns; the same checks as
+ * lsmx_quantize_mxfp4 apply to each tensor. */
+int lsmx_quantize_mxfp4_batch(const lsmx_q_item *items, int n, int x_dtype, int scale_fmt, void *stream);
+
 /* The same quantizer along the OTHER axis: x[K, cols] (ldx >= cols) is
  * quantized in blocks of `block` consecutive ROWS, and the outputs are laid
  * out for x^T: codes [cols, ld_codes], scale [cols, ld_scale].

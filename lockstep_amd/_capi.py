@@ -35,6 +35,7 @@ SIGNATURES = {
     "lsmx_last_error": [],
     "lsmx_device_check": [],
     "lsmx_quantize_mxfp4": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
+    "lsmx_quantize_mxfp4_batch": [_vp, _int, _int, _int, _vp],
     "lsmx_quantize_mxfp4_t": [_vp, _int, _i64, _i64, _i64, _int, _vp, _int, _i64, _vp, _int, _i64, _vp],
     "lsmx_quantize_mxfp4_2d": [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp],
     "lsmx_quantize_mxfp4_2d_batch": [_vp, _int, _int, _int, _vp],
@@ -65,6 +66,12 @@ SIGNATURES = {
 }
 
 RET_I64 = ("lsmx_gemm_bf16f4_workspace",)
+
+
+class QItem(ctypes.Structure):
+    """lsmx_q_item of include/lsmx.h."""
+    _fields_ = [("x", _vp), ("rows", _i64), ("K", _i64), ("ldx", _i64), ("codes", _vp), ("ld_codes", _i64),
+                ("scale", _vp), ("ld_scale", _i64)]
 
 
 class Q2dItem(ctypes.Structure):

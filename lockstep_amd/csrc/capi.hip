@@ -111,10 +111,11 @@ const char *lsmx_last_error(void) { return g_err; }
 
 int lsmx_device_check(void) { return device_guard(); }
 
-static int quantize_common(const void *x, int x_dtype, int64_t rows, int64_t K, int64_t ldx, int block,
-                           void *codes, int codes_fmt, int64_t ld_codes, void *scale, int scale_fmt,
-                           int64_t ld_scale, void *stream, bool cols) {
-    const char *fn = cols ? "lsmx_quantize_mxfp4_t" : "lsmx_quantize_mxfp4";
+// The argument checks of lsmx_quantize_mxfp4(_t) and of each tensor of
+// lsmx_quantize_mxfp4_batch.
+static int check_quant(const char *fn, const void *x, int x_dtype, int64_t rows, int64_t K, int64_t ldx, int block,
+                       const void *codes, int codes_fmt, int64_t ld_codes, const void *scale, int scale_fmt,
+                       int64_t ld_scale, bool cols) {
     if (!x || !codes || !scale) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
     if (x_dtype != LSMX_F32 && x_dtype != LSMX_BF16 && x_dtype != LSMX_F16)
         return fail(LSMX_ERR_DTYPE, "%s: x_dtype %d unsupported", fn, x_dtype);
@@ -147,6 +148,16 @@ static int quantize_common(const void *x, int x_dtype, int64_t rows, int64_t K, 
     }
     if ((scale_fmt == LSMX_SCALE_F32 || scale_fmt == LSMX_SCALE_E8M0_KMAJOR) && !aligned(scale, 4))
         return fail(LSMX_ERR_ALIGN, "%s: fp32 and K-major scales must be 4-byte aligned", fn);
+    return LSMX_OK;
+}
+
+static int quantize_common(const void *x, int x_dtype, int64_t rows, int64_t K, int64_t ldx, int block,
+                           void *codes, int codes_fmt, int64_t ld_codes, void *scale, int scale_fmt,
+                           int64_t ld_scale, void *stream, bool cols) {
+    const char *fn = cols ? "lsmx_quantize_mxfp4_t" : "lsmx_quantize_mxfp4";
+    if (int r = check_quant(fn, x, x_dtype, rows, K, ldx, block, codes, codes_fmt, ld_codes, scale, scale_fmt,
+                            ld_scale, cols))
+        return r;
     if (int r = device_guard()) return r;
     if (rows == 0 || K == 0) return LSMX_OK;
     lsmx::QuantArgs a{x, x_dtype, rows, K, ldx, block, codes, codes_fmt, ld_codes, scale, scale_fmt, ld_scale};
@@ -165,6 +176,30 @@ int lsmx_quantize_mxfp4_t(const void *x, int x_dtype, int64_t K, int64_t cols, i
                           int64_t ld_scale, void *stream) {
     return quantize_common(x, x_dtype, cols, K, ldx, block, codes, codes_fmt, ld_codes, scale, scale_fmt,
                            ld_scale, stream, true);
+}
+
+int lsmx_quantize_mxfp4_batch(const lsmx_q_item *items, int n, int x_dtype, int scale_fmt, void *stream) {
+    const char *fn = "lsmx_quantize_mxfp4_batch";
+    if (!items) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (n < 0 || n > lsmx::kQBatch) return fail(LSMX_ERR_SHAPE, "%s: n must be 0 .. %d", fn, lsmx::kQBatch);
+    if (scale_fmt != LSMX_SCALE_E8M0 && scale_fmt != LSMX_SCALE_E8M0_KMAJOR)
+        return fail(LSMX_ERR_DTYPE, "%s: scale_fmt must be E8M0 or K-major E8M0", fn);
+    lsmx::QuantBatch b{};
+    int64_t rows = 0;
+    for (int k = 0; k < n; ++k) {
+        const lsmx_q_item &it = items[k];
+        if (int r = check_quant(fn, it.x, x_dtype, it.rows, it.K, it.ldx, 32, it.codes, LSMX_CODES_PACKED,
+                                it.ld_codes, it.scale, scale_fmt, it.ld_scale, false))
+            return r;
+        if (it.rows == 0 || it.K == 0) continue;   // empty tensors take no row of the grid
+        b.a[b.n] = lsmx::QuantArgs{it.x, x_dtype, it.rows, it.K, it.ldx, 32, it.codes, LSMX_CODES_PACKED,
+                                   it.ld_codes, it.scale, scale_fmt, it.ld_scale};
+        rows += it.rows;
+        b.end[b.n++] = rows;
+    }
+    if (int r = device_guard()) return r;
+    if (b.n == 0) return LSMX_OK;
+    return launched(lsmx::launch_quantize_batch(b, (hipStream_t)stream), fn);
 }
 
 // The argument checks of one tensor of lsmx_quantize_mxfp4_2d(_batch).

@@ -50,6 +50,16 @@ struct Quant2dArgs {
     int scale_fmt;
 };
 
+// Up to kQBatch tensors of one dtype and scale format quantized along their
+// rows by one launch (packed codes, 32-blocks, E8M0 scales); end[k] = rows of
+// tensors 0 .. k.
+constexpr int kQBatch = 8;
+struct QuantBatch {
+    QuantArgs a[kQBatch];
+    int64_t end[kQBatch];
+    int n;
+};
+
 // Up to kQ2Batch tensors of one dtype and scale format quantized by one
 // launch; end[k] = tiles of tensors 0 .. k.
 constexpr int kQ2Batch = 8;
@@ -168,6 +178,7 @@ struct E8m0Batch {
 hipError_t launch_quantize(const QuantArgs &a, bool cols, hipStream_t s);
 hipError_t launch_quantize_2d(const Quant2dArgs &a, hipStream_t s);
 hipError_t launch_quantize_2d_batch(const Quant2dBatch &b, hipStream_t s);
+hipError_t launch_quantize_batch(const QuantBatch &b, hipStream_t s);
 hipError_t launch_round(const void *q, int q_dtype, int64_t n, uint8_t *codes, hipStream_t s);
 hipError_t launch_pack(const uint8_t *codes, uint8_t *packed, int64_t n_bytes, hipStream_t s);
 hipError_t launch_unpack(const uint8_t *packed, uint8_t *codes, int64_t n_bytes, hipStream_t s);

@@ -185,74 +185,100 @@ LSMX_DEV void store_scale(void *scale, int64_t r, int64_t kb, int64_t ld_scale, 
         reinterpret_cast<uint8_t *>(scale)[((kb >> 2) * ld_scale + r) * 4 + (kb & 3)] = (uint8_t)e8;
 }
 
+// Row r of x (xr: its first element), the kQUnroll vectors of this thread
+// from vector v0 on.  Every lane of the workgroup calls it for the same row
+// (the block maxima and K-major scale gathers are cross-lane).
+template <typename T, int BLOCK, bool PACKED, int SFMT>
+LSMX_DEV void quantize_row(const T *__restrict__ xr, int64_t K, uint8_t *__restrict__ codes, int64_t ld_codes,
+                           void *__restrict__ scale, int64_t ld_scale, int64_t r, int64_t v0) {
+    constexpr int E = Elem<T>::kPerVec;
+    constexpr int G = BLOCK / E;  // lanes per block
+    const int64_t vpr = K / E;    // vectors per row
+    uint4 buf[kQUnroll];
+#pragma unroll
+    for (int u = 0; u < kQUnroll; ++u) {
+        const int64_t v = v0 + u * kQThreads;
+        if (v < vpr) {
+            // streaming read: each input byte is used exactly once
+            const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr) + v);
+            buf[u] = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            buf[u] = make_uint4(0, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kQUnroll; ++u) {
+        const int64_t v = v0 + u * kQThreads;
+        uint32_t b[E];
+        Elem<T>::bits(buf[u], b);
+        uint32_t am = 0;
+#pragma unroll
+        for (int i = 0; i < E; ++i) am = max(am, b[i] & 0x7FFFFFFFu);
+        am = group_max<G>(am);  // every lane of the block participates
+        const uint32_t e8 = block_e8m0(am);
+        // K-major scales: the lane holding block kb (kb % 4 == 0) gathers
+        // the bytes of kb..kb+3 -- the same row's dword -- for one store.
+        // Every lane takes part in the cross-lane reads.
+        uint32_t e4 = 0;
+        if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR && BLOCK == 32) {
+            const int l = (int)(threadIdx.x & 63);
+            e4 = e8 | ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + G) & 63) << 2, (int)e8) << 8) |
+                 ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + 2 * G) & 63) << 2, (int)e8) << 16) |
+                 ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + 3 * G) & 63) << 2, (int)e8) << 24);
+        }
+        if (v >= vpr) continue;  // whole blocks are in or out of range
+        // NaN blocks are rare: any lane with one takes the whole wave
+        // through the exact per-element rule
+        uint32_t w;
+        if (__any(e8 == 255u)) w = e2m1_pack_exact<E>(b, e8);
+        else if constexpr (sizeof(T) == 2) w = e2m1_pack_hw16<E>(b, e8);
+        else w = e2m1_pack_hw<E>(b, e8);
+        const int64_t col = v * E;
+        if constexpr (PACKED) {
+            if constexpr (E == 4) *reinterpret_cast<uint16_t *>(codes + r * ld_codes + col / 2) = (uint16_t)w;
+            else *reinterpret_cast<uint32_t *>(codes + r * ld_codes + col / 2) = w;
+        } else {
+            uint32_t c[E];
+#pragma unroll
+            for (int i = 0; i < E; ++i) c[i] = (w >> (4 * i)) & 0xF;
+            CodeStore<E>::unpacked(codes + r * ld_codes + col, c);
+        }
+        if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR && BLOCK == 32) {
+            const int64_t kb = col / BLOCK;
+            // vectors of a wave start on a 4-block boundary (64 lanes x E elements)
+            if ((threadIdx.x % (4 * G)) == 0)
+                reinterpret_cast<uint32_t *>(scale)[(kb >> 2) * ld_scale + r] = e4;
+        } else {
+            if ((threadIdx.x % G) == 0) store_scale<SFMT>(scale, r, col / BLOCK, ld_scale, e8);
+        }
+    }
+}
+
 template <typename T, int BLOCK, bool PACKED, int SFMT>
 __global__ __launch_bounds__(kQThreads) void quantize_rows_kernel(
     const T *__restrict__ x, int64_t rows, int64_t K, int64_t ldx, uint8_t *__restrict__ codes,
     int64_t ld_codes, void *__restrict__ scale, int64_t ld_scale) {
-    constexpr int E = Elem<T>::kPerVec;
-    constexpr int G = BLOCK / E;  // lanes per block
-    const int64_t vpr = K / E;    // vectors per row
     const int64_t v0 = (int64_t)blockIdx.x * (kQThreads * kQUnroll) + threadIdx.x;
-    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
-        const T *xr = x + r * ldx;
-        uint4 buf[kQUnroll];
-#pragma unroll
-        for (int u = 0; u < kQUnroll; ++u) {
-            const int64_t v = v0 + u * kQThreads;
-            if (v < vpr) {
-                // streaming read: each input byte is used exactly once
-                const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr) + v);
-                buf[u] = make_uint4(w[0], w[1], w[2], w[3]);
-            } else {
-                buf[u] = make_uint4(0, 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kQUnroll; ++u) {
-            const int64_t v = v0 + u * kQThreads;
-            uint32_t b[E];
-            Elem<T>::bits(buf[u], b);
-            uint32_t am = 0;
-#pragma unroll
-            for (int i = 0; i < E; ++i) am = max(am, b[i] & 0x7FFFFFFFu);
-            am = group_max<G>(am);  // every lane of the block participates
-            const uint32_t e8 = block_e8m0(am);
-            // K-major scales: the lane holding block kb (kb % 4 == 0) gathers
-            // the bytes of kb..kb+3 -- the same row's dword -- for one store.
-            // Every lane takes part in the cross-lane reads.
-            uint32_t e4 = 0;
-            if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR && BLOCK == 32) {
-                const int l = (int)(threadIdx.x & 63);
-                e4 = e8 | ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + G) & 63) << 2, (int)e8) << 8) |
-                     ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + 2 * G) & 63) << 2, (int)e8) << 16) |
-                     ((uint32_t)__builtin_amdgcn_ds_bpermute(((l + 3 * G) & 63) << 2, (int)e8) << 24);
-            }
-            if (v >= vpr) continue;  // whole blocks are in or out of range
-            // NaN blocks are rare: any lane with one takes the whole wave
-            // through the exact per-element rule
-            uint32_t w;
-            if (__any(e8 == 255u)) w = e2m1_pack_exact<E>(b, e8);
-            else if constexpr (sizeof(T) == 2) w = e2m1_pack_hw16<E>(b, e8);
-            else w = e2m1_pack_hw<E>(b, e8);
-            const int64_t col = v * E;
-            if constexpr (PACKED) {
-                if constexpr (E == 4) *reinterpret_cast<uint16_t *>(codes + r * ld_codes + col / 2) = (uint16_t)w;
-                else *reinterpret_cast<uint32_t *>(codes + r * ld_codes + col / 2) = w;
-            } else {
-                uint32_t c[E];
-#pragma unroll
-                for (int i = 0; i < E; ++i) c[i] = (w >> (4 * i)) & 0xF;
-                CodeStore<E>::unpacked(codes + r * ld_codes + col, c);
-            }
-            if constexpr (SFMT == LSMX_SCALE_E8M0_KMAJOR && BLOCK == 32) {
-                const int64_t kb = col / BLOCK;
-                // vectors of a wave start on a 4-block boundary (64 lanes x E elements)
-                if ((threadIdx.x % (4 * G)) == 0)
-                    reinterpret_cast<uint32_t *>(scale)[(kb >> 2) * ld_scale + r] = e4;
-            } else {
-                if ((threadIdx.x % G) == 0) store_scale<SFMT>(scale, r, col / BLOCK, ld_scale, e8);
-            }
-        }
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)
+        quantize_row<T, BLOCK, PACKED, SFMT>(x + r * ldx, K, codes, ld_codes, scale, ld_scale, r, v0);
+}
+
+// Several tensors of one dtype and format in one launch: the rows of tensor
+// k are global rows end[k - 1] .. end[k] - 1, walked grid-strided along y;
+// the grid's x extent covers the longest row (workgroups past a shorter
+// row's end store nothing for it).
+template <typename T, int SFMT>
+__global__ __launch_bounds__(kQThreads) void quantize_rows_batch_kernel(QuantBatch b) {
+    const int64_t v0 = (int64_t)blockIdx.x * (kQThreads * kQUnroll) + threadIdx.x;
+    const int64_t total = b.end[b.n - 1];
+    int k = 0;
+    for (int64_t gr = blockIdx.y; gr < total; gr += gridDim.y) {
+        while (gr >= b.end[k]) ++k;   // gr < total = end[n - 1]: k stays below n
+        const QuantArgs &a = b.a[k];
+        const int64_t r = gr - (k ? b.end[k - 1] : 0);
+        quantize_row<T, 32, true, SFMT>(reinterpret_cast<const T *>(a.x) + r * a.ldx, a.K,
+                                        reinterpret_cast<uint8_t *>(a.codes), a.ld_codes, a.scale, a.ld_scale, r,
+                                        v0);
     }
 }
 
@@ -790,6 +816,31 @@ static hipError_t launch_rows(const QuantArgs &a, hipStream_t s) {
                        dim3(kQThreads), 0, s, reinterpret_cast<const T *>(a.x), a.rows, a.K, a.ldx,
                        reinterpret_cast<uint8_t *>(a.codes), a.ld_codes, a.scale, a.ld_scale);
     return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_rows_batch(const QuantBatch &b, hipStream_t s) {
+    constexpr int E = Elem<T>::kPerVec;
+    int64_t kmax = 0;
+    for (int k = 0; k < b.n; ++k) kmax = b.a[k].K > kmax ? b.a[k].K : kmax;
+    const int64_t gx = (kmax / E + kQThreads * kQUnroll - 1) / (kQThreads * kQUnroll);
+    const int64_t total = b.end[b.n - 1];
+    const int64_t gy = total < 65535 ? total : 65535;
+    if (b.a[0].scale_fmt == LSMX_SCALE_E8M0_KMAJOR)
+        hipLaunchKernelGGL((quantize_rows_batch_kernel<T, LSMX_SCALE_E8M0_KMAJOR>), dim3((unsigned)gx, (unsigned)gy),
+                           dim3(kQThreads), 0, s, b);
+    else
+        hipLaunchKernelGGL((quantize_rows_batch_kernel<T, LSMX_SCALE_E8M0>), dim3((unsigned)gx, (unsigned)gy),
+                           dim3(kQThreads), 0, s, b);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_batch(const QuantBatch &b, hipStream_t s) {
+    switch (b.a[0].x_dtype) {
+        case LSMX_F32: return launch_rows_batch<float>(b, s);
+        case LSMX_BF16: return launch_rows_batch<bf16_t>(b, s);
+        default: return launch_rows_batch<f16_t>(b, s);
+    }
 }
 
 template <typename T, int BLOCK, bool PACKED, int SF32>

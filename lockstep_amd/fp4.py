@@ -125,9 +125,10 @@ def quantize_mxfp4(x: torch.Tensor, block: int = 32):
     rows = x2.shape[0]
     codes = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
     scale = torch.empty((rows, K // block), dtype=torch.float32, device=x.device)
-    C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
-           x2.stride(0) if rows > 1 else K, block, codes.data_ptr(), C.CODES_UNPACKED, K,
-           scale.data_ptr(), C.SCALE_F32, K // block, C.stream_of(x2))
+    if x2.numel():   # an empty tensor has no storage to pass (fp4.py returns empty outputs)
+        C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
+               x2.stride(0) if rows > 1 else K, block, codes.data_ptr(), C.CODES_UNPACKED, K,
+               scale.data_ptr(), C.SCALE_F32, K // block, C.stream_of(x2))
     return codes.reshape(*lead, K), _mark_e8m0_exact(scale.reshape(*lead, K // block))
 
 
@@ -155,12 +156,53 @@ def quantize_pack_mxfp4(x: torch.Tensor, block: int = 32, scale_layout: str = "r
         fmt, ld = C.SCALE_E8M0, K // block
     else:
         raise ValueError(f"scale_layout must be 'rows' or 'kmajor', got {scale_layout!r}")
-    C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
-           x2.stride(0) if rows > 1 else K, block, packed.data_ptr(), C.CODES_PACKED, K // 2,
-           e8m0.data_ptr(), fmt, ld, C.stream_of(x2))
+    if x2.numel():
+        C.call("lsmx_quantize_mxfp4", x2.data_ptr(), C.dtype_code(x2.dtype), rows, K,
+               x2.stride(0) if rows > 1 else K, block, packed.data_ptr(), C.CODES_PACKED, K // 2,
+               e8m0.data_ptr(), fmt, ld, C.stream_of(x2))
     if scale_layout == "kmajor":
         return packed.reshape(*lead, K // 2), e8m0
     return packed.reshape(*lead, K // 2), e8m0.reshape(*lead, K // block)
+
+
+def quantize_pack_mxfp4_many(xs, scale_layout: str = "rows"):
+    """[quantize_pack_mxfp4(x, 32, scale_layout) for x in xs], bit for bit.
+    fp32 / bf16 / fp16 tensors of one dtype go to the device in one launch per
+    group of up to 8 (lsmx_quantize_mxfp4_batch): the two operands of a GEMM
+    stream through one launch instead of two."""
+    if scale_layout not in ("rows", "kmajor"):
+        raise ValueError(f"scale_layout must be 'rows' or 'kmajor', got {scale_layout!r}")
+    km = scale_layout == "kmajor"
+    out = [None] * len(xs)
+    groups = {}
+    for i, x in enumerate(xs):
+        C.require_device(x)
+        K = x.shape[-1]
+        assert K % 32 == 0, f"K={K} must be a multiple of block=32"
+        if km:
+            assert x.dim() == 2 and K % 128 == 0, "K-major scales need a 2-D x with K % 128 == 0"
+        x2, lead = _as_rows(_src(x))
+        rows = x2.shape[0]
+        packed = torch.empty((rows, K // 2), dtype=torch.uint8, device=x.device)
+        if km:
+            e8m0 = torch.empty((K // 128, rows, 4), dtype=torch.uint8, device=x.device)
+            ld = rows
+            out[i] = (packed.reshape(*lead, K // 2), e8m0)
+        else:
+            e8m0 = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
+            ld = K // 32
+            out[i] = (packed.reshape(*lead, K // 2), e8m0.reshape(*lead, K // 32))
+        if x2.numel():
+            item = C.QItem(x2.data_ptr(), rows, K, x2.stride(0) if rows > 1 else K, packed.data_ptr(), K // 2,
+                           e8m0.data_ptr(), ld)
+            groups.setdefault((x2.dtype, x.device), []).append((item, x2))
+    for (dt, _), its in groups.items():
+        for g0 in range(0, len(its), 8):
+            part = its[g0:g0 + 8]
+            items = (C.QItem * len(part))(*[it for it, _ in part])
+            C.call("lsmx_quantize_mxfp4_batch", ctypes.addressof(items), len(part), C.dtype_code(dt),
+                   C.SCALE_E8M0_KMAJOR if km else C.SCALE_E8M0, C.stream_of(part[0][1]))
+    return out
 
 
 def kmajor_scales(e8m0: torch.Tensor) -> torch.Tensor:

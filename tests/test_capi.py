@@ -100,6 +100,26 @@ def test_batched_quantizer_and_quantizing_gemm_validate_before_launch():
                256, FAKE, 128, FAKE, 256, 256, 256, 256, None) == C.ERR_ARG
 
 
+def test_row_quantizer_batch_validates_before_launch():
+    """lsmx_quantize_mxfp4_batch takes 0 .. 8 items, E8M0 scales only, and
+    checks each item as lsmx_quantize_mxfp4 does (block 32, packed codes)."""
+    f = 0x1000
+    items = (C.QItem * 9)()
+    assert _rc("lsmx_quantize_mxfp4_batch", None, 1, C.F32, C.SCALE_E8M0, None) == C.ERR_ARG
+    assert _rc("lsmx_quantize_mxfp4_batch", ctypes.addressof(items), 9, C.F32, C.SCALE_E8M0, None) == C.ERR_SHAPE
+    items[0] = C.QItem(f, 4, 64, 64, f, 32, f, 2)
+    assert _rc("lsmx_quantize_mxfp4_batch", ctypes.addressof(items), 1, C.F32, C.SCALE_F32, None) == C.ERR_DTYPE
+    items[1] = C.QItem(f, 4, 48, 48, f, 24, f, 2)                 # K % 32 != 0
+    assert _rc("lsmx_quantize_mxfp4_batch", ctypes.addressof(items), 2, C.F32, C.SCALE_E8M0, None) == C.ERR_SHAPE
+    items[1] = C.QItem(f + 4, 4, 64, 64, f, 32, f, 2)             # x rows not 16-byte aligned
+    assert _rc("lsmx_quantize_mxfp4_batch", ctypes.addressof(items), 2, C.F32, C.SCALE_E8M0, None) == C.ERR_ALIGN
+    items[1] = C.QItem(f, 4, 64, 64, f, 32, f, 2)                 # K-major needs K % 128 == 0
+    assert _rc("lsmx_quantize_mxfp4_batch", ctypes.addressof(items), 2, C.F32, C.SCALE_E8M0_KMAJOR,
+               None) == C.ERR_SHAPE
+    items[1] = C.QItem(None, 4, 64, 64, f, 32, f, 2)
+    assert _rc("lsmx_quantize_mxfp4_batch", ctypes.addressof(items), 2, C.F32, C.SCALE_E8M0, None) == C.ERR_ARG
+
+
 def test_promotion_entry_points_validate_before_launch():
     """lsmx_scale_to_e8m0_batch takes 0 .. 4 items with K-major output and an
     8-byte aligned flag; lsmx_gemm_mx_promote takes packed FP4 or E4M3

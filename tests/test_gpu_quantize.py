@@ -422,3 +422,35 @@ def test_quantize_both_axes_batch(dev, fp4mod):
                 want = fp4mod.quantize_pack_mxfp4_2d(x, scale_layout=lay)
                 for a, b in zip(gt, want):
                     assert a.shape == b.shape and torch.equal(a, b), (tuple(x.shape), lay)
+
+
+def test_quantize_rows_batch(dev, fp4mod, oracle):
+    """quantize_pack_mxfp4_many (lsmx_quantize_mxfp4_batch, up to 8 tensors
+    per launch) gives quantize_pack_mxfp4's bytes for every tensor: fp32,
+    bf16 and fp16 groups, rows of different lengths in one launch (the grid
+    covers the longest), a strided view, a 3-D tensor, an empty tensor, NaN
+    and Inf blocks, and two launches for 10 tensors; the oracle pins one
+    tensor of the batch."""
+    g = torch.Generator(device=dev).manual_seed(23)
+    rn = lambda *s: torch.randn(s, device=dev, generator=g)   # noqa: E731
+    odd = rn(64, 384)
+    odd[3, 40] = float("nan")
+    odd[7, 100] = float("inf")
+    odd[9, :32] = 0.0
+    xs = [rn(256, 8192) * 0.05, rn(300, 256), odd, rn(96, 1024)[:, 128:640], torch.empty((0, 128), device=dev),
+          rn(2, 5, 128), rn(128, 384).to(torch.bfloat16), rn(64, 640).to(torch.float16), rn(1, 4096)]
+    many = [rn(32, 128) * (k + 1) for k in range(10)]
+    for group, lays in ((xs, ("rows",)), ([x for x in xs if x.dim() == 2 and x.shape[1] % 128 == 0], ("kmajor",)),
+                        (many, ("rows", "kmajor"))):
+        for lay in lays:
+            got = fp4mod.quantize_pack_mxfp4_many(group, scale_layout=lay)
+            assert len(got) == len(group)
+            for x, gt in zip(group, got):
+                want = fp4mod.quantize_pack_mxfp4(x, scale_layout=lay)
+                for a, b in zip(gt, want):
+                    assert a.shape == b.shape and torch.equal(a, b), (tuple(x.shape), x.dtype, lay)
+    # the batch against the oracle directly, for the tensor with specials
+    got = fp4mod.quantize_pack_mxfp4_many([xs[0], odd], scale_layout="rows")[1]
+    codes, scale = oracle.quantize_mxfp4(odd.cpu().numpy(), 32)
+    assert np.array_equal(got[0].cpu().numpy(), oracle.pack_fp4(codes))
+    assert np.array_equal(got[1].cpu().numpy(), oracle.scale_to_e8m0(scale))
