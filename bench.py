@@ -187,14 +187,16 @@ def _time_events(fn, reps=20, warm=3):
 
 
 def _time_ops(ops, reps=10, warm=2):
-    """Per-op median event times of a sequence of ops run as one step."""
+    """A sequence of ops run as one step: (per-op median event times, median
+    step time).  The per-op times come from steps with an event between ops;
+    the step time from steps with events only at their ends, since each
+    event between two kernels adds a few microseconds of its own."""
     import torch
     for _ in range(warm):
         for _, f in ops:
             f()
     torch.cuda.synchronize()
     per = {name: [] for name, _ in ops}
-    tot = []
     for _ in range(reps):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(ops) + 1)]
         torch.cuda._sleep(2_000_000)
@@ -205,7 +207,16 @@ def _time_ops(ops, reps=10, warm=2):
         torch.cuda.synchronize()
         for i, (name, _) in enumerate(ops):
             per[name].append(ev[i].elapsed_time(ev[i + 1]))
-        tot.append(ev[0].elapsed_time(ev[-1]))
+    tot = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)
+        e0.record()
+        for _, f in ops:
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        tot.append(e0.elapsed_time(e1))
     return {k: median(v) for k, v in per.items()}, median(tot)
 
 
@@ -614,7 +625,9 @@ def bench_cfg5(torch, dev, cpu, T=8192, H=2048, F=8192):
                               "TFLOP/s"),
          "roofline_quantize": roofline("hbm", "quantize_2d_batch_kernel (x, w1, w2) + quantize_2d_kernel (dy)",
                                        qbytes / q_ms / 1e6, PEAK_HBM_GBS, "GB/s"),
-         "ops_ms": {k: round(v, 4) for k, v in per.items()}}
+         "ops_ms": {k: round(v, 4) for k, v in per.items()},
+         "how": "ms: median step with events only at its ends; ops_ms: steps with an event between ops, whose "
+                "sum exceeds ms by the events' own cost"}
     if cpu:
         from oracle import oracle as O
         bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)   # noqa: E731
