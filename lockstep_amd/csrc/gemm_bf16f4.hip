@@ -1083,9 +1083,10 @@ LSMX_DEV float f32_scale_nb(uint32_t b) {
     return u2f(ok ? b : 0x7FC00000u);
 }
 
-// MT = 1 with R <= 32: at most 128 VGPRs, two workgroups per CU
+// One workgroup per CU (the launcher gives each CU one share of the weight
+// rows): 8 waves, two per SIMD, so up to 256 VGPRs per wave.
 template <int MT, int R, int CT, bool SF32>
-__global__ __launch_bounds__(dk::NT, (R <= 32 && MT == 1) ? 2 : 1) void gemm_bf16f4_decode_kernel(GemmArgs g) {
+__global__ __launch_bounds__(dk::NT, 2) void gemm_bf16f4_decode_kernel(GemmArgs g) {
     using namespace dk;
     constexpr int TN = R / 16;                   // 16-column MFMA tiles
     constexpr int XW = R / 4;                    // weight loads per wave per pass
