@@ -33,7 +33,9 @@ from . import _capi as C
 # had then.  mxfp4_gemm_packed and mxfp4_gemm_fp8 skip the promotion launch
 # for scales still in that state (an in-place write to the tensor or to any
 # view of it bumps the shared version counter); any other fp32 scales are
-# checked on the device.
+# checked on the device.  Writes that bypass the version counter -- through
+# `tensor.data`, or from outside torch (DLPack, raw pointers) -- are not seen:
+# after such a write, pass a copy (`s.clone()`), which takes the checked path.
 _E8M0_EXACT: dict = {}
 
 
