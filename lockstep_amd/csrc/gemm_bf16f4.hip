@@ -1611,11 +1611,31 @@ namespace gv {
 // 9.5 us for 2-wave ones and 9.5-9.8 us with 1 or 4 rows per wave.  Of the
 // 8.4 us, the dequantize-and-dot arithmetic adds ~1.2 us and the activation
 // staging ~0.5 us to the 6.8 us of the loads alone (a plain 31 MB read runs
-// in 6.0 us)
+// in 6.0 us); the lane sum on the vector ALU (wave_sum_fixed) took ~0.5 us
+// off the arithmetic's share
 constexpr int NT = 256;
 constexpr int RPW = 2;
 constexpr int UB = 2;     // groups of 64 blocks per lane in flight
 }  // namespace gv
+
+// Sum over the 64 lanes, the same in every lane, in a fixed tree on the
+// vector ALU: pairs (l, l ^ 1), (l, l ^ 2) of each quad (DPP quad_perm), then
+// the two quads of each 8 (row_half_mirror), the two halves of each row of
+// 16 (row_mirror), then rows l, l ^ 16 and halves l, l ^ 32
+// (v_permlane16_swap / v_permlane32_swap).  Each step adds a pair whose two
+// lanes hold the same two values, and fp32 addition commutes, so all lanes
+// end with the same bits.  Through __shfl_xor (LDS permutes) the six
+// dependent steps cost ~0.5 us of the M = 1 GEMV.
+LSMX_DEV float wave_sum_fixed(float v) {
+    v += u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0xB1, 0xF, 0xF, false));
+    v += u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x4E, 0xF, 0xF, false));
+    v += u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x141, 0xF, 0xF, false));
+    v += u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), 0x140, 0xF, 0xF, false));
+    const auto s16 = __builtin_amdgcn_permlane16_swap(f2u(v), f2u(v), false, false);
+    v = u2f(s16[0]) + u2f(s16[1]);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(f2u(v), f2u(v), false, false);
+    return u2f(s32[0]) + u2f(s32[1]);
+}
 
 template <int VM, bool SF32, int CT>
 __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
@@ -1740,12 +1760,7 @@ __global__ __launch_bounds__(gv::NT) void gemv_bf16f4_kernel(GemmArgs g) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int m = 0; m < VM; ++m) {
-            float v = acc[r][m];
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-            acc[r][m] = v;
-        }
+        for (int m = 0; m < VM; ++m) acc[r][m] = wave_sum_fixed(acc[r][m]);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
