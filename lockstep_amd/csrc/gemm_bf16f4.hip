@@ -281,9 +281,10 @@ LSMX_DEV void split_bf16_terms(uint32_t xb, uint32_t &hb, uint32_t &mb, uint32_t
     lb = f2u(r1 - u2f(mb << 16)) >> 16;
 }
 
-template <int AT, bool SF32, int CT, int BR, int BN, int KS>
-__global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
+template <int AT, bool SF32, int CT, int BR, int BN, int KS, int KG = 1>
+__global__ __launch_bounds__(xf::NT * KG, KG == 1 ? 2 : 4) void gemm_xf4_kernel(GemmArgs g) {
     using namespace xf;
+    static_assert(KG == 1 || KS == 4, "K groups split the 32 x 32 tile form");
     constexpr int ES = AT == LSMX_F32 ? 4 : 2;        // activation bytes
     constexpr int NTERM = AT == LSMX_F32 ? 3 : 2;     // bf16 terms per activation
     constexpr int WM = KS == 1 ? 2 : 1, WN = KS == 1 ? 2 : 1;  // wave grid over the tile
@@ -293,19 +294,27 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
     constexpr int CPR = BK / EPC;                     // source chunks per row per stage (16 or 8)
     constexpr int XA = BR * CPR / NT;                 // source chunks per thread per stage (4 or 2)
     constexpr int WCH = BN * 2;                       // 16-byte W chunks per stage
-    __shared__ __attribute__((aligned(16))) uint8_t sX[2][NTERM][BR * ROW_B];  // 2 x 3 x 8 KiB (fp32)
-    __shared__ __attribute__((aligned(16))) uint8_t sW[2][BN * 32];            // [half][col][16 B]
-    __shared__ uint32_t sS[2][BN];
+    // K group kg's activation rows are rows kg * BR .. of each term plane,
+    // its W chunks and scales the kg-th part of each buffer, so that every
+    // LDS address is a per-lane offset (which includes kg) plus an immediate
+    __shared__ __attribute__((aligned(16))) uint8_t sX[2][NTERM][KG * BR * ROW_B];  // 2 x 3 x 8 KiB per group (fp32)
+    __shared__ __attribute__((aligned(16))) uint8_t sW[2][KG * BN * 32];            // [group][half][col][16 B]
+    __shared__ uint32_t sS[2][KG * BN];
 
     const int tiles_m = (int)((g.M + BR - 1) / BR), tiles_n = (int)((g.N + BN - 1) / BN);
     int tm, tn;
     tile_coords_w(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BR, n0 = (int64_t)tn * BN;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // K group kg (4 waves) runs stages kg * nkg .. + nkg - 1 on its own LDS
+    // buffers; the groups meet only at the workgroup barriers, which they
+    // reach in step
+    const int kg = __builtin_amdgcn_readfirstlane((int)threadIdx.x / NT);
+    const int t = (int)threadIdx.x % NT, lane = t & 63, wave = t >> 6;
     const int wm = KS == 1 ? wave >> 1 : 0, wn = KS == 1 ? wave & 1 : 0;
     const int wk = KS == 1 ? 0 : wave;                // this wave's K-steps: wk, wk + KS, ... of each stage
     const int frow = lane & 31, half = lane >> 5;
-    const int nk = (int)(g.K / BK);
+    const int nk = (int)(g.K / BK) / KG;              // stages of this K group (the launcher keeps KG | K / BK)
+    const int64_t kg0 = (int64_t)kg * nk;             // its first stage
 
     // source chunk q = i * NT + t: row q / CPR, activations EPC * (q % CPR)
     // .. +EPC, i.e. 2 * EPC bytes of each term plane at byte 2 * EPC * (q %
@@ -315,14 +324,14 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < XA; ++i) {
         const int q = i * NT + t;
-        const int row = q / CPR, c = q % CPR;
+        const int row = q / CPR, c = q % CPR, lrow = kg * BR + row;
         ga[i] = g.a + min(m0 + row, g.M - 1) * g.lda * ES + c * 16;
         const int pb = 2 * EPC * c;  // byte in the plane row
-        x_off[i] = row * ROW_B + (((pb >> 4) ^ a_swz(row)) << 4) + (pb & 15);
+        x_off[i] = lrow * ROW_B + (((pb >> 4) ^ a_swz(lrow)) << 4) + (pb & 15);
     }
     const int wq = t < WCH ? t : 0;  // W chunk of this thread (threads >= WCH load none)
     const uint8_t *gw = g.b + min(n0 + (wq >> 1), g.N - 1) * g.ldb + (wq & 1) * 16;
-    const int w_off = (wq & 1) * (BN * 16) + (wq >> 1) * 16;
+    const int w_off = (2 * kg + (wq & 1)) * (BN * 16) + (wq >> 1) * 16;
     const int64_t s_row = min(n0 + (t % BN), g.N - 1) * g.ld_sb;
 
     // two register slots of staged loads: stage k lives in slot k % 2 from
@@ -332,9 +341,9 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
     auto gload = [&](int kt, auto slot) {
         constexpr int q = decltype(slot)::value;
 #pragma unroll
-        for (int i = 0; i < XA; ++i) ra[q][i] = *reinterpret_cast<const u32x4 *>(ga[i] + (int64_t)kt * BK * ES);
-        if (t < WCH) rw[q] = *reinterpret_cast<const u32x4 *>(gw + (int64_t)kt * 32);
-        rs[q] = load_scale2<SF32>(g.sb, s_row + (int64_t)kt * 2);
+        for (int i = 0; i < XA; ++i) ra[q][i] = *reinterpret_cast<const u32x4 *>(ga[i] + (kg0 + kt) * BK * ES);
+        if (t < WCH) rw[q] = *reinterpret_cast<const u32x4 *>(gw + (kg0 + kt) * 32);
+        rs[q] = load_scale2<SF32>(g.sb, s_row + (kg0 + kt) * 2);
     };
     auto swrite = [&](int buf, auto slot) {
         constexpr int q = decltype(slot)::value;
@@ -363,7 +372,7 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
             }
         }
         if (t < WCH) *reinterpret_cast<u32x4 *>(&sW[buf][w_off]) = rw[q];
-        if (t < BN) sS[buf][t] = rs[q];
+        if (t < BN) sS[buf][kg * BN + t] = rs[q];
     };
 
     v16f acc[CTW];
@@ -381,8 +390,8 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < CTW; ++j) {
             const int col = wn * (BN / WN) + j * 32 + frow;
-            const u32x4 pw = *reinterpret_cast<const u32x4 *>(&sW[buf][half * (BN * 16) + col * 16]);
-            const float sc = e8m0_scale_f32((sS[buf][col] >> (8 * half)) & 0xFF);
+            const u32x4 pw = *reinterpret_cast<const u32x4 *>(&sW[buf][(2 * kg + half) * (BN * 16) + col * 16]);
+            const float sc = e8m0_scale_f32((sS[buf][kg * BN + col] >> (8 * half)) & 0xFF);
 #pragma unroll
             for (int ss = 0; ss < NS; ++ss) {
                 const uint32_t cw = KS == 1 ? pw[ss] : pw[wk];
@@ -393,7 +402,7 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
                 fw[j][ss] = v8bf{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
             }
         }
-        const int row = wm * 32 + frow;
+        const int row = kg * BR + wm * 32 + frow;
 #pragma unroll
         for (int ss = 0; ss < NS; ++ss) {
             const int s = wk + KS * ss;
@@ -424,19 +433,23 @@ __global__ __launch_bounds__(xf::NT, 2) void gemm_xf4_kernel(GemmArgs g) {
     }
 
     if constexpr (KS > 1) {
-        // waves 1 .. KS-1 hand their partial tiles to wave 0 through LDS
-        // (the staging planes are free after the last barrier), which adds
-        // them in wave order
+        // waves 1 .. KG * KS - 1 (wave wk of K group kg is kg * KS + wk)
+        // hand their partial tiles to wave 0 through LDS (the staging planes
+        // are free after the last barrier), which adds them in that order
+        constexpr int NW = KG * KS;
+        const int gwv = kg * KS + wk;
         float *red = reinterpret_cast<float *>(&sX[0][0][0]);
-        static_assert(CTW == 1 && (KS - 1) * 16 * 64 * 4 <= (int)sizeof(sX), "reduction buffer");
-        if (wk > 0) {
+        static_assert(CTW == 1 && (NW - 1) * 16 * 64 * 4 <= (int)sizeof(sX), "reduction buffer");
+        if (gwv > 0) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) red[((wk - 1) * 16 + e) * 64 + lane] = acc[0][e];
+            for (int e = 0; e < 16; ++e) red[((gwv - 1) * 16 + e) * 64 + lane] = acc[0][e];
         }
         __syncthreads();
-        if (wk > 0) return;
-#pragma unroll
-        for (int w2 = 0; w2 < KS - 1; ++w2)
+        if (gwv > 0) return;
+        // one partial tile at a time (unrolled over 15 tiles, the compiler
+        // would issue all 240 reads at once and spill)
+#pragma nounroll
+        for (int w2 = 0; w2 < NW - 1; ++w2)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[0][e] += red[(w2 * 16 + e) * 64 + lane];
     }
@@ -456,14 +469,18 @@ hipError_t launch_gemm_xf4(const GemmArgs &g, int a_dtype, hipStream_t s) {
     // 32 x 32 tiles split four ways along K
     auto tiles = [&](int br, int bn) { return ((g.M + br - 1) / br) * ((g.N + bn - 1) / bn); };
     const int cus = num_cus_w();
-    const int shape = tiles(64, 128) >= cus ? 0 : (tiles(64, 64) >= cus ? 1 : 2);
+    // the 32 x 32 form: 4 K groups of 4 waves when the stage count allows
+    // (each group runs a quarter of the stages; cfg1's 16 dependent stages
+    // become 4)
+    const int shape = tiles(64, 128) >= cus ? 0 : (tiles(64, 64) >= cus ? 1 : ((g.K / xf::BK) % 4 == 0 ? 3 : 2));
     const dim3 grid((unsigned)(shape == 0 ? tiles(64, 128) : shape == 1 ? tiles(64, 64) : tiles(32, 32))),
-        blk(xf::NT);
+        blk(xf::NT), blk4(4 * xf::NT);
     const bool f = g.scale_fmt == LSMX_SCALE_F32;
 #define LSMX_X(AT, F, CT)                                                                           \
     do {                                                                                            \
         if (shape == 0) hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT, 64, 128, 1>), grid, blk, 0, s, g); \
         else if (shape == 1) hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT, 64, 64, 1>), grid, blk, 0, s, g); \
+        else if (shape == 3) hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT, 32, 32, 4, 4>), grid, blk4, 0, s, g); \
         else hipLaunchKernelGGL((gemm_xf4_kernel<AT, F, CT, 32, 32, 4>), grid, blk, 0, s, g);       \
     } while (0)
 #define LSMX_XC(AT, F)                                           \

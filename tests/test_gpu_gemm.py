@@ -392,14 +392,16 @@ def test_weight_only_split_k_on_two_streams(dev, mods):
 
 @pytest.mark.parametrize("adt", [torch.float32, torch.float16])
 @pytest.mark.parametrize("M,N,K", [(256, 1024, 1024), (1000, 2100, 512), (4096, 4096, 256), (512, 2048, 256),
-                                   (1, 300, 128), (70, 130, 384)])
+                                   (1, 300, 128), (70, 130, 384), (70, 130, 2048), (33, 40, 256)])
 def test_weight_only_wide_activations(dev, mods, oracle, adt, M, N, K):
     """fp32 and fp16 activations (lsmx_gemm_wonly_f4): each activation is
     split exactly into bf16 terms, so Y = X . deq(W)^T has the arithmetic of
     an fp32 matmul (fp4.py:75-78 dequantization, fp4_linear.py:40's
-    fake-quant forward with an unquantized X).  All three tile shapes on
-    256 CUs (64 x 128; 64 x 64 at 512 x 2048; 32 x 32 split four ways along
-    K for the smaller outputs), ragged edges; fp32 output <=
+    fake-quant forward with an unquantized X).  All tile shapes on 256 CUs
+    (64 x 128; 64 x 64 at 512 x 2048; 32 x 32 split four ways along K for
+    the smaller outputs, with four K groups of 4 waves when K / 64 % 4 == 0:
+    cfg1's 256 x 1024 x 1024, 70 x 130 x 2048 and 33 x 40 x 256 with one
+    stage per group), ragged edges; fp32 output <=
     1e-5 vs fp64; bf16 output is the RNE of the fp32 one; fp32 scales give
     the same bits as E8M0 bytes; a row holding +-Inf gives the oracle's
     non-finite pattern."""
