@@ -4,9 +4,15 @@
 
 Headline workload (BASELINE cfg4, the config the metric is quoted on):
 A, B fp32 [8192, 8192] = 0.05 * Student-t(3), resident in HBM.  One step =
-quantize A along K (fused quantize+pack, K-major E8M0 scales) + quantize B
-along K + f4 x f4 block-scaled GEMM (v_mfma_scale_f32_32x32x64_f8f6f4), bf16
-out.  `value` is 2*M*N*K / step time over the timed region.
+quantize A and B along K (fused quantize+pack, K-major E8M0 scales, both
+operands in one launch) + f4 x f4 block-scaled GEMM
+(v_mfma_scale_f32_16x16x128_f8f6f4), bf16 out.  `value` is 2*M*N*K / step
+time over the timed region.
+
+Order: the configs' GPU measurements, the cfg4 per-kernel timings (the
+GEMM's back-to-back loop last), the headline (W warm-up steps, K timed
+steps), then every CPU baseline: the headline's warm-up starts on a GPU
+that has been under load, not after an idle period.
 
 Alongside it:
   gemm / quantize     per-kernel rates from HIP events recorded on the
@@ -282,6 +288,16 @@ def main():
     B = t3(n, g, dev, torch)
     torch.cuda.synchronize()
 
+    # Every GPU measurement first, the CPU baselines last.  The config rows
+    # run before the headline, so its warm-up starts on a GPU already under
+    # load: from idle the chip first runs at its boost clock, then its power
+    # management throttles it for a few milliseconds before the clock settles
+    # (cfg4 steps 6-40 after idle measured 0.34-0.41 ms against 0.33 ms
+    # settled), and a short warm-up alone would time that transient.
+    deferred = None if args.no_cpu else []
+    config_rows = run_configs(torch, dev, deferred) if not args.no_configs else None
+    torch.cuda.synchronize()
+
     def step(ev=None):
         if ev:
             ev[0].record()
@@ -296,18 +312,14 @@ def main():
             ev[2].record()
         return c
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # timed region: exactly `steps` steps, synchronized on both sides
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / args.steps
-
+    # Per-kernel timings first (isolated launches after a spin kernel, the
+    # quantizer's average launch, the reference-spelling row, the GEMM back
+    # to back), then the step itself back to back (step_sustained, ~13 ms),
+    # right before the headline's warm-up: the timed steps then run at the
+    # step's own sustained clock, not in the power transient that follows
+    # an idle period (a throttling dip after the boost) or another workload
+    # (after the GEMM-only loop the clock briefly runs above the step's
+    # settled value).
     qab, gm = [], []
     for _ in range(max(args.steps, 5)):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
@@ -324,11 +336,24 @@ def main():
                             lambda: fp4.quantize_pack_mxfp4(B, scale_layout="kmajor")] * 4)
     apk, ae8 = fp4.quantize_pack_mxfp4(A, scale_layout="kmajor")
     bpk, be8 = fp4.quantize_pack_mxfp4(B, scale_layout="kmajor")
-    sustained_ms = _time_loop(lambda: mxfp4_gemm.mxfp4_gemm_packed(apk, bpk, ae8, be8), n=50)
     ref_spelling = None
     if not args.no_configs:
         ref_spelling = bench_cfg4_reference_spelling(torch, A, B, apk, bpk, ae8, be8)
+    sustained_ms = _time_loop(lambda: mxfp4_gemm.mxfp4_gemm_packed(apk, bpk, ae8, be8), n=50)
     del apk, bpk
+    step_sustained_ms = _time_loop(step, n=40)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` steps, synchronized on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
 
     flop = 2.0 * n * n * n
     gemm_tflops = flop / (gemm_ms * 1e-3) / 1e12
@@ -356,6 +381,9 @@ def main():
         "device": props.name,
         "gemm": {"ms": round(gemm_ms, 4), "tflops": round(gemm_tflops, 1),
                  "frac_fp4_peak": round(gemm_tflops / PEAK_FP4_TFLOPS, 4)},
+        "step_sustained": {"ms": round(step_sustained_ms, 4),
+                           "tflops": round(flop / (step_sustained_ms * 1e-3) / 1e12, 1),
+                           "how": "40 steps back to back, events around the loop, right before the warm-up"},
         "gemm_sustained": {"ms": round(sustained_ms, 4), "tflops": round(sus_tflops, 1),
                            "frac_fp4_peak": round(sus_tflops / PEAK_FP4_TFLOPS, 4),
                            "how": "50 GEMMs back to back, events around the loop"},
@@ -383,22 +411,25 @@ def main():
     del A, B
     torch.cuda.empty_cache()
 
+    suite_lines = bench_reference_rows(torch, dev) if args.suite else None
+
     cfg4_cpu = None
     if not args.no_cpu:
         cfg4_cpu = cpu_cfg4(n)
         out["cpu_baseline"] = cfg4_cpu
-    if not args.no_configs:
-        out["configs"] = run_configs(torch, dev, cpu=not args.no_cpu)
+        for leg in deferred:
+            leg()
+    if config_rows is not None:
+        out["configs"] = config_rows
         out["configs"].insert(len(out["configs"]) - 1, {
             "workload": "cfg4 fully-FP4 GEMM 8192^3, both operands quantized on the fly (the headline)",
             "ms": round(ms_per_step, 4), "rate": round(value, 1), "unit": "TFLOP/s",
             "roofline": out["roofline"], "roofline_quantize": out["roofline_quantize"],
             "cpu_baseline": cfg4_cpu})
         out["configs"].insert(len(out["configs"]) - 1, ref_spelling)
-    if args.suite:
-        lines = bench_reference_rows(torch, dev)
+    if suite_lines is not None:
         with open(args.suite, "w") as f:
-            for ln in lines:
+            for ln in suite_lines:
                 f.write(json.dumps(ln) + "\n")
     print(json.dumps(out), flush=True)
 
@@ -455,10 +486,15 @@ def cpu_cfg4(n):
 
 
 # ----------------------------------------------------------------- configs
-def run_configs(torch, dev, cpu=True):
-    """cfg1, cfg2, cfg3 (M sweep) and cfg5 at their BASELINE shapes: GPU rate,
-    roofline of the dominant kernel, CPU restatement timed beside it."""
+def run_configs(torch, dev, deferred=None):
+    """cfg1, cfg2, cfg3 (M sweep) and cfg5 at their BASELINE shapes: GPU rate
+    and roofline of the dominant kernel.  With a list `deferred`, each row's
+    CPU restatement is appended to it as a closure that fills the row's
+    cpu_baseline when called; it holds its inputs on the GPU and copies them
+    to the host only then.  The caller runs the closures after every GPU
+    measurement, so the GPU does not idle between the measurements."""
     import numpy as np
+    cpu = deferred is not None
 
     from lockstep_amd import dual_gemm, fp4, mxfp4_gemm
     from oracle import gen
@@ -487,12 +523,14 @@ def run_configs(torch, dev, cpu=True):
          "note": "a correctness config: 0.5 GFLOP per step does not fill the GPU; the fp32 activations cost "
                  "three bf16 MFMAs per product"}
     if cpu:
-        from oracle import oracle as O
+        def leg1(r=r):
+            from oracle import oracle as O
 
-        def run1():
-            x1 @ cpu_quant_deq(O, w1).T
-        r["cpu_baseline"] = cpu_leg(run1, fl1, "TFLOP/s", "full cfg1: quantize W (C oracle), dequantize, "
-                                                          "fp32 X @ W^T (numpy)")
+            def run1():
+                x1 @ cpu_quant_deq(O, w1).T
+            r["cpu_baseline"] = cpu_leg(run1, fl1, "TFLOP/s", "full cfg1: quantize W (C oracle), dequantize, "
+                                                              "fp32 X @ W^T (numpy)")
+        deferred.append(leg1)
     rows.append(r)
 
     # cfg2: A0, A1 bf16 [2048, 4096], W [4096, 4096] MXFP4, one dual launch
@@ -510,26 +548,26 @@ def run_configs(torch, dev, cpu=True):
                               "TFLOP/s", traffic_from_profiles("gemm_bf16f4_ring_kernel<2")),
          "two_launch_ms": round(ms2, 4)}
     if cpu:
-        from oracle import oracle as O
-        wc, ws = O.quantize_mxfp4(w2.cpu().numpy())
-        A0, A1 = _bf16_to_f32_np(a0), _bf16_to_f32_np(a1)
+        def leg2(r=r, w2=w2, a0=a0, a1=a1):
+            from oracle import oracle as O
+            wc, ws = O.quantize_mxfp4(w2.cpu().numpy())
+            A0, A1 = _bf16_to_f32_np(a0), _bf16_to_f32_np(a1)
 
-        def run2():
-            W = O.dequantize_mxfp4(wc, ws)
-            A0 @ W.T
-            A1 @ W.T
-        r["cpu_baseline"] = cpu_leg(run2, fl2, "TFLOP/s", "full cfg2: dequantize W (C oracle), two fp32 "
-                                                          "matmuls (numpy)")
+            def run2():
+                W = O.dequantize_mxfp4(wc, ws)
+                A0 @ W.T
+                A1 @ W.T
+            r["cpu_baseline"] = cpu_leg(run2, fl2, "TFLOP/s", "full cfg2: dequantize W (C oracle), two fp32 "
+                                                              "matmuls (numpy)")
+        deferred.append(leg2)
     rows.append(r)
     del a0, a1, w2, wpk, we8
 
     # cfg3: W [14336, 4096], M sweep
     w3 = torch.randn((14336, 4096), device=dev, generator=g) * 0.02
     w3pk, w3e8 = fp4.quantize_pack_mxfp4(w3)
-    w3c = w3s = None
-    if cpu:
-        from oracle import oracle as O
-        w3c, w3s = O.quantize_mxfp4(w3.cpu().numpy())
+    # the CPU legs quantize W once, when the first of them runs
+    q3 = {}
     # copies of the packed weight, rotated between launches: 16 x 31 MB is
     # twice the MALL, so every launch streams its weight from HBM
     wcopies = [(w3pk.clone(), w3e8.clone()) for _ in range(16)]
@@ -551,22 +589,27 @@ def run_configs(torch, dev, cpu=True):
              "rate": round(fl / ms / 1e9, 2), "unit": "TFLOP/s", "gbs": round(by / ms / 1e6, 1), "roofline": rl,
              "how": "16 launches back to back over 16 copies of W, events around the batch"}
         if cpu:
-            A = _bf16_to_f32_np(a)
+            def leg3(r=r, a=a, w3=w3, M=M, fl=fl):
+                from oracle import oracle as O
+                if not q3:
+                    q3["c"], q3["s"] = O.quantize_mxfp4(w3.cpu().numpy())
+                A = _bf16_to_f32_np(a)
 
-            def run3(A=A):
-                A @ O.dequantize_mxfp4(w3c, w3s).T
-            r["cpu_baseline"] = cpu_leg(run3, fl, "TFLOP/s", f"full cfg3 M={M}: dequantize W (C oracle), fp32 "
-                                                             "A @ W^T (numpy)")
+                def run3():
+                    A @ O.dequantize_mxfp4(q3["c"], q3["s"]).T
+                r["cpu_baseline"] = cpu_leg(run3, fl, "TFLOP/s", f"full cfg3 M={M}: dequantize W (C oracle), fp32 "
+                                                                 "A @ W^T (numpy)")
+            deferred.append(leg3)
         rows.append(r)
         del a
-    del w3, w3pk, w3e8, w3c, w3s, wcopies
+    del w3, w3pk, w3e8, wcopies
     torch.cuda.empty_cache()
 
-    rows.append(bench_cfg5(torch, dev, cpu))
+    rows.append(bench_cfg5(torch, dev, deferred))
     return rows
 
 
-def bench_cfg5(torch, dev, cpu, T=8192, H=2048, F=8192):
+def bench_cfg5(torch, dev, deferred, T=8192, H=2048, F=8192):
     """cfg5: one MLP block (fc H->F, out F->H) forward + MXFP4 backward, timed
     op by op inside one step: the 6 f4 x f4 GEMMs (fwd, dgrad, wgrad of each
     linear, train_step.py:3-6) on operands quantized along both axes.  x, w1,
@@ -628,24 +671,27 @@ def bench_cfg5(torch, dev, cpu, T=8192, H=2048, F=8192):
          "ops_ms": {k: round(v, 4) for k, v in per.items()},
          "how": "ms: median step with events only at its ends; ops_ms: steps with an event between ops, whose "
                 "sum exceeds ms by the events' own cost"}
-    if cpu:
-        from oracle import oracle as O
+    if deferred is not None:
         bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)   # noqa: E731
-        X, W1, W2, DY = (bits(t) for t in (x, w1, w2, dy))
         # the bf16 h and dh the CPU leg starts from (outside the timed ops)
-        hf = _bf16_to_f32_np(mm("x_r", "w1_r"))
-        dhf = _bf16_to_f32_np(mm("dy_r", "w2_c"))
+        h_dev, dh_dev = mm("x_r", "w1_r"), mm("dy_r", "w2_c")
 
-        def run5():
-            qd = lambda a, d=None: cpu_quant_deq(O, a, d)   # noqa: E731
-            qd(X, "bf16") @ qd(W1, "bf16").T                              # fc fwd
-            qd(hf) @ qd(W2, "bf16").T                                     # out fwd
-            qd(DY, "bf16") @ qd(np.ascontiguousarray(W2.T), "bf16").T     # out dgrad
-            qd(np.ascontiguousarray(DY.T), "bf16") @ qd(np.ascontiguousarray(hf.T)).T   # out wgrad
-            qd(dhf) @ qd(np.ascontiguousarray(W1.T), "bf16").T            # fc dgrad
-            qd(np.ascontiguousarray(dhf.T)) @ qd(np.ascontiguousarray(X.T), "bf16").T   # fc wgrad
-        r["cpu_baseline"] = cpu_leg(run5, fl, "TFLOP/s", "full cfg5: 12 quantizations (C oracle, transposes by "
-                                                         "numpy), dequantize, 6 fp32 matmuls (numpy)")
+        def leg5(r=r, xs=(x, w1, w2, dy), h_dev=h_dev, dh_dev=dh_dev):
+            from oracle import oracle as O
+            X, W1, W2, DY = (bits(t) for t in xs)
+            hf, dhf = _bf16_to_f32_np(h_dev), _bf16_to_f32_np(dh_dev)
+
+            def run5():
+                qd = lambda a, d=None: cpu_quant_deq(O, a, d)   # noqa: E731
+                qd(X, "bf16") @ qd(W1, "bf16").T                              # fc fwd
+                qd(hf) @ qd(W2, "bf16").T                                     # out fwd
+                qd(DY, "bf16") @ qd(np.ascontiguousarray(W2.T), "bf16").T     # out dgrad
+                qd(np.ascontiguousarray(DY.T), "bf16") @ qd(np.ascontiguousarray(hf.T)).T   # out wgrad
+                qd(dhf) @ qd(np.ascontiguousarray(W1.T), "bf16").T            # fc dgrad
+                qd(np.ascontiguousarray(dhf.T)) @ qd(np.ascontiguousarray(X.T), "bf16").T   # fc wgrad
+            r["cpu_baseline"] = cpu_leg(run5, fl, "TFLOP/s", "full cfg5: 12 quantizations (C oracle, transposes "
+                                                             "by numpy), dequantize, 6 fp32 matmuls (numpy)")
+        deferred.append(leg5)
     del s
     return r
 
