@@ -75,6 +75,8 @@ def dual_mxfp4(a0, a1, w_pk, w_scale, out_dtype=torch.bfloat16):
     c1 = torch.empty_like(c0)
     if M == 0 or N == 0:
         return c0, c1
+    if K == 0:   # no K iteration: zeros
+        return c0.zero_(), c1.zero_()
     nws = C.load().lsmx_gemm_bf16f4_workspace(M, N, K, 1)
     ws = C.workspace(a0.device, nws) if nws > 0 else None
     C.call("lsmx_gemm_bf16f4_ws", a0.data_ptr(), a1.data_ptr(), a0.stride(0) if M > 1 else K,

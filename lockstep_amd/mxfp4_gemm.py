@@ -82,6 +82,8 @@ def mxfp4_gemm_packed(a_pk, bt_pk, a_scale, b_scale, out_dtype=torch.bfloat16):
     c = torch.empty((M, N), device=a_pk.device, dtype=out_dtype)
     if M == 0 or N == 0:
         return c
+    if K == 0:   # the reference's K loop runs no iteration: C = 0
+        return c.zero_()
     if a_scale.dim() == 3:
         assert a_scale.dtype == torch.uint8, "K-major scales are E8M0 bytes"
         assert a_scale.shape == (K // 128, M, 4) and b_scale.shape == (K // 128, N, 4), \
@@ -173,12 +175,12 @@ def mxfp4_gemm_bf16(a, w_pk, w_scale, out_dtype=torch.bfloat16):
     if a.dtype not in _ACT:
         raise TypeError(f"activations must be bfloat16, float32 or float16, got {a.dtype}")
     C.require_device(a, w_pk, w_scale)
+    if M == 0 or N == 0 or K == 0:   # K == 0: no K iteration, zeros
+        return torch.zeros((M, N), device=a.device, dtype=out_dtype)
     a = _rows16(a)
     w_pk = _rows16(w_pk)
     w_scale = _wscales(w_scale, N, K // 32)
     c = torch.empty((M, N), device=a.device, dtype=out_dtype)
-    if M == 0 or N == 0:
-        return c
     if a.dtype == torch.bfloat16:
         # with a workspace the library may split K (mid-size M against a wide W)
         nws = C.load().lsmx_gemm_bf16f4_workspace(M, N, K, 0)

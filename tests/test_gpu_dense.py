@@ -215,6 +215,24 @@ def test_empty_and_zero_k(dev, mods):
     z = mg.mxfp4_gemm_fp8(f8, f8.t(), torch.ones((4, 0), device=dev), torch.ones((0, 4), device=dev),
                           out_dtype=torch.float32)
     assert z.shape == (4, 4) and not z.any()
+    # the f4 x f4 and weight-only GEMMs: K = 0 gives zeros (no K iteration),
+    # an empty side an empty output
+    pk, e8 = torch.zeros((4, 0), device=dev, dtype=torch.uint8), torch.zeros((4, 0), device=dev, dtype=torch.uint8)
+    z = mg.mxfp4_gemm_packed(pk, pk, e8, e8)
+    assert z.shape == (4, 4) and not z.any()
+    z = mg.mxfp4_gemm_packed(pk, pk, torch.ones((4, 0), device=dev), torch.ones((4, 0), device=dev))
+    assert z.shape == (4, 4) and not z.any()
+    z = mg.mxfp4_gemm_bf16(torch.ones((3, 0), device=dev, dtype=torch.bfloat16), pk, e8)
+    assert z.shape == (3, 4) and not z.any()
+    z = mg.mxfp4_gemm_bf16(torch.ones((3, 0), device=dev), pk, e8, out_dtype=torch.float32)
+    assert z.shape == (3, 4) and not z.any()
+    z0, z1 = dg.dual_mxfp4(torch.ones((3, 0), device=dev, dtype=torch.bfloat16),
+                           torch.ones((3, 0), device=dev, dtype=torch.bfloat16), pk, e8)
+    assert z0.shape == z1.shape == (3, 4) and not z0.any() and not z1.any()
+    assert mg.mxfp4_gemm_packed(torch.zeros((0, 64), device=dev, dtype=torch.uint8),
+                                torch.zeros((8, 64), device=dev, dtype=torch.uint8),
+                                torch.zeros((0, 4), device=dev, dtype=torch.uint8),
+                                torch.zeros((8, 4), device=dev, dtype=torch.uint8)).shape == (0, 8)
 
 
 @pytest.mark.parametrize("elem", [1, 2, 4])
