@@ -314,6 +314,17 @@ int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0
                     int dtype, int mode, float *c0, float *c1, int64_t ldc, int64_t M, int64_t N, int64_t K,
                     int splits, void *stream);
 
+/* lsmx_gemm_dense (bf16 / fp16, no split-K) with B as the reference passes
+ * it: b0, b1 [K, ldb] N-contiguous (dual_gemm.py:188-289 take b [K, N]), so
+ * no transpose is needed.  The kernel reads B rows of 256 columns into LDS
+ * and forms each MFMA operand with transposing LDS reads (ds_read_b64_tr_b16);
+ * same sums in the same order as lsmx_gemm_dense on the transposed B, so the
+ * same bits.  K % 64 == 0, N % 8 == 0; lda >= K, ldb >= N, both <= 2^22;
+ * rows 16-byte aligned. */
+int lsmx_gemm_dense_nb(const void *a0, const void *a1, int64_t lda, const void *b0, const void *b1, int64_t ldb,
+                       int dtype, int mode, float *c0, float *c1, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                       void *stream);
+
 /* MXFP4 GEMM on E4M3 operands holding E2M1 values, with E8M0 block scales:
  *   C[M, N] = sum_kb 2^(sa[m,kb]-127) 2^(sb[n,kb]-127) (A_kb . Bt_kb)
  * Replaces mxfp4_gemm.py:74-87 mxfp4_gemm_fp8 / _mxfp4_gemm_fp8_kernel

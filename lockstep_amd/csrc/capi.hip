@@ -449,6 +449,36 @@ int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0
     return launched(lsmx::launch_gemm_dense(g, dtype, mode, (hipStream_t)stream), fn);
 }
 
+int lsmx_gemm_dense_nb(const void *a0, const void *a1, int64_t lda, const void *b0, const void *b1, int64_t ldb,
+                       int dtype, int mode, float *c0, float *c1, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                       void *stream) {
+    const char *fn = "lsmx_gemm_dense_nb";
+    if (dtype != LSMX_BF16 && dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: dtype must be bf16 or fp16", fn);
+    if (mode < 0 || mode > 2) return fail(LSMX_ERR_ARG, "%s: mode must be 0, 1 or 2", fn);
+    if (!a0 || !b0 || !c0 || (mode && (!a1 || !b1)) || (mode == 2 && !c1))
+        return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % 64) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 64 (max BLOCK_K); zero-pad if shorter");
+    // whole 16-byte pieces of every B row: the last row's loads stop at its
+    // N-th column, and a piece cut there would read as zeros
+    if (N % 8) return fail(LSMX_ERR_SHAPE, "%s: N must be a multiple of 8", fn);
+    if (((M + 255) / 256) * ((N + 255) / 256) > 0x3FFFFFFF)
+        return fail(LSMX_ERR_SHAPE, "%s: too many output tiles", fn);
+    if (lda < K || ldb < N || ldc < N) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (lda > ((int64_t)1 << 22) || ldb > ((int64_t)1 << 22))
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimensions above 2^22 elements", fn);
+    if (!rows16(a0, lda, 2) || !rows16(b0, ldb, 2) || (mode && (!rows16(a1, lda, 2) || !rows16(b1, ldb, 2))))
+        return fail(LSMX_ERR_ALIGN, "%s: operand rows must be 16-byte aligned", fn);
+    if (!aligned(c0, 4) || (c1 && !aligned(c1, 4))) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
+    lsmx::DenseArgs g{reinterpret_cast<const uint8_t *>(a0), reinterpret_cast<const uint8_t *>(a1), lda,
+                      reinterpret_cast<const uint8_t *>(b0), reinterpret_cast<const uint8_t *>(b1), ldb,
+                      nullptr, nullptr, 0, 0, c0, c1, LSMX_F32, ldc, M, N, K, K, 1};
+    return launched(lsmx::launch_gemm_dense_ring(g, dtype, mode, (hipStream_t)stream), fn);
+}
+
 int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *bt,
                    int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, int scale_fmt, void *c, int c_dtype,
                    int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream) {

@@ -70,7 +70,27 @@ struct DrLoader {
     static constexpr bool value = V;
 };
 
-template <int DT, int MODE>
+// Four bf16/fp16 values of one column from a [K][N] LDS tile with
+// ds_read_b64_tr_b16: within each 16-lane group, lanes 4k .. 4k + 3 give the
+// addresses of 4 consecutive values of row k (8 bytes each), and lane j
+// receives value j % 4 of lane 4k + j / 4's row piece as its element k, i.e.
+// column j of the group's 4 x 16 block (the lane layout was checked on the
+// device with an in-bounds probe).
+typedef short v4s_d __attribute__((ext_vector_type(4)));
+typedef int v2i_d __attribute__((ext_vector_type(2)));
+LSMX_DEV v2i_d ds_read_tr16x4(const uint8_t *p) {
+    const v4s_d v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_d *)(p));
+    return __builtin_bit_cast(v2i_d, v);
+}
+
+// BNC: B arrives as the reference passes it, [K, N] with N contiguous (row
+// stride ldb elements), instead of K-contiguous Bt [N, K].  A stage of B is
+// then 64 K-rows of 512 bytes (256 columns); a DMA instruction carries two
+// rows, LDS position p of row r holding source chunk p ^ 4 (r & 3) (the 4
+// rows a half-wave reads at once land in 4 different 64-byte windows of the
+// 256-byte bank span), and each B fragment is two transposing reads of 4 K
+// values.
+template <int DT, int MODE, bool BNC = false>
 __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g) {
     using namespace dr;
     constexpr int P = MODE == 2 ? 2 : 1;      // GEMM problems
@@ -96,8 +116,13 @@ __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g)
     const int64_t lda_b = g.lda * 2, ldb_b = g.ldb * 2;
     const int drow0 = wave * RPI + lane / CPR;
     const uint32_t offA0 = (uint32_t)(drow0 * lda_b + ((lane % CPR) ^ swz(drow0)) * 16);
-    const uint32_t offB0 = (uint32_t)(drow0 * ldb_b + ((lane % CPR) ^ swz(drow0)) * 16);
-    const uint32_t stepA = (uint32_t)(NLW * RPI * lda_b), stepB = (uint32_t)(NLW * RPI * ldb_b);
+    // BNC: load i of this lane reads K-row 2 (i*NLW + wave) + lane/32 of the
+    // stage, chunk (lane % 32) ^ 4 (row & 3) (row & 3 does not depend on i)
+    const int brow0 = 2 * wave + (lane >> 5);
+    const uint32_t offB0 = BNC ? (uint32_t)(brow0 * ldb_b + (((lane & 31) ^ (4 * (brow0 & 3))) << 4))
+                               : (uint32_t)(drow0 * ldb_b + ((lane % CPR) ^ swz(drow0)) * 16);
+    const uint32_t stepA = (uint32_t)(NLW * RPI * lda_b);
+    const uint32_t stepB = BNC ? (uint32_t)(2 * NLW * ldb_b) : (uint32_t)(NLW * RPI * ldb_b);
 
     // Tile id -> (problem, tile row, tile column).  Workgroup ids reach the 8
     // XCDs round-robin; the remap gives each XCD a contiguous run of ids, in
@@ -127,10 +152,13 @@ __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g)
         for (int h = 0; h < KC; ++h) {
             const bool second = (P == 2 && p == 1) || (KC == 2 && h == 1);
             pa[h] = (second ? g.a1 : g.a0) + m0 * lda_b;
-            pb[h] = (second ? g.b1 : g.b0) + n0 * ldb_b;
+            pb[h] = (second ? g.b1 : g.b0) + (BNC ? n0 * 2 : n0 * ldb_b);
         }
         na = min(g.M - m0, (int64_t)BM) * lda_b;
-        nb = min(g.N - n0, (int64_t)BN) * ldb_b;
+        // BNC: to the last column of the last K-row; columns past N in other
+        // rows read the next row's values, whose products only reach outputs
+        // that are not stored
+        nb = BNC ? (g.K - 1) * ldb_b + (g.N - n0) * 2 : min(g.N - n0, (int64_t)BN) * ldb_b;
     };
     v4i_rsrc rsA, rsB;
     // descriptors of stage kt of the refill tile, in two parts.  MODE 1
@@ -141,7 +169,10 @@ __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g)
         const int h = KC == 2 ? (kt & 1) : 0;
         const int64_t ko = (int64_t)(KC == 2 ? kt >> 1 : kt) * BKB;
         if (part == 0) rsA = buf_rsrc((h ? pa[KC - 1] : pa[0]) + ko, (uint64_t)(na - ko));
-        else rsB = buf_rsrc((h ? pb[KC - 1] : pb[0]) + ko, (uint64_t)(nb - ko));
+        else if constexpr (BNC) {
+            const int64_t kr = (int64_t)(KC == 2 ? kt >> 1 : kt) * 64 * ldb_b;   // 64 K-rows per stage
+            rsB = buf_rsrc((h ? pb[KC - 1] : pb[0]) + kr, (uint64_t)(nb - kr));
+        } else rsB = buf_rsrc((h ? pb[KC - 1] : pb[0]) + ko, (uint64_t)(nb - ko));
     };
     auto issue_op = [&](int s, int q) __attribute__((always_inline)) {
         const int i = q >> 1;
@@ -152,7 +183,27 @@ __global__ __launch_bounds__(dr::NT, 1) void gemm_dense_ring_kernel(DenseArgs g)
 
     // K-step st: lane half h supplies 16-byte chunk 4h + st of its row (A and
     // B alike, so the sum is unchanged)
+    // BNC fragment reads: lane (group g = lane/16, j = lane % 16) of B tile
+    // jt at K-step st addresses row 8 (4 half + st) + j/4 (+ 4 for the second
+    // read) and columns wn*128 + jt*32 + 16 (g & 1) + 4 (j & 3) .. + 3, i.e.
+    // chunk wn*16 + jt*4 + cx, cx = 2 (g & 1) + (j & 3) / 2, which the row's
+    // swizzle 4 (j/4) moves to wn*16 + (jt ^ j/4)*4 + cx; all but st and the
+    // read is per lane (one offset per jt)
+    const int bj = lane & 15, brs = bj >> 2;
+    const uint32_t bl = (uint32_t)(half * (32 * 512) + brs * 512 + ((2 * ((lane >> 4) & 1) + ((bj & 3) >> 1)) << 4) +
+                                   (bj & 1) * 8 + wn * (TN * 64));
+    uint32_t bjo[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bjo[j] = bl + (uint32_t)(((j ^ brs) & 3) << 6);
     auto read_frag = [&](int s, int st, int q, v4i_d (&fa)[TM], v4i_d (&fb)[TN]) __attribute__((always_inline)) {
+        if constexpr (BNC) {
+            if (q >= TM) {
+                const uint8_t *p = sB[s] + bjo[q - TM] + st * 4096;
+                const v2i_d lo = ds_read_tr16x4(p), hi = ds_read_tr16x4(p + 4 * 512);
+                fb[q - TM] = v4i_d{lo.x, lo.y, hi.x, hi.y};
+                return;
+            }
+        }
         const int c = 4 * half + st;
         const int r = q < TM ? rowA0 + q * 32 : rowB0 + (q - TM) * 32;
         const uint8_t *base = q < TM ? sA[s] : sB[s];
@@ -359,7 +410,11 @@ bool dense_ring_ok(const DenseArgs &g, int dtype) {
 hipError_t launch_gemm_dense_ring(const DenseArgs &g, int dtype, int mode, hipStream_t s) {
     const int tiles = (int)(((g.M + dr::BM - 1) / dr::BM) * ((g.N + dr::BN - 1) / dr::BN)) * (mode == 2 ? 2 : 1);
     const int grid = tiles < num_cus_dr() ? tiles : num_cus_dr();
-#define LSMX_DR(DT, MD) hipLaunchKernelGGL((gemm_dense_ring_kernel<DT, MD>), dim3(grid), dim3(dr::NT), 0, s, g)
+#define LSMX_DR(DT, MD)                                                                                  \
+    do {                                                                                             \
+        if (g.b_nc) hipLaunchKernelGGL((gemm_dense_ring_kernel<DT, MD, true>), dim3(grid), dim3(dr::NT), 0, s, g); \
+        else hipLaunchKernelGGL((gemm_dense_ring_kernel<DT, MD>), dim3(grid), dim3(dr::NT), 0, s, g);  \
+    } while (0)
     if (dtype == LSMX_BF16) {
         if (mode == 0) LSMX_DR(LSMX_BF16, 0);
         else if (mode == 1) LSMX_DR(LSMX_BF16, 1);

@@ -131,6 +131,7 @@ struct DenseArgs {
     int64_t ldc;
     int64_t M, N, K;
     int64_t k_split;         // K per split (== K without split-K)
+    int b_nc;                // 1: b0, b1 are B [K, ldb] N-contiguous (bf16/fp16 ring kernel only)
 };
 
 // The reference's promotion arithmetic for fp32 block scales of any value

@@ -95,6 +95,14 @@ _DENSE = {torch.bfloat16: C.BF16, torch.float16: C.F16, torch.float8_e4m3fn: C.E
 _BK = 64
 
 
+def _ncontig(b: torch.Tensor, N: int) -> bool:
+    """B [K, N] with unit stride along N, N % 8 == 0, 16-byte aligned rows and
+    a row stride the N-contiguous kernel takes (at most 2^22 elements)."""
+    ld = b.stride(0) if b.shape[0] > 1 else N
+    return N % 8 == 0 and (b.stride(1) == 1 or N <= 1) and ld >= N and ld <= (1 << 22) and b.data_ptr() % 16 == 0 and \
+        (ld * b.element_size()) % 16 == 0
+
+
 def _dense(mode, a1, a2, b1, b2, out, splits=1):
     """Launch one dense kernel.  mode 0: out[0] = a1 b1; 1: out[0] = a1 b1 + a2 b2;
     2: out[0] = a1 b1, out[1] = a2 b2.  b* are [K, N]; a2 and b2 share a1's and
@@ -120,6 +128,22 @@ def _dense(mode, a1, a2, b1, b2, out, splits=1):
             o.zero_()
         return
     code = _DENSE[dt]
+    if splits == 1 and dt != torch.float8_e4m3fn and _ncontig(b1, N) and (not mode or (
+            _ncontig(b2, N) and b2.stride(0) == b1.stride(0))):
+        # B as the reference passes it, [K, N] N-contiguous: the kernel reads
+        # it directly (no transpose)
+        a1 = _rows16(a1)
+        a2p = 0
+        if mode:
+            a2 = _rows16(a2)
+            if a2.stride(0) != a1.stride(0) and M > 1:
+                a1, a2 = a1.contiguous(), a2.contiguous()
+            a2p = a2.data_ptr()
+        c1 = out[1].data_ptr() if mode == 2 else 0
+        C.call("lsmx_gemm_dense_nb", a1.data_ptr(), a2p, a1.stride(0) if M > 1 else K, b1.data_ptr(),
+               b2.data_ptr() if mode else 0, b1.stride(0) if K > 1 else N, code, mode, out[0].data_ptr(), c1, N, M,
+               N, K, C.stream_of(out[0]))
+        return
     raw = (lambda t: t.view(torch.uint8)) if dt == torch.float8_e4m3fn else (lambda t: t)
     a1 = _rows16(raw(a1))
     bt1 = kmajor_operand(raw(b1))

@@ -376,3 +376,41 @@ def test_fp8_kmajor_kernel_matches_rowmajor_kernel(dev, mods, M, N, K):
         out.append(c)
     assert not out[1].isnan().any()
     assert torch.equal(out[0], out[1])
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K,pad", [(256, 256, 64, 0), (300, 520, 192, 8), (37, 40, 128, 24), (1, 264, 64, 8),
+                                       (512, 1024, 1024, 0)])
+def test_n_contiguous_b_matches_transposed_b(dev, mods, dt, mode, M, N, K, pad):
+    """lsmx_gemm_dense_nb (B [K, ldb] N-contiguous, transposing LDS reads)
+    gives lsmx_gemm_dense's bits on B's transpose: the same sums in the same
+    order, on random data where the order shows.  Ragged tiles (columns and
+    rows past N and M), padded B rows (ldb > N), every mode; N % 8 != 0 is
+    refused (dual_gemm then transposes B, as before)."""
+    from lockstep_amd import _capi as C
+    g = torch.Generator(device=dev).manual_seed(M + N + K + mode)
+    a = [torch.randn((M, K), device=dev, generator=g).to(dt) for _ in range(2)]
+    b = [torch.randn((K, N + pad), device=dev, generator=g).to(dt)[:, :N] for _ in range(2)]
+    bt = [x.t().contiguous() for x in b]
+    code = C.BF16 if dt == torch.bfloat16 else C.F16
+    outs = []
+    for nb in (False, True):
+        c = [torch.zeros((M, N), device=dev) for _ in range(2)]
+        if nb:
+            args = (a[0].data_ptr(), a[1].data_ptr(), K, b[0].data_ptr(), b[1].data_ptr(), N + pad, code, mode,
+                    c[0].data_ptr(), c[1].data_ptr(), N, M, N, K, C.stream_of(c[0]))
+            C.call("lsmx_gemm_dense_nb", *args)
+        else:
+            C.call("lsmx_gemm_dense", a[0].data_ptr(), a[1].data_ptr(), K, bt[0].data_ptr(), bt[1].data_ptr(), K,
+                   code, mode, c[0].data_ptr(), c[1].data_ptr(), N, M, N, K, 1, C.stream_of(c[0]))
+        outs.append(c)
+    torch.cuda.synchronize(dev)
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
+    if mode == 0 and M == 1:
+        rc = C.load().lsmx_gemm_dense_nb(a[0].data_ptr(), None, K, b[0].data_ptr(), None, N + pad, code, 0,
+                                         outs[1][0].data_ptr(), None, N, M, N - 1, K, C.stream_of(outs[1][0]))
+        assert rc == C.ERR_SHAPE and "multiple of 8" in C.last_error()
+    ref = a[0].double() @ b[0].double() + (a[1].double() @ b[1].double() if mode == 1 else 0)
+    assert (outs[1][0].double() - ref).abs().max() <= 1e-5 * ref.abs().max()
