@@ -343,6 +343,17 @@ int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t
                    int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, int scale_fmt, void *c, int c_dtype,
                    int64_t ldc, int64_t M, int64_t N, int64_t K, void *stream);
 
+/* lsmx_gemm_f8f8 with K-major E8M0 scales and B as the reference passes it:
+ * b [K, ldb] E4M3, N-contiguous (mxfp4_gemm.py:74-87 takes b_fp8 [K, N]), so
+ * no transpose is needed; b_e8m0 is K-major [K/128][ld_sb][4] over B's
+ * columns.  The kernel forms each MFMA operand with transposing LDS reads
+ * (ds_read_b64_tr_b8); same sums in the same order as lsmx_gemm_f8f8 on the
+ * transposed B, so the same bits.  K % 128 == 0, N % 16 == 0; rows 16-byte
+ * aligned. */
+int lsmx_gemm_f8f8_nb(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *b,
+                      int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, void *c, int c_dtype, int64_t ldc, int64_t M,
+                      int64_t N, int64_t K, void *stream);
+
 /* y[cols, ldy] = x[rows, ldx]^T for elements of elem_bytes = 1, 2 or 4 bytes.
  * Lays out the reference's N-contiguous B operands ([K, N], dual_gemm.py:
  * 189-289, mxfp4_gemm.py:29-87) K-contiguous for the kernels above. */

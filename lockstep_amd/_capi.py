@@ -59,6 +59,7 @@ SIGNATURES = {
     "lsmx_gemm_dense": [_vp, _vp, _i64, _vp, _vp, _i64, _int, _int, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp],
     "lsmx_gemm_dense_nb": [_vp, _vp, _i64, _vp, _vp, _i64, _int, _int, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "lsmx_gemm_f8f8": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp],
+    "lsmx_gemm_f8f8_nb": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _vp],
     "lsmx_transpose": [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp],
     "lsmx_scale_to_e8m0": [_vp, _i64, _i64, _i64, _int, _vp, _i64, _vp],
     "lsmx_scale_to_e8m0_batch": [_vp, _int, _vp, _u64, _vp],

@@ -449,6 +449,34 @@ int lsmx_gemm_dense(const void *a0, const void *a1, int64_t lda, const void *bt0
     return launched(lsmx::launch_gemm_dense(g, dtype, mode, (hipStream_t)stream), fn);
 }
 
+int lsmx_gemm_f8f8_nb(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *b,
+                      int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, void *c, int c_dtype, int64_t ldc, int64_t M,
+                      int64_t N, int64_t K, void *stream) {
+    const char *fn = "lsmx_gemm_f8f8_nb";
+    if (!a || !a_e8m0 || !b || !b_e8m0 || !c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
+    if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
+    if (K % 128) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
+    // whole 16-byte pieces of every B row (see lsmx_gemm_dense_nb)
+    if (N % 16) return fail(LSMX_ERR_SHAPE, "%s: N must be a multiple of 16", fn);
+    if (lda < K || ldb < N || ldc < N || ld_sa < M || ld_sb < N)
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (!rows16(a, lda, 1) || !rows16(b, ldb, 1)) return fail(LSMX_ERR_ALIGN, "%s: operand rows must be 16-byte aligned", fn);
+    if (!aligned(a_e8m0, 4) || !aligned(b_e8m0, 4)) return fail(LSMX_ERR_ALIGN, "%s: K-major scales must be 4-byte aligned", fn);
+    if (!aligned(c, c_dtype == LSMX_F32 ? 4 : 2)) return fail(LSMX_ERR_ALIGN, "%s: c misaligned", fn);
+    if (lda > 0x7FFFFFFF / 256 || ldb > 0x7FFFFFFF / 256)
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too large for 32-bit load offsets", fn);
+    if (M > 0x7FFFFFFF || N > 0x7FFFFFFF || ld_sa > 0x7FFFFFFF || ld_sb > 0x7FFFFFFF ||
+        ((M + 255) / 256) * ((N + 255) / 256) > 0x7FFFFFFF)
+        return fail(LSMX_ERR_SHAPE, "%s: M, N and scale leading dimensions must be below 2^31", fn);
+    if (int r = device_guard()) return r;
+    if (M == 0 || N == 0) return LSMX_OK;
+    if (K == 0) return fail(LSMX_ERR_SHAPE, "%s: K == 0", fn);
+    lsmx::DenseArgs g{a, nullptr, lda, b, nullptr, ldb, a_e8m0, b_e8m0, ld_sa, ld_sb, c, nullptr, c_dtype, ldc,
+                      M, N, K, K, 1};
+    return launched(lsmx::launch_gemm_f8f8_kmajor(g, (hipStream_t)stream), fn);
+}
+
 int lsmx_gemm_dense_nb(const void *a0, const void *a1, int64_t lda, const void *b0, const void *b1, int64_t ldb,
                        int dtype, int mode, float *c0, float *c1, int64_t ldc, int64_t M, int64_t N, int64_t K,
                        void *stream) {

@@ -52,7 +52,22 @@ typedef float v16f8 __attribute__((ext_vector_type(16)));
 __device__ v16f8 mfma_scale_f8(v8i a, v8i b, v16f8 c, int cbsz, int blgp, int opsel_a, int scale_a, int opsel_b,
                                int scale_b) __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v8i32.v8i32");
 
-template <int CT>
+// Eight E4M3 values of one column from a [K][N] LDS tile with
+// ds_read_b64_tr_b8: within each 16-lane group, lanes 2m and 2m + 1 give the
+// addresses of 8 consecutive bytes each of row m (16 columns), and lane j
+// receives column j of the group's 8 x 16 block, row m as its byte m (the
+// lane layout was checked on the device with an in-bounds probe).
+typedef int v2i_f8 __attribute__((ext_vector_type(2)));
+LSMX_DEV v2i_f8 ds_read_tr8x8(const uint8_t *p) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i_f8 *)(p));
+}
+
+// BNC: B arrives as the reference passes it, [K, N] E4M3 with N contiguous
+// (row stride ldb bytes).  A stage of B is then 128 K-rows of 256 bytes; a
+// DMA instruction carries 4 rows, LDS chunk p of row r holding source chunk
+// p ^ 2 (r & 7) (the 8 rows a half-wave reads at once cover the 256-byte bank
+// span), and each B fragment is four transposing reads of 8 K values.
+template <int CT, bool BNC = false>
 __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
     using namespace f8;
     __shared__ __attribute__((aligned(16))) uint8_t sA[S][TILE_B];
@@ -77,8 +92,13 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
     // off0 + i*step.  Descriptors end at the operand's last row.
     const int drow0 = wave * RPI + lane / CPR;
     const uint32_t offA0 = (uint32_t)(drow0 * g.lda + (((lane % CPR) ^ swz(drow0)) << 4));
-    const uint32_t offB0 = (uint32_t)(drow0 * g.ldb + (((lane % CPR) ^ swz(drow0)) << 4));
-    const uint32_t stepA = (uint32_t)(NW * RPI * g.lda), stepB = (uint32_t)(NW * RPI * g.ldb);
+    // BNC: load i of this lane reads K-row 4 (i*NW + wave) + lane/16 of the
+    // stage, chunk (lane % 16) ^ 2 (row & 7) (row & 7 does not depend on i)
+    const int brow0 = 4 * wave + (lane >> 4);
+    const uint32_t offB0 = BNC ? (uint32_t)(brow0 * g.ldb + (((lane & 15) ^ (2 * (brow0 & 7))) << 4))
+                               : (uint32_t)(drow0 * g.ldb + (((lane % CPR) ^ swz(drow0)) << 4));
+    const uint32_t stepA = (uint32_t)(NW * RPI * g.lda);
+    const uint32_t stepB = BNC ? (uint32_t)(4 * NW * g.ldb) : (uint32_t)(NW * RPI * g.ldb);
     // scales: every wave loads 64 rows of A's and of B's dwords per stage
     const uint32_t offS = (uint32_t)((wave * 64 + lane) * 4);
     const uint64_t sbytes_a = (uint64_t)(((g.K / 128 - 1) * g.ld_sa + g.M) * 4);
@@ -108,8 +128,17 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
             const uint32_t m0 = (uint32_t)rm0, rows = min(M32 - m0, (uint32_t)BM);
             rsA = buf_rsrc(g.a0 + (uint64_t)m0 * lda32 + ko, rows * lda32 - ko);
         } else if (part == 1) {
-            const uint32_t n0 = (uint32_t)rn0, rows = min(N32 - n0, (uint32_t)BN);
-            rsB = buf_rsrc(g.b0 + (uint64_t)n0 * ldb32 + ko, rows * ldb32 - ko);
+            if constexpr (BNC) {
+                // 128 K-rows per stage; the range ends at the last column of
+                // the last K-row (columns past N in other rows read the next
+                // row's values, whose products reach no stored output)
+                const uint64_t kr = (uint64_t)kt * BKB * (uint64_t)g.ldb;
+                rsB = buf_rsrc(g.b0 + (uint64_t)rn0 + kr, (uint64_t)(g.K - 1) * (uint64_t)g.ldb +
+                                                                (uint64_t)(g.N - rn0) - kr);
+            } else {
+                const uint32_t n0 = (uint32_t)rn0, rows = min(N32 - n0, (uint32_t)BN);
+                rsB = buf_rsrc(g.b0 + (uint64_t)n0 * ldb32 + ko, rows * ldb32 - ko);
+            }
         } else {
             // K-major scale slice kt: rows past the operand read later slices
             // or zeros; their products only reach outputs that are not stored
@@ -134,7 +163,27 @@ __global__ __launch_bounds__(f8::NT, 1) void gemm_f8f8_kernel(DenseArgs g) {
 
     // K-step st: lane half h supplies chunks 4st + h (block 0 part) and
     // 4st + 2 + h (block 1 part) of its row
+    // BNC fragment reads: lane (group g = lane/16, j = lane % 16) of B tile
+    // jt reads rows k0 + j/2 (k0 = 64 st + 16 half + {0, 8, 32, 40}: the
+    // K-contiguous fragment's two 16-byte pieces) and the 8 bytes 8 (j & 1) of
+    // column chunk wn*8 + jt*2 + (g & 1), which the row swizzle 2 (j/2) moves
+    // to 2 ((wn*4 + jt) ^ j/2) + (g & 1); one offset per jt, the rest immediates
+    const int bj8 = lane & 15, brs8 = bj8 >> 1;
+    uint32_t bfo[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+        bfo[j] = (uint32_t)(half * (16 * 256) + brs8 * 256 + ((2 * ((wn * 4 + j) ^ brs8) + ((lane >> 4) & 1)) << 4) +
+                            8 * (bj8 & 1));
     auto read_frag = [&](int s, int st, int q, v8i (&fa)[TM], v8i (&fb)[TN]) __attribute__((always_inline)) {
+        if constexpr (BNC) {
+            if (q >= TM) {
+                const uint8_t *p = sB[s] + bfo[q - TM] + st * (64 * 256);
+                const v2i_f8 r0 = ds_read_tr8x8(p), r1 = ds_read_tr8x8(p + 8 * 256);
+                const v2i_f8 r2 = ds_read_tr8x8(p + 32 * 256), r3 = ds_read_tr8x8(p + 40 * 256);
+                fb[q - TM] = v8i{r0.x, r0.y, r1.x, r1.y, r2.x, r2.y, r3.x, r3.y};
+                return;
+            }
+        }
         const int r = q < TM ? rowA0 + q * 32 : rowB0 + (q - TM) * 32;
         const uint8_t *base = (q < TM ? sA[s] : sB[s]) + r * BKB;
         const u32x4 lo = *reinterpret_cast<const u32x4 *>(base + (((4 * st + half) ^ swz(r)) << 4));
@@ -315,9 +364,15 @@ hipError_t launch_gemm_f8f8_kmajor(const DenseArgs &g, hipStream_t s) {
     const int tiles = (int)(((g.M + f8::BM - 1) / f8::BM) * ((g.N + f8::BN - 1) / f8::BN));
     const int grid = tiles < num_cus_f8() ? tiles : num_cus_f8();
     const dim3 blk(f8::NT);
-    if (g.c_dtype == LSMX_F32) hipLaunchKernelGGL(gemm_f8f8_kernel<LSMX_F32>, dim3(grid), blk, 0, s, g);
-    else if (g.c_dtype == LSMX_BF16) hipLaunchKernelGGL(gemm_f8f8_kernel<LSMX_BF16>, dim3(grid), blk, 0, s, g);
-    else hipLaunchKernelGGL(gemm_f8f8_kernel<LSMX_F16>, dim3(grid), blk, 0, s, g);
+#define LSMX_F8(CT)                                                                                   \
+    do {                                                                                          \
+        if (g.b_nc) hipLaunchKernelGGL((gemm_f8f8_kernel<CT, true>), dim3(grid), blk, 0, s, g);    \
+        else hipLaunchKernelGGL((gemm_f8f8_kernel<CT, false>), dim3(grid), blk, 0, s, g);          \
+    } while (0)
+    if (g.c_dtype == LSMX_F32) LSMX_F8(LSMX_F32);
+    else if (g.c_dtype == LSMX_BF16) LSMX_F8(LSMX_BF16);
+    else LSMX_F8(LSMX_F16);
+#undef LSMX_F8
     return hipGetLastError();
 }
 

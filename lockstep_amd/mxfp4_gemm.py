@@ -353,8 +353,10 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
     fp32 accumulation (reference: mxfp4_gemm.py:29-87).  fp32 scales that are
     not all powers of two are flagged by their conversion and C is then
     recomputed with the reference's promotion (lsmx_gemm_mx_promote,
-    mxfp4_gemm.py:52-63).  B is transposed to K-contiguous rows on the device
-    first unless b_fp8 is a transposed view of such rows."""
+    mxfp4_gemm.py:52-63).  An N-contiguous B (N % 16 == 0) is read in place
+    (lsmx_gemm_f8f8_nb) unless that promotion may run; otherwise B is
+    transposed to K-contiguous rows on the device first unless b_fp8 is a
+    transposed view of such rows."""
     M, K = a_fp8.shape
     K2, N = b_fp8.shape
     assert K == K2 and K % 128 == 0, "K must be a multiple of 128 (max BLOCK_K)"
@@ -369,7 +371,7 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
     if K == 0:
         return c.zero_()
     a = _rows16(a_fp8.view(torch.uint8))
-    bt = kmajor_operand(b_fp8.view(torch.uint8))
+    b8 = b_fp8.view(torch.uint8)
     # fp32 scales (the reference's form) or E8M0 bytes, either way as K-major
     # E8M0 for the persistent 256 x 256-tile kernel (csrc/gemm_f8f8.hip)
     promote = None
@@ -383,7 +385,18 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
                                                      flagged=not exact)
         promote = None if exact else (sa32, False, sb32, True, flag, epoch)
     fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
-    lda, ldb = a.stride(0) if M > 1 else K, bt.stride(0) if N > 1 else K
+    lda = a.stride(0) if M > 1 else K
+    ldn = b8.stride(0) if K > 1 else N
+    if promote is None and N % 16 == 0 and b8.stride(1) == 1 and N <= ldn <= 0x7FFFFFFF // 256 and \
+            ldn % 16 == 0 and b8.data_ptr() % 16 == 0:
+        # B as the reference passes it, [K, N] N-contiguous: the kernel reads
+        # it directly (no transpose; the promotion kernel, which needs K-
+        # contiguous rows, is not launched on this path)
+        C.call("lsmx_gemm_f8f8_nb", a.data_ptr(), lda, sa.data_ptr(), lsa, b8.data_ptr(), ldn, sb.data_ptr(), lsb,
+               c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
+        return c
+    bt = kmajor_operand(b8)
+    ldb = bt.stride(0) if N > 1 else K
     C.call("lsmx_gemm_f8f8", a.data_ptr(), lda, sa.data_ptr(), lsa, bt.data_ptr(), ldb, sb.data_ptr(), lsb, fmt,
            c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
     if promote is not None:

@@ -414,3 +414,41 @@ def test_n_contiguous_b_matches_transposed_b(dev, mods, dt, mode, M, N, K, pad):
         assert rc == C.ERR_SHAPE and "multiple of 8" in C.last_error()
     ref = a[0].double() @ b[0].double() + (a[1].double() @ b[1].double() if mode == 1 else 0)
     assert (outs[1][0].double() - ref).abs().max() <= 1e-5 * ref.abs().max()
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K,pad", [(256, 256, 128, 0), (300, 528, 384, 16), (37, 48, 256, 32), (1, 272, 128, 0),
+                                       (512, 1024, 2048, 0)])
+def test_fp8_n_contiguous_b_matches_transposed_b(dev, mods, M, N, K, pad, out_dtype):
+    """lsmx_gemm_f8f8_nb (E4M3 B [K, ldb] N-contiguous, transposing LDS reads)
+    gives lsmx_gemm_f8f8's bits on B's transpose, with K-major E8M0 scales of
+    random exponents; ragged tiles and padded rows; N % 16 != 0 is refused
+    (mxfp4_gemm_fp8 then transposes B, as before)."""
+    from lockstep_amd import _capi as C
+    from lockstep_amd import fp4
+    _, mg = mods[0], mods[1]
+    g = torch.Generator(device=dev).manual_seed(M * 3 + N + K)
+    a = fp4.codes_to_e4m3(torch.randint(0, 16, (M, K), device=dev, generator=g).to(torch.uint8)).view(torch.uint8)
+    b = fp4.codes_to_e4m3(torch.randint(0, 16, (K, N + pad), device=dev, generator=g).to(torch.uint8)).view(
+        torch.uint8)[:, :N]
+    bt = b.t().contiguous()
+    sa = torch.randint(120, 134, (K // 128, M, 4), device=dev, generator=g).to(torch.uint8)
+    sb = torch.randint(120, 134, (K // 128, N, 4), device=dev, generator=g).to(torch.uint8)
+    code = {torch.float32: C.F32, torch.bfloat16: C.BF16}[out_dtype]
+    c0 = torch.empty((M, N), device=dev, dtype=out_dtype)
+    c1 = torch.empty_like(c0)
+    C.call("lsmx_gemm_f8f8", a.data_ptr(), K, sa.data_ptr(), M, bt.data_ptr(), K, sb.data_ptr(), N,
+           C.SCALE_E8M0_KMAJOR, c0.data_ptr(), code, N, M, N, K, C.stream_of(c0))
+    C.call("lsmx_gemm_f8f8_nb", a.data_ptr(), K, sa.data_ptr(), M, b.data_ptr(), N + pad, sb.data_ptr(), N,
+           c1.data_ptr(), code, N, M, N, K, C.stream_of(c1))
+    torch.cuda.synchronize(dev)
+    assert torch.equal(c0, c1)
+    # the Python wrapper takes the in-place path for E8M0 scales and gives the same bits
+    b_s = sb.permute(0, 2, 1).reshape(K // 32, N)          # [K/32, N] row-major E8M0 of the same scales
+    a_s = sa.permute(1, 0, 2).reshape(M, K // 32)
+    got = mg.mxfp4_gemm_fp8(a.view(torch.float8_e4m3fn), b.view(torch.float8_e4m3fn), a_s, b_s, out_dtype=out_dtype)
+    assert torch.equal(got, c1)
+    if M == 1:
+        rc = C.load().lsmx_gemm_f8f8_nb(a.data_ptr(), K, sa.data_ptr(), M, b.data_ptr(), N + pad, sb.data_ptr(), N,
+                                        c1.data_ptr(), code, N, M, N - 8, K, C.stream_of(c1))
+        assert rc == C.ERR_SHAPE and "multiple of 16" in C.last_error()
