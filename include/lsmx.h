@@ -348,8 +348,10 @@ int lsmx_gemm_f8f8(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t
  * no transpose is needed; b_e8m0 is K-major [K/128][ld_sb][4] over B's
  * columns.  The kernel forms each MFMA operand with transposing LDS reads
  * (ds_read_b64_tr_b8); same sums in the same order as lsmx_gemm_f8f8 on the
- * transposed B, so the same bits.  K % 128 == 0, N % 16 == 0; rows 16-byte
- * aligned. */
+ * transposed B, so the same bits.  K % 128 == 0, N % 16 == 0; ldb >= N;
+ * lda, ldb <= (2^31 - 1) / 256; rows 16-byte aligned.  fp32 scales that may
+ * not be powers of two: follow with lsmx_gemm_mx_promote on the same b
+ * (op_fmt LSMX_E4M3 | LSMX_B_NCONTIG). */
 int lsmx_gemm_f8f8_nb(const uint8_t *a, int64_t lda, const uint8_t *a_e8m0, int64_t ld_sa, const uint8_t *b,
                       int64_t ldb, const uint8_t *b_e8m0, int64_t ld_sb, void *c, int c_dtype, int64_t ldc, int64_t M,
                       int64_t N, int64_t K, void *stream);
@@ -412,7 +414,11 @@ int lsmx_scale_to_e8m0_batch(const lsmx_e8m0_item *items, int n, uint64_t *flag,
  * on its E8M0 bytes, then this on the same C, and a call whose scales are all
  * powers of two costs one early-exit launch while the others get every
  * output recomputed by this kernel.  Vector-ALU bound (2 fp32 operations per
- * output per 32-block): a fallback, not a fast path. */
+ * output per 32-block): a fallback, not a fast path.
+ * op_fmt LSMX_E4M3 | LSMX_B_NCONTIG: bt is instead the reference's b_fp8
+ * itself, [K, ldb] E4M3 with N contiguous (N % 16 == 0, ldb >= N; the
+ * lsmx_gemm_f8f8_nb form), read with transposing LDS loads: same bits. */
+#define LSMX_B_NCONTIG 0x10
 int lsmx_gemm_mx_promote(const uint8_t *a, int64_t lda, const float *a_scale, int64_t sa_row, int64_t sa_blk,
                          const uint8_t *bt, int64_t ldb, const float *b_scale, int64_t sb_row, int64_t sb_blk,
                          int op_fmt, void *c, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K,

@@ -22,6 +22,7 @@ ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_DEVICE, ERR_LAUNCH, ERR_ARG = -1, -2, -3, -
 F32, BF16, F16, E4M3 = 0, 1, 2, 3
 E8M0_IN_T, E8M0_OUT_KMAJOR = 1, 2
 CODES_PACKED, CODES_UNPACKED = 0, 1
+B_NCONTIG = 0x10  # lsmx_gemm_mx_promote op_fmt bit: B [K, ldb] N-contiguous E4M3
 SCALE_E8M0, SCALE_F32, SCALE_E8M0_KMAJOR = 0, 1, 2
 
 _i64 = ctypes.c_int64

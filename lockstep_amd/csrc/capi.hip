@@ -607,13 +607,18 @@ int lsmx_gemm_mx_promote(const uint8_t *a, int64_t lda, const float *a_scale, in
                          const uint64_t *flag, uint64_t epoch, void *stream) {
     const char *fn = "lsmx_gemm_mx_promote";
     if (!a || !a_scale || !bt || !b_scale || !c) return fail(LSMX_ERR_ARG, "%s: null pointer", fn);
+    const int b_nc = (op_fmt & LSMX_B_NCONTIG) ? 1 : 0;
+    op_fmt &= ~LSMX_B_NCONTIG;
     if (op_fmt != LSMX_CODES_PACKED && op_fmt != LSMX_E4M3)
         return fail(LSMX_ERR_DTYPE, "%s: op_fmt must be LSMX_CODES_PACKED or LSMX_E4M3", fn);
+    if (b_nc && op_fmt != LSMX_E4M3) return fail(LSMX_ERR_DTYPE, "%s: LSMX_B_NCONTIG needs LSMX_E4M3", fn);
+    if (b_nc && N % 16) return fail(LSMX_ERR_SHAPE, "%s: N must be a multiple of 16 for N-contiguous B", fn);
     if (c_dtype != LSMX_F32 && c_dtype != LSMX_BF16 && c_dtype != LSMX_F16) return fail(LSMX_ERR_DTYPE, "%s: c_dtype", fn);
     if (M < 0 || N < 0 || K < 0) return fail(LSMX_ERR_SHAPE, "%s: negative size", fn);
     if (K % 128) return fail(LSMX_ERR_SHAPE, "K must be a multiple of 128 (max BLOCK_K)");
     const int64_t kbytes = op_fmt == LSMX_CODES_PACKED ? K / 2 : K;
-    if (lda < kbytes || ldb < kbytes || ldc < N) return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
+    if (lda < kbytes || ldb < (b_nc ? N : kbytes) || ldc < N)
+        return fail(LSMX_ERR_SHAPE, "%s: leading dimension too small", fn);
     if (sa_row < 0 || sa_blk < 0 || sb_row < 0 || sb_blk < 0) return fail(LSMX_ERR_SHAPE, "%s: negative scale stride", fn);
     if (!aligned(a, 16) || !aligned(bt, 16) || lda % 16 || ldb % 16)
         return fail(LSMX_ERR_ALIGN, "%s: operand rows must be 16-byte aligned", fn);
@@ -622,7 +627,7 @@ int lsmx_gemm_mx_promote(const uint8_t *a, int64_t lda, const float *a_scale, in
     // the kernel forms every load offset in 32 bits, over rows up to a
     // tile past M or N and blocks up to a chunk past K
     const int64_t lim = (int64_t)1 << 31, nkb = K / 32;
-    if (128 * lda + kbytes + 256 >= lim || 128 * ldb + kbytes + 256 >= lim)
+    if (128 * lda + kbytes + 256 >= lim || (b_nc ? 256 * ldb + 256 : 128 * ldb + kbytes + 256) >= lim)
         return fail(LSMX_ERR_SHAPE, "%s: operand rows of %lld / %lld bytes are too long", fn, (long long)lda,
                     (long long)ldb);
     if (M + 128 > lim / 4 || N + 128 > lim / 4 || 4 * ((M + 128) * sa_row + (nkb + 8) * sa_blk) >= lim ||
@@ -633,7 +638,7 @@ int lsmx_gemm_mx_promote(const uint8_t *a, int64_t lda, const float *a_scale, in
     const int sa_bytes = nkb ? (int)(4 * ((M - 1) * sa_row + (nkb - 1) * sa_blk + 1)) : 0;
     const int sb_bytes = nkb ? (int)(4 * ((N - 1) * sb_row + (nkb - 1) * sb_blk + 1)) : 0;
     lsmx::PromoteArgs g{a, lda, bt, ldb, a_scale, sa_row, sa_blk, b_scale, sb_row, sb_blk, sa_bytes, sb_bytes,
-                        c, c_dtype, ldc, M, N, K, flag, epoch};
+                        c, c_dtype, ldc, M, N, K, flag, epoch, b_nc};
     return launched(lsmx::launch_gemm_promote(g, op_fmt == LSMX_CODES_PACKED, (hipStream_t)stream), fn);
 }
 

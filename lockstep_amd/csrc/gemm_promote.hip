@@ -27,6 +27,14 @@
 // compares *flag with the caller's epoch and returns when they differ, so a
 // launch that follows the fast GEMM costs one load when all scales were
 // powers of two (the scale conversion writes the epoch when one is not).
+//
+// BNC (E4M3 only): B arrives as the reference passes b_fp8, [K, N] with N
+// contiguous (row stride ldb bytes).  A chunk of B is then 256 K-rows of the
+// tile's 128 columns in LDS (row stride RSN), and each MFMA operand (8 K
+// positions of one column per lane) comes from one transposing LDS read
+// (ds_read_b64_tr_b8): in each 16-lane group, lanes 2m and 2m + 1 address the
+// two 8-byte halves of K-row m and lane j receives column j.  Same products,
+// same order, same bits as on the transposed B.
 #include "lsmx_store.h"
 #include "lsmx_internal.h"
 
@@ -45,7 +53,15 @@ struct PmOp {
     static constexpr int RS = 32 * pm::KC + 16;           // LDS row stride (E4M3 bytes): rows 4 banks apart
     static constexpr int PPR = CB / 16;                    // 16-byte pieces per row
     static constexpr int PT = pm::BM * PPR / pm::NT;       // pieces per thread per operand
+    static constexpr int RSN = pm::BN + 16;                // BNC: LDS stride of a K-row of B
 };
+
+typedef int v2i_pm __attribute__((ext_vector_type(2)));
+
+LSMX_DEV uint64_t ds_read_tr8(const uint8_t *p) {
+    return __builtin_bit_cast(
+        uint64_t, __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i_pm *)(p)));
+}
 
 // 8 packed FP4 codes (code j in bits 4j .. 4j+3) -> 8 E4M3 bytes, the even
 // codes first (x: codes 0, 2, 4, 6; y: 1, 3, 5, 7): the magnitude by a byte
@@ -59,12 +75,13 @@ LSMX_DEV u32x2 fp4x8_to_e4m3x8_eo(uint32_t p) {
     return u32x2{me | ((ev << 4) & 0x80808080u), mo | ((od << 4) & 0x80808080u)};
 }
 
-template <bool F4, int CT>
+template <bool F4, int CT, bool BNC = false>
 __global__ __launch_bounds__(pm::NT, 2) void gemm_promote_kernel(PromoteArgs g) {
     using O = PmOp<F4>;
+    static_assert(!(BNC && F4), "N-contiguous B is an E4M3 form");
     if (g.flag && *g.flag != g.epoch) return;
     __shared__ __align__(16) uint8_t la[pm::BM * O::RS];
-    __shared__ __align__(16) uint8_t lb[pm::BN * O::RS];
+    __shared__ __align__(16) uint8_t lb[BNC ? pm::KC * 32 * O::RSN : pm::BN * O::RS];
     __shared__ __align__(16) float lsa[pm::KC][pm::BM];
     __shared__ __align__(16) float lsb[pm::KC][pm::BN];
 
@@ -100,9 +117,24 @@ __global__ __launch_bounds__(pm::NT, 2) void gemm_promote_kernel(PromoteArgs g) 
         auto load = [&](int ch) {
             const int oa = ar0 * lda + ac0 + ch * O::CB, ob = ar0 * ldb + ac0 + ch * O::CB;
 #pragma unroll
-            for (int i = 0; i < O::PT; ++i) {
-                ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra_, oa + 16 * i, 0, 0);
-                rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb_, ob + 16 * i, 0, 0);
+            for (int i = 0; i < O::PT; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra_, oa + 16 * i, 0, 0);
+            if constexpr (BNC) {
+                // K-rows ch * 256 + t / 8 + 32 i, bytes 16 (t % 8) .. of the
+                // tile's columns, through a descriptor based at the chunk's
+                // first row that ends after column N - 1 of row K - 1: rows
+                // past K read zeros (their blocks are not used), columns past
+                // N (N % 16 == 0) land in LDS columns no output reads
+                const int64_t k0 = (int64_t)ch * (pm::KC * 32);
+                const __amdgpu_buffer_rsrc_t rbc = __builtin_amdgcn_make_buffer_rsrc(
+                    (void *)(g.b + k0 * g.ldb + n0), 0,
+                    (int)min((g.K - 1 - k0) * g.ldb + (g.N - n0), (int64_t)0x7FFFFFFF), 0x00020000);
+                const int ob_n = (t >> 3) * ldb + (t & 7) * 16;
+#pragma unroll
+                for (int i = 0; i < O::PT; ++i)
+                    rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rbc, ob_n, i * 32 * ldb, 0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < O::PT; ++i) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb_, ob + 16 * i, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -131,7 +163,10 @@ __global__ __launch_bounds__(pm::NT, 2) void gemm_promote_kernel(PromoteArgs g) 
                     *reinterpret_cast<u32x4 *>(lb + o + 16) = u32x4{b2.x, b2.y, b3.x, b3.y};
                 } else {
                     *reinterpret_cast<u32x4 *>(la + ar0 * O::RS + ac0 + 16 * i) = ra[i];
-                    *reinterpret_cast<u32x4 *>(lb + ar0 * O::RS + ac0 + 16 * i) = rb[i];
+                    if constexpr (BNC)
+                        *reinterpret_cast<u32x4 *>(lb + ((t >> 3) + 32 * i) * O::RSN + (t & 7) * 16) = rb[i];
+                    else
+                        *reinterpret_cast<u32x4 *>(lb + ar0 * O::RS + ac0 + 16 * i) = rb[i];
                 }
             }
 #pragma unroll
@@ -160,7 +195,11 @@ __global__ __launch_bounds__(pm::NT, 2) void gemm_promote_kernel(PromoteArgs g) 
                 for (int x = 0; x < 4; ++x) {
                     const int ar = wm * 64 + x * 16 + r16, br = wn * 64 + x * 16 + r16;
                     af[x] = *reinterpret_cast<const uint64_t *>(la + ar * O::RS + j * 32 + g4 * 8);
-                    bf[x] = *reinterpret_cast<const uint64_t *>(lb + br * O::RS + j * 32 + g4 * 8);
+                    if constexpr (BNC)
+                        bf[x] = ds_read_tr8(lb + (j * 32 + g4 * 8 + (r16 >> 1)) * O::RSN + wn * 64 + x * 16 +
+                                            8 * (r16 & 1));
+                    else
+                        bf[x] = *reinterpret_cast<const uint64_t *>(lb + br * O::RS + j * 32 + g4 * 8);
                 }
                 f32x4 sa4[4];
                 float sb1[4];
@@ -226,7 +265,12 @@ hipError_t launch_gemm_promote(const PromoteArgs &g, bool fp4, hipStream_t s) {
     const int64_t tiles = ((g.M + pm::BM - 1) / pm::BM) * ((g.N + pm::BN - 1) / pm::BN);
     const dim3 grid((unsigned)min(tiles, (int64_t)1024)), blk(pm::NT);
 #define LSMX_PM(F, CT) hipLaunchKernelGGL((gemm_promote_kernel<F, CT>), grid, blk, 0, s, g)
-    if (fp4) {
+#define LSMX_PMN(CT) hipLaunchKernelGGL((gemm_promote_kernel<false, CT, true>), grid, blk, 0, s, g)
+    if (g.b_nc) {
+        if (g.c_dtype == LSMX_F32) LSMX_PMN(LSMX_F32);
+        else if (g.c_dtype == LSMX_BF16) LSMX_PMN(LSMX_BF16);
+        else LSMX_PMN(LSMX_F16);
+    } else if (fp4) {
         if (g.c_dtype == LSMX_F32) LSMX_PM(true, LSMX_F32);
         else if (g.c_dtype == LSMX_BF16) LSMX_PM(true, LSMX_BF16);
         else LSMX_PM(true, LSMX_F16);
@@ -236,6 +280,7 @@ hipError_t launch_gemm_promote(const PromoteArgs &g, bool fp4, hipStream_t s) {
         else LSMX_PM(false, LSMX_F16);
     }
 #undef LSMX_PM
+#undef LSMX_PMN
     return hipGetLastError();
 }
 

@@ -154,6 +154,7 @@ struct PromoteArgs {
     int64_t M, N, K;
     const uint64_t *flag;
     uint64_t epoch;
+    int b_nc;  // 1: b is B [K, ldb] N-contiguous E4M3 (else Bt [N, ldb])
 };
 
 // Up to kE8Batch fp32 scale tensors converted to K-major E8M0 in one launch;

@@ -354,7 +354,7 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
     not all powers of two are flagged by their conversion and C is then
     recomputed with the reference's promotion (lsmx_gemm_mx_promote,
     mxfp4_gemm.py:52-63).  An N-contiguous B (N % 16 == 0) is read in place
-    (lsmx_gemm_f8f8_nb) unless that promotion may run; otherwise B is
+    by both kernels (lsmx_gemm_f8f8_nb, LSMX_B_NCONTIG); otherwise B is
     transposed to K-contiguous rows on the device first unless b_fp8 is a
     transposed view of such rows."""
     M, K = a_fp8.shape
@@ -387,13 +387,14 @@ def mxfp4_gemm_fp8(a_fp8, b_fp8, a_scale, b_scale, out_dtype=torch.bfloat16):
     fmt, lsa, lsb = C.SCALE_E8M0_KMAJOR, M, N
     lda = a.stride(0) if M > 1 else K
     ldn = b8.stride(0) if K > 1 else N
-    if promote is None and N % 16 == 0 and b8.stride(1) == 1 and N <= ldn <= 0x7FFFFFFF // 256 and \
-            ldn % 16 == 0 and b8.data_ptr() % 16 == 0:
-        # B as the reference passes it, [K, N] N-contiguous: the kernel reads
-        # it directly (no transpose; the promotion kernel, which needs K-
-        # contiguous rows, is not launched on this path)
+    if N % 16 == 0 and b8.stride(1) == 1 and N <= ldn < 0x7FFFFFFF // 256 and ldn % 16 == 0 and \
+            b8.data_ptr() % 16 == 0:
+        # B as the reference passes it, [K, N] N-contiguous: both kernels
+        # read it in place with transposing LDS loads (no transpose)
         C.call("lsmx_gemm_f8f8_nb", a.data_ptr(), lda, sa.data_ptr(), lsa, b8.data_ptr(), ldn, sb.data_ptr(), lsb,
                c.data_ptr(), _out_code(out_dtype), N, M, N, K, C.stream_of(c))
+        if promote is not None:
+            _promote(a, lda, b8, ldn, C.E4M3 | C.B_NCONTIG, c, K, *promote)
         return c
     bt = kmajor_operand(b8)
     ldb = bt.stride(0) if N > 1 else K

@@ -154,10 +154,11 @@ def _e4m3(fp4, dev, codes):
     return fp4.codes_to_e4m3(torch.from_numpy(codes).to(dev))
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (200, 300, 384), (1, 64, 128)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (200, 300, 384), (1, 64, 128), (130, 528, 1152), (300, 48, 384)])
 def test_fp8_any_scales_match_the_promotion_oracle(dev, mods, oracle, M, N, K):
     """mxfp4_gemm_fp8 with E4M3 operands holding E2M1 values and fp32 scales
-    in (-2, 2); b_scale is the reference's [K/32, N]."""
+    in (-2, 2); b_scale is the reference's [K/32, N].  N % 16 == 0 reads the
+    N-contiguous B in place in both kernels; N = 300 transposes it first."""
     C, fp4, mg = mods
     rng = np.random.default_rng(M + 3 * N + K)
     ca, cb = _codes(rng, M, K), _codes(rng, K, N)
@@ -194,6 +195,43 @@ def test_fp8_off_grid_operands_within_the_summation_bound(dev, mods, oracle):
     mag = oracle.gemm_promote(np.abs(A), np.abs(B), np.abs(san), np.abs(sbn), sb_transposed=True).astype(np.float64)
     err = float((np.abs(got - want) / mag).max())
     assert err <= 2.0 ** -12, err
+
+
+@pytest.mark.parametrize("M,N,K,pad", [(256, 256, 256, 0), (130, 400, 1152, 16), (1, 16, 128, 48), (300, 144, 384, 0)])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_capi_promotion_reads_n_contiguous_b(dev, mods, oracle, M, N, K, pad, out):
+    """lsmx_gemm_mx_promote with op_fmt LSMX_E4M3 | LSMX_B_NCONTIG on B
+    [K, N + pad] gives the bits of the same call on B's K-contiguous
+    transpose, and the oracle's; N % 16 != 0 and packed operands with the
+    bit are refused."""
+    C, fp4, mg = mods
+    rng = np.random.default_rng(M + N + K + pad)
+    ca, cb = _codes(rng, M, K), _codes(rng, K, N + pad)
+    sa = rng.uniform(-2, 2, (M, K // 32)).astype(np.float32)
+    sb = rng.uniform(-2, 2, (K // 32, N)).astype(np.float32)
+    a, b = _e4m3(fp4, dev, ca).view(torch.uint8), _e4m3(fp4, dev, cb).view(torch.uint8)
+    bt = b[:, :N].t().contiguous()
+    tsa, tsb = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
+    code = C.F32 if out == torch.float32 else C.BF16
+    c0, c1 = torch.empty((M, N), device=dev, dtype=out), torch.empty((M, N), device=dev, dtype=out)
+    C.call("lsmx_gemm_mx_promote", a.data_ptr(), K, tsa.data_ptr(), K // 32, 1, bt.data_ptr(), K, tsb.data_ptr(), 1,
+           N, C.E4M3, c0.data_ptr(), code, N, M, N, K, None, 0, C.stream_of(c0))
+    C.call("lsmx_gemm_mx_promote", a.data_ptr(), K, tsa.data_ptr(), K // 32, 1, b.data_ptr(), N + pad,
+           tsb.data_ptr(), 1, N, C.E4M3 | C.B_NCONTIG, c1.data_ptr(), code, N, M, N, K, None, 0, C.stream_of(c1))
+    torch.cuda.synchronize(dev)
+    assert torch.equal(c0, c1)
+    _same(c1, oracle.gemm_promote(oracle.E2M1_VALUES[ca], np.ascontiguousarray(oracle.E2M1_VALUES[cb][:, :N].T),
+                                  sa, sb, sb_transposed=True))
+    if M == 1:
+        lib = C.load()
+        rc = lib.lsmx_gemm_mx_promote(a.data_ptr(), K, tsa.data_ptr(), K // 32, 1, b.data_ptr(), N + pad,
+                                      tsb.data_ptr(), 1, N, C.E4M3 | C.B_NCONTIG, c1.data_ptr(), code, N, M, N - 8,
+                                      K, None, 0, C.stream_of(c1))
+        assert rc == C.ERR_SHAPE and "multiple of 16" in C.last_error()
+        rc = lib.lsmx_gemm_mx_promote(a.data_ptr(), K, tsa.data_ptr(), K // 32, 1, b.data_ptr(), N + pad,
+                                      tsb.data_ptr(), 1, N, C.CODES_PACKED | C.B_NCONTIG, c1.data_ptr(), code, N, M,
+                                      N, K, None, 0, C.stream_of(c1))
+        assert rc == C.ERR_DTYPE
 
 
 def test_capi_flag_gates_the_promotion_launch(dev, mods, oracle):
