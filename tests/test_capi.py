@@ -37,6 +37,7 @@ def test_header_constants_match_binding():
     assert consts["LSMX_ERR_DTYPE"] == C.ERR_DTYPE and consts["LSMX_ERR_DEVICE"] == C.ERR_DEVICE
     assert consts["LSMX_F32"] == C.F32 and consts["LSMX_BF16"] == C.BF16 and consts["LSMX_F16"] == C.F16
     assert consts["LSMX_CODES_PACKED"] == C.CODES_PACKED and consts["LSMX_SCALE_F32"] == C.SCALE_F32
+    assert int(re.search(r"#define LSMX_B_NCONTIG (0x[0-9a-fA-F]+)", src).group(1), 16) == C.B_NCONTIG
 
 
 def test_version_string():
@@ -151,6 +152,31 @@ def test_promotion_entry_points_validate_before_launch():
     assert pm(sa_r=1 << 24) == C.ERR_SHAPE and "2^31" in C.last_error()
     assert _rc("lsmx_gemm_mx_promote", None, 128, FAKE, 8, 1, FAKE, 128, FAKE, 8, 1, C.CODES_PACKED, FAKE, C.F32,
                64, 64, 64, 256, None, 0, None) == C.ERR_ARG
+    # N-contiguous B (LSMX_B_NCONTIG): E4M3 only, N % 16 == 0, ldb >= N, 256 rows of ldb within 2^31
+
+    def pmn(op=C.E4M3 | C.B_NCONTIG, N=64, ldb=64, K=256):
+        return _rc("lsmx_gemm_mx_promote", FAKE, K, FAKE, 8, 1, FAKE, ldb, FAKE, 1, N, op, FAKE, C.F32, N, 64, N, K,
+                   None, 0, None)
+    assert pmn(op=C.CODES_PACKED | C.B_NCONTIG) == C.ERR_DTYPE and "LSMX_E4M3" in C.last_error()
+    assert pmn(N=40, ldb=48) == C.ERR_SHAPE and "multiple of 16" in C.last_error()
+    assert pmn(ldb=48) == C.ERR_SHAPE and "too small" in C.last_error()
+    assert pmn(ldb=1 << 23) == C.ERR_SHAPE and "too long" in C.last_error()
+
+
+def test_n_contiguous_e4m3_gemm_validates_before_launch():
+    """lsmx_gemm_f8f8_nb: K % 128, N % 16, ldb >= N, K-major scale strides
+    >= rows, 16-byte rows and leading dimensions below 2^31 / 256."""
+    def nb(K=128, N=64, ldb=64, lda=128, ld_sa=8, ld_sb=64, c_dtype=C.BF16, b=FAKE):
+        return _rc("lsmx_gemm_f8f8_nb", FAKE, lda, FAKE, ld_sa, b, ldb, FAKE, ld_sb, FAKE, c_dtype, N, 8, N, K, None)
+    assert nb(K=192) == C.ERR_SHAPE and "multiple of 128" in C.last_error()
+    assert nb(N=40, ldb=48, ld_sb=40) == C.ERR_SHAPE and "multiple of 16" in C.last_error()
+    assert nb(ldb=48) == C.ERR_SHAPE and "too small" in C.last_error()
+    assert nb(ld_sa=4) == C.ERR_SHAPE and nb(ld_sb=32) == C.ERR_SHAPE
+    assert nb(c_dtype=C.E4M3) == C.ERR_DTYPE
+    assert nb(b=ctypes.c_void_p(0x1008)) == C.ERR_ALIGN
+    assert nb(ldb=1 << 23) == C.ERR_SHAPE and "too large" in C.last_error()
+    assert _rc("lsmx_gemm_f8f8_nb", None, 128, FAKE, 8, FAKE, 64, FAKE, 64, FAKE, C.BF16, 64, 8, 64, 128,
+               None) == C.ERR_ARG
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="a GPU is present")
