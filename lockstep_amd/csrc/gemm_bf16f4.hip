@@ -1951,17 +1951,20 @@ int64_t gemm_bf16f4_workspace(int64_t M, int64_t N, int64_t K, bool dual) {
 }
 
 // C[b][m][n] = sum over slices s = 0, 1, ... of partial[s][b][m][n], in that
-// order: 4 consecutive columns per thread, one 16-byte load per slice.
+// order: 4 consecutive columns per thread, one 16-byte load per slice.  A
+// workgroup covers 1024 columns of one output row: workgroup x is row
+// x / cb (cb workgroups per row), so the row and batch come from scalar
+// 32-bit divisions of uniform values and the loads issue at once (64-bit
+// per-thread divisions put ~1 us of index arithmetic in front of them).
 template <int CT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws, int splits, int nb,
                                                             int64_t Mp, int64_t Np, void *c0, void *c1, int64_t ldc,
                                                             int64_t M, int64_t N) {
-    const int64_t q4 = Np / 4;  // column quads per row
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t b = i / (M * q4), rem = i - b * (M * q4);
-    if (b >= nb) return;
-    const int64_t m = rem / q4, n = (rem - m * q4) * 4;
-    if (n >= N) return;
+    const uint32_t cb = (uint32_t)((Np / 4 + 255) / 256);   // workgroups per output row
+    const uint32_t row = blockIdx.x / cb, b = row / (uint32_t)M;
+    const int64_t m = row - b * (uint32_t)M;
+    const int64_t n = ((int64_t)(blockIdx.x - row * cb) * 256 + threadIdx.x) * 4;
+    if ((int)b >= nb || n >= N) return;
     const float *p = ws + (b * Mp + m) * Np + n;
     const int64_t slice = (int64_t)nb * Mp * Np;
     u32x4 v = *reinterpret_cast<const u32x4 *>(p);
@@ -2001,8 +2004,7 @@ static hipError_t launch_ring_splitk(GemmArgs g, int splits, hipStream_t s) {
     g.k_split = g.K / splits;
     const dim3 grid((unsigned)(tiles * splits)), blk(wr::NT);
     const int64_t Mp = (g.M + 127) / 128 * 128, Np = (g.N + BN - 1) / BN * BN;
-    const int64_t threads = NB * g.M * (Np / 4);
-    const dim3 rgrid((unsigned)((threads + 255) / 256)), rblk(256);
+    const dim3 rgrid((unsigned)(NB * g.M * ((Np / 4 + 255) / 256))), rblk(256);
 #define LSMX_RS(CT)                                                                                              \
     do {                                                                                                         \
         hipLaunchKernelGGL((gemm_bf16f4_ring_kernel<NB, CT, BR, BN, SL, true, WGM>), grid, blk, 0, s, g);        \
